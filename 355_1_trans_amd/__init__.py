@@ -1,0 +1,262 @@
+"""MI355X (gfx950) quantized-GEMM hot path: host-side mirror of the reference.
+
+The compute lives in ``libqgemm.so`` (hand-written HIP for gfx950, C ABI in
+``include/qgemm.h``).  This module loads that library with ctypes and exposes
+PyTorch-facing wrappers that validate tensors, build the 96-byte kargs block
+and launch on the current stream:
+
+* ``blockscale_bpreshuffle.gemm_a8w8_blockscale_bpreshuffle`` -- the
+  reference's E8M0 block-scale adapter (SNAP blockscale_bpreshuffle.py:37-97);
+* ``gemm_a8w8_bpreshuffle`` -- block-scale FP8 with fp32 1x128 / 128x128
+  scales and a K-panel pre-shuffled B (BPS host.cc:66-111, 254-284);
+* ``gemm_a8w8_mxfp8`` -- MXFP8 TN GEMM (MX8 host.cc:96-122, 266-296);
+* ``gemm_a4w4_mxfp4`` -- MXFP4 A4W4 GEMM (MX4 host.cc:96-115, 201-216).
+
+There is no CPU fallback: every wrapper raises if the library is missing or
+the tensors are not on a GPU.
+"""
+import ctypes
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libqgemm.so"
+
+OUT_FP32 = 0
+OUT_BF16 = 1
+
+
+class Kargs(ctypes.Structure):
+    """opus_gemm_scale_kargs: 96 bytes, field order of the reference ABI."""
+
+    _fields_ = (
+        [(name, ctypes.c_void_p) for name in ("ptr_a", "ptr_b", "ptr_c")]
+        + [(name, ctypes.c_int) for name in (
+            "m", "n", "k", "batch", "stride_a", "stride_b", "stride_c",
+            "stride_a_batch", "stride_b_batch", "stride_c_batch")]
+        + [(name, ctypes.c_void_p) for name in ("ptr_sfa", "ptr_sfb")]
+        + [(name, ctypes.c_int) for name in (
+            "stride_sfa", "stride_sfb", "stride_sfa_batch", "stride_sfb_batch")]
+    )
+
+
+class LdsBypassKargs(ctypes.Structure):
+    """opus_gemm_ldsbypass_kargs: ptr_b_pp after ptr_b, stride_b_pp_batch appended."""
+
+    _fields_ = (
+        [(name, ctypes.c_void_p) for name in ("ptr_a", "ptr_b", "ptr_b_pp", "ptr_c")]
+        + [(name, ctypes.c_int) for name in (
+            "m", "n", "k", "batch", "stride_a", "stride_b", "stride_c",
+            "stride_a_batch", "stride_b_batch", "stride_c_batch")]
+        + [(name, ctypes.c_void_p) for name in ("ptr_sfa", "ptr_sfb")]
+        + [(name, ctypes.c_int) for name in (
+            "stride_sfa", "stride_sfb", "stride_sfa_batch", "stride_sfb_batch", "stride_b_pp_batch")]
+    )
+
+
+assert ctypes.sizeof(Kargs) == 96
+
+
+EXPORTS = {
+    # name: (restype, argtypes)
+    "launch_blockscale_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "gemm_a8w8_blockscale_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p,
+                                                        ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a8w8_blockscale_bpreshuffle_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "gemm_a8w8_mxfp8": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_void_p]),
+    "gemm_a8w8_mxfp8_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "gemm_a4w4_mxfp4": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_void_p]),
+    "gemm_a4w4_mxfp4_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "qgemm_shuffle_b_kpanel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
+    "qgemm_shuffle_weight_16x16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
+    "qgemm_e8m0_shuffle_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "qgemm_e8m0_shuffle": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
+    "qgemm_probe_words": (ctypes.c_int, []),
+    "qgemm_probe_mfma_layout": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "qgemm_version": (ctypes.c_char_p, []),
+}
+
+
+@lru_cache(None)
+def lib():
+    """Load libqgemm.so; raises if it has not been built (no fallback)."""
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                           "(the HIP library is the only implementation)")
+    L = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in EXPORTS.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
+def _check(status, what):
+    if status:
+        raise RuntimeError(f"{what} failed: HIP error {status}")
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device)
+
+
+def _record(stream, *tensors):
+    for t in tensors:
+        if t is not None:
+            t.record_stream(stream)
+
+
+def _require_gpu(*tensors):
+    dev = tensors[0].device
+    if not tensors[0].is_cuda:
+        raise ValueError("inputs must be GPU tensors (there is no CPU implementation)")
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError("all tensors must be on the same GPU")
+    return dev
+
+
+def _u8(t):
+    return t.view(torch.uint8) if t.dtype != torch.uint8 else t
+
+
+def _out(out, shape, dtype, device):
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or out.device != device or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the requested shape/dtype/device")
+    return out
+
+
+def _out_code(dtype):
+    if dtype == torch.bfloat16:
+        return OUT_BF16
+    if dtype == torch.float32:
+        return OUT_FP32
+    raise ValueError("output dtype must be torch.bfloat16 or torch.float32")
+
+
+def gemm_a8w8_mxfp8(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None):
+    """MXFP8 TN GEMM: A [M,K] e4m3, B [N,K] e4m3, A_scale [M,K/32], B_scale [N,K/32] E8M0 bytes."""
+    dev = _require_gpu(A, B, A_scale, B_scale)
+    m, k = A.shape
+    n = B.shape[0]
+    if B.shape[1] != k or k % 128:
+        raise ValueError("requires matching K with K % 128 == 0")
+    if A_scale.shape != (m, k // 32) or B_scale.shape != (n, k // 32):
+        raise ValueError("requires A_scale [M,K/32] and B_scale [N,K/32]")
+    for t in (A, B, A_scale, B_scale):
+        if not t.is_contiguous():
+            raise ValueError("A, B and scales must be contiguous")
+    out = _out(out, (m, n), dtype, dev)
+    args = Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, k, k, n, m * k, n * k, m * n,
+                 A_scale.data_ptr(), B_scale.data_ptr(), k // 32, k // 32, m * (k // 32), n * (k // 32))
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        st = lib().gemm_a8w8_mxfp8(ctypes.byref(args), _out_code(dtype), None, 0, ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B, A_scale, B_scale, out)
+    _check(st, "gemm_a8w8_mxfp8")
+    return out
+
+
+def gemm_a4w4_mxfp4(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None, workspace=None):
+    """MXFP4 A4W4 GEMM: A [M,K/2], B [N,K/2] packed e2m1 bytes, scales [rows,K/32] E8M0."""
+    dev = _require_gpu(A, B, A_scale, B_scale)
+    m, kb = A.shape
+    n = B.shape[0]
+    k = 2 * kb
+    if B.shape[1] != kb or k % 256:
+        raise ValueError("requires matching K with K % 256 == 0")
+    if A_scale.shape != (m, k // 32) or B_scale.shape != (n, k // 32):
+        raise ValueError("requires A_scale [M,K/32] and B_scale [N,K/32]")
+    for t in (A, B, A_scale, B_scale):
+        if not t.is_contiguous():
+            raise ValueError("A, B and scales must be contiguous")
+    out = _out(out, (m, n), dtype, dev)
+    args = Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
+                 A_scale.data_ptr(), B_scale.data_ptr(), k // 32, k // 32, m * (k // 32), n * (k // 32))
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        st = lib().gemm_a4w4_mxfp4(ctypes.byref(args), _out_code(dtype), ws_ptr, ws_bytes,
+                                   ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B, A_scale, B_scale, out, workspace)
+    _check(st, "gemm_a4w4_mxfp4")
+    return out
+
+
+def gemm_a8w8_bpreshuffle(A, B_kpanel, A_scale, B_scale, dtype=torch.bfloat16, out=None, workspace=None):
+    """Block-scale FP8 with fp32 scales.
+
+    A [M,K] e4m3; B_kpanel [K/128, N, 128] e4m3 (shuffle_b_kpanel of B [N,K]);
+    A_scale fp32 [M,K/128] (row-major, BASELINE) or a [M,K/128] view with
+    strides (1, M) (the reference's column-major [K/128][M]); B_scale fp32
+    [ceil(N/128), K/128]."""
+    dev = _require_gpu(A, B_kpanel, A_scale, B_scale)
+    m, k = A.shape
+    if B_kpanel.dim() != 3 or B_kpanel.shape[0] * 128 != k or B_kpanel.shape[2] != 128:
+        raise ValueError("B_kpanel must be [K/128, N, 128]")
+    n = B_kpanel.shape[1]
+    kg = k // 128
+    if k % 128 or A_scale.shape != (m, kg) or B_scale.shape != ((n + 127) // 128, kg):
+        raise ValueError("requires K % 128 == 0, A_scale [M,K/128], B_scale [ceil(N/128),K/128]")
+    if A_scale.dtype != torch.float32 or B_scale.dtype != torch.float32:
+        raise ValueError("block scales must be fp32")
+    if not (A.is_contiguous() and B_kpanel.is_contiguous() and B_scale.is_contiguous()):
+        raise ValueError("A, B_kpanel and B_scale must be contiguous")
+    if A_scale.is_contiguous():
+        stride_sfa = 1 if m > 1 else m
+    elif A_scale.stride() == (1, m):
+        stride_sfa = m
+    else:
+        raise ValueError("A_scale must be row-major [M,K/128] or column-major with strides (1,M)")
+    out = _out(out, (m, n), dtype, dev)
+    args = Kargs(A.data_ptr(), B_kpanel.data_ptr(), out.data_ptr(), m, n, k, 1, k, 128, n, m * k, n * k, m * n,
+                 A_scale.data_ptr(), B_scale.data_ptr(), stride_sfa, kg, m * kg, B_scale.shape[0] * kg)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        st = lib().gemm_a8w8_blockscale_bpreshuffle(ctypes.byref(args), _out_code(dtype), ws_ptr, ws_bytes,
+                                                    ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B_kpanel, A_scale, B_scale, out, workspace)
+    _check(st, "gemm_a8w8_blockscale_bpreshuffle")
+    return out
+
+
+def probe_mfma_layout(device=None):
+    """Run the layout probes; returns the int32 word tensor (see csrc/probe.hip)."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    words = lib().qgemm_probe_words()
+    out = torch.zeros(words, dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        s = _stream(device)
+        st = lib().qgemm_probe_mfma_layout(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(s.cuda_stream))
+    _check(st, "qgemm_probe_mfma_layout")
+    torch.cuda.synchronize(device)
+    return out.cpu()
+
+
+# ------------------------------------------------------------------ layouts
+def shuffle_b_kpanel(B):
+    """K-panel pre-shuffle (BPS host.cc:92-111): [N, K] -> [K/128, N, 128]."""
+    n, k = B.shape
+    if k % 128:
+        raise ValueError("K must be a multiple of 128")
+    return B.reshape(n, k // 128, 128).permute(1, 0, 2).contiguous()
+
+
+def shuffle_weight_16x16(B):
+    """shuffle_weight(layout=(16,16)) over bytes: [N, Kb] -> [N/16, Kb/16, 16, 16] (SNAP host.cc:161-179)."""
+    n, kb = B.shape
+    if n % 16 or kb % 16:
+        raise ValueError("N and K bytes must be multiples of 16")
+    return B.reshape(n // 16, 16, kb // 16, 16).permute(0, 2, 1, 3).contiguous().reshape(n, kb)
+
+
+from . import blockscale_bpreshuffle  # noqa: E402  (reference adapter mirror)

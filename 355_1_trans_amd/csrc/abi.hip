@@ -1,0 +1,326 @@
+// C ABI of libqgemm.so: argument validation, dispatch, layout helpers.
+//
+// Host C++ only; every entry point launches asynchronously on the caller's
+// stream, allocates nothing and returns a hipError_t (contract of the
+// reference launcher, SNAP gemm_a8w8_blockscale_bpreshuffle_launch.cc:29-65).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <climits>
+#include <cstdint>
+#include <cstring>
+
+#include "launch.hpp"
+#include "qgemm.h"
+
+static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
+static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "reference kargs ABI");
+static_assert(__builtin_offsetof(opus_gemm_scale_kargs, stride_sfa) == 80, "reference kargs ABI");
+static_assert(__builtin_offsetof(opus_gemm_ldsbypass_kargs, ptr_c) == 24, "ldsbypass kargs ABI");
+
+namespace {
+
+using qg::TileArgs;
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_arch_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 other
+
+// Current device must be gfx950 (SNAP launch.cc:55-61).
+hipError_t check_arch() {
+    int dev = 0;
+    hipError_t st = hipGetDevice(&dev);
+    if (st != hipSuccess) return st;
+    if (dev >= 0 && dev < kMaxDevices) {
+        const int known = g_arch_ok[dev].load(std::memory_order_relaxed);
+        if (known == 1) return hipSuccess;
+        if (known == 2) return hipErrorInvalidDeviceFunction;
+    }
+    hipDeviceProp_t props{};
+    st = hipGetDeviceProperties(&props, dev);
+    if (st != hipSuccess) return st;
+    const bool ok = std::strncmp(props.gcnArchName, "gfx950", 6) == 0;
+    if (dev >= 0 && dev < kMaxDevices) g_arch_ok[dev].store(ok ? 1 : 2, std::memory_order_relaxed);
+    return ok ? hipSuccess : hipErrorInvalidDeviceFunction;
+}
+
+// rows*cols*batch*bytes fits in int32 (the kernels use signed 32-bit
+// offsets within one batch; SNAP launch.cc:10-15).
+bool bounded_count(long long rows, long long cols, long long batch, long long bytes) {
+    if (rows <= 0 || cols <= 0 || batch <= 0) return false;
+    const long long limit = INT_MAX / bytes;
+    if (rows > limit / cols) return false;
+    return batch <= limit / (rows * cols);
+}
+
+bool overlaps(const void* a, uint64_t a_bytes, const void* b, uint64_t b_bytes) {
+    const auto ba = reinterpret_cast<uintptr_t>(a);
+    const auto bb = reinterpret_cast<uintptr_t>(b);
+    return ba < bb + b_bytes && bb < ba + a_bytes;
+}
+
+// Bytes spanned by a strided batch of `rows` rows of `pitch` elements.
+uint64_t span(long long batch, long long batch_stride, long long rows, long long pitch, long long last_row_len,
+              long long elem) {
+    if (rows <= 0) return 0;
+    return (uint64_t)(((batch - 1) * batch_stride + (rows - 1) * pitch + last_row_len) * elem);
+}
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+void fill_common(TileArgs& t, const opus_gemm_scale_kargs& a, int kbytes) {
+    t.a = static_cast<const uint8_t*>(a.ptr_a);
+    t.b = static_cast<const uint8_t*>(a.ptr_b);
+    t.c = a.ptr_c;
+    t.sfa = static_cast<const uint8_t*>(a.ptr_sfa);
+    t.sfb = static_cast<const uint8_t*>(a.ptr_sfb);
+    t.m = a.m;
+    t.n = a.n;
+    t.kbytes = kbytes;
+    t.lda = a.stride_a;
+    t.ldb = a.stride_b;
+    t.ldc = a.stride_c;
+    t.a_batch = a.stride_a_batch;
+    t.b_batch = a.stride_b_batch;
+    t.c_batch = a.stride_c_batch;
+    t.sfa_batch = a.stride_sfa_batch;
+    t.sfb_batch = a.stride_sfb_batch;
+    t.tiles_m = ceil_div(a.m, 256);
+    t.tiles_n = ceil_div(a.n, 256);
+    t.group_m = 4;
+    t.unit_scale = 127;
+}
+
+bool flag01(int v) { return v == 0 || v == 1; }
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// The kernels move A/B rows with 16-byte DMAs and scales with 4-byte DMAs.
+bool dma_aligned(const opus_gemm_scale_kargs& a, bool scales_dword) {
+    if (!aligned(a.ptr_a, 16) || !aligned(a.ptr_b, 16) || a.stride_a % 16 || a.stride_a_batch % 16 ||
+        a.stride_b_batch % 16)
+        return false;
+    if (scales_dword && (!aligned(a.ptr_sfa, 4) || !aligned(a.ptr_sfb, 4)))
+        return false;
+    return true;
+}
+
+// Validation shared by the MX entry points: dense or padded row-major A/B,
+// row-major scales, C [M, N] with stride_c >= N.
+hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kbytes_per_row, int k_align) {
+    if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
+        !flag01(out_dtype))
+        return hipErrorInvalidValue;
+    const auto& a = *args;
+    const int kg = a.k / 32;
+    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % k_align) return hipErrorInvalidValue;
+    if (a.stride_a < kbytes_per_row || a.stride_b < kbytes_per_row || a.stride_c < a.n || a.stride_sfa < kg ||
+        a.stride_sfb < kg)
+        return hipErrorInvalidValue;
+    if (!dma_aligned(a, true) || a.stride_b % 16 || a.stride_sfa % 4 || a.stride_sfb % 4 ||
+        a.stride_sfa_batch % 4 || a.stride_sfb_batch % 4)
+        return hipErrorInvalidValue;
+    const long long outb = out_dtype ? 2 : 4;
+    if (a.batch > 1 &&
+        ((long long)a.stride_a_batch < (long long)a.m * a.stride_a ||
+         (long long)a.stride_b_batch < (long long)a.n * a.stride_b ||
+         (long long)a.stride_c_batch < (long long)a.m * a.stride_c ||
+         (long long)a.stride_sfa_batch < (long long)a.m * a.stride_sfa ||
+         (long long)a.stride_sfb_batch < (long long)a.n * a.stride_sfb))
+        return hipErrorInvalidValue;
+    if (!bounded_count(a.m, a.stride_a, 1, 1) || !bounded_count(a.n, a.stride_b, 1, 1) ||
+        !bounded_count(a.m, a.stride_c, 1, outb) || !bounded_count(a.m, a.stride_sfa, 1, 1) ||
+        !bounded_count(a.n, a.stride_sfb, 1, 1))
+        return hipErrorInvalidValue;
+    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb);
+    if (overlaps(a.ptr_c, cb, a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, kbytes_per_row, 1)) ||
+        overlaps(a.ptr_c, cb, a.ptr_b, span(a.batch, a.stride_b_batch, a.n, a.stride_b, kbytes_per_row, 1)) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfa, span(a.batch, a.stride_sfa_batch, a.m, a.stride_sfa, kg, 1)) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfb, span(a.batch, a.stride_sfb_batch, a.n, a.stride_sfb, kg, 1)))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------- MXFP8
+hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    hipError_t st = validate_mx(args, out_dtype, args ? args->k : 0, 128);
+    if (st != hipSuccess) return st;
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    TileArgs t{};
+    fill_common(t, *args, args->k);
+    t.sfa_sm = args->stride_sfa;
+    t.sfb_sn = args->stride_sfb;
+    return qg::launch_tile_mx8_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, stream);
+}
+
+size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
+    (void)args;
+    return 0;
+}
+
+// ---------------------------------------------------------------- MXFP4
+hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256);
+    if (st != hipSuccess) return st;
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    TileArgs t{};
+    fill_common(t, *args, args->k / 2);
+    t.sfa_sm = args->stride_sfa;
+    t.sfb_sn = args->stride_sfb;
+    return qg::launch_tile_mx4_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, stream);
+}
+
+size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
+    (void)args;
+    return 0;
+}
+
+// ------------------------------------------------ block-scale FP8, E8M0 scales
+// Same checks, in the same order, as SNAP gemm_a8w8_blockscale_bpreshuffle_launch.cc:31-65.
+hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int output_bf16, int tiles,
+                                         hipStream_t stream) {
+    if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
+        !flag01(output_bf16) || !flag01(tiles))
+        return hipErrorInvalidValue;
+    const auto& a = *args;
+    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.m % 256 || a.n % 256 || a.k % 128 ||
+        !bounded_count(a.m, a.k, a.batch, 1) || !bounded_count(a.n, a.k, a.batch, 1) ||
+        !bounded_count(a.m, a.n, a.batch, output_bf16 ? 2 : 4) || !bounded_count(a.m, a.k / 128, a.batch, 1) ||
+        !bounded_count(a.n / 128, a.k / 128, a.batch, 1))
+        return hipErrorInvalidValue;
+    if (a.stride_a != a.k || a.stride_b != a.k || a.stride_c != a.n || a.stride_a_batch != a.m * a.k ||
+        a.stride_b_batch != a.n * a.k || a.stride_c_batch != a.m * a.n || a.stride_sfa != a.m ||
+        a.stride_sfb != a.k / 128 || a.stride_sfa_batch != a.m * (a.k / 128) ||
+        a.stride_sfb_batch != (a.n / 128) * (a.k / 128))
+        return hipErrorInvalidValue;
+    const uint64_t c_bytes = uint64_t(a.m) * a.n * a.batch * (output_bf16 ? 2 : 4);
+    if (overlaps(a.ptr_c, c_bytes, a.ptr_a, uint64_t(a.stride_a_batch) * a.batch) ||
+        overlaps(a.ptr_c, c_bytes, a.ptr_b, uint64_t(a.stride_b_batch) * a.batch) ||
+        overlaps(a.ptr_c, c_bytes, a.ptr_sfa, uint64_t(a.stride_sfa_batch) * a.batch) ||
+        overlaps(a.ptr_c, c_bytes, a.ptr_sfb, uint64_t(a.stride_sfb_batch) * a.batch))
+        return hipErrorInvalidValue;
+    if (!dma_aligned(a, false)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    TileArgs t{};
+    fill_common(t, a, a.k);
+    t.sfa_sk = a.stride_sfa;
+    t.sfb_sn = a.stride_sfb;
+    return qg::launch_tile_bs8_w16(t, a.batch, output_bf16 == 1, stream);
+}
+
+// ------------------------------------------------ block-scale FP8, fp32 scales
+hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
+                                            size_t workspace_bytes, hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
+        !flag01(out_dtype))
+        return hipErrorInvalidValue;
+    const auto& a = *args;
+    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % 128) return hipErrorInvalidValue;
+    const int kg = a.k / 128, nbk = ceil_div(a.n, 128);
+    // B is K-panel [K/128][N][128] (stride_b = 128); SFA column-major
+    // [K/128][M] (stride_sfa >= M) or row-major [M][K/128] (stride_sfa == 1).
+    const bool sfa_rowmajor = (a.stride_sfa == 1 && a.m > 1);
+    if (a.stride_a < a.k || a.stride_b != 128 || a.stride_c < a.n || a.stride_sfb < kg ||
+        (!sfa_rowmajor && a.stride_sfa < a.m))
+        return hipErrorInvalidValue;
+    if (!dma_aligned(a, true)) return hipErrorInvalidValue;
+    const long long outb = out_dtype ? 2 : 4;
+    const long long sfa_elems = (long long)a.m * kg;
+    const long long sfa_span = sfa_rowmajor ? sfa_elems : (long long)(kg - 1) * a.stride_sfa + a.m;
+    if (a.batch > 1 &&
+        ((long long)a.stride_a_batch < (long long)a.m * a.stride_a ||
+         (long long)a.stride_b_batch < (long long)a.n * a.k ||
+         (long long)a.stride_c_batch < (long long)a.m * a.stride_c ||
+         (long long)a.stride_sfa_batch < sfa_span || (long long)a.stride_sfb_batch < (long long)nbk * a.stride_sfb))
+        return hipErrorInvalidValue;
+    if (!bounded_count(a.m, a.stride_a, 1, 1) || !bounded_count(a.n, a.k, 1, 1) ||
+        !bounded_count(a.m, a.stride_c, 1, outb) || !bounded_count(sfa_span, 1, 1, 4) ||
+        !bounded_count(nbk, a.stride_sfb, 1, 4))
+        return hipErrorInvalidValue;
+    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb);
+    if (overlaps(a.ptr_c, cb, a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, a.k, 1)) ||
+        overlaps(a.ptr_c, cb, a.ptr_b, span(a.batch, a.stride_b_batch, 1, 0, (long long)a.n * a.k, 1)) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfa, span(a.batch, a.stride_sfa_batch, 1, 0, sfa_span, 4)) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfb, span(a.batch, a.stride_sfb_batch, nbk, a.stride_sfb, kg, 4)))
+        return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    TileArgs t{};
+    fill_common(t, a, a.k);
+    t.sfa_sm = sfa_rowmajor ? kg : 1;
+    t.sfa_sk = sfa_rowmajor ? 1 : a.stride_sfa;
+    t.sfb_sn = a.stride_sfb;
+    return qg::launch_tile_bsf32_kpanel(t, a.batch, out_dtype == QGEMM_OUT_BF16, stream);
+}
+
+size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {
+    (void)args;
+    return 0;
+}
+
+// ---------------------------------------------------------------- layouts
+int qgemm_shuffle_b_kpanel(const uint8_t* src, uint8_t* dst, int n, int k_bytes) {
+    if (!src || !dst || n <= 0 || k_bytes <= 0 || k_bytes % 128) return (int)hipErrorInvalidValue;
+    const int nkt = k_bytes / 128;
+    for (int r = 0; r < n; ++r)
+        for (int kt = 0; kt < nkt; ++kt)
+            std::memcpy(dst + ((size_t)kt * n + r) * 128, src + (size_t)r * k_bytes + (size_t)kt * 128, 128);
+    return 0;
+}
+
+int qgemm_shuffle_weight_16x16(const uint8_t* src, uint8_t* dst, int n, int k_bytes) {
+    if (!src || !dst || n <= 0 || k_bytes <= 0 || n % 16 || k_bytes % 16) return (int)hipErrorInvalidValue;
+    const int kb = k_bytes / 16;
+    for (int b = 0; b < n / 16; ++b)
+        for (int c = 0; c < kb; ++c)
+            for (int ni = 0; ni < 16; ++ni)
+                std::memcpy(dst + ((size_t)b * kb + c) * 256 + (size_t)ni * 16,
+                            src + (size_t)(b * 16 + ni) * k_bytes + (size_t)c * 16, 16);
+    return 0;
+}
+
+size_t qgemm_e8m0_shuffle_bytes(int rows, int groups_k) {
+    if (rows <= 0 || groups_k <= 0) return 0;
+    return (size_t)((rows + 31) / 32 * 32) * (size_t)((groups_k + 7) / 8 * 8);
+}
+
+int qgemm_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int groups_k) {
+    if (!src || !dst || rows <= 0 || groups_k <= 0) return (int)hipErrorInvalidValue;
+    const int kg8 = (groups_k + 7) / 8 * 8;
+    std::memset(dst, 0x7F, qgemm_e8m0_shuffle_bytes(rows, groups_k));
+    for (int r = 0; r < rows; ++r)
+        for (int g = 0; g < groups_k; ++g) {
+            const size_t o = ((size_t)(r / 32) * (kg8 / 8) + g / 8) * 256 + (size_t)(g % 4) * 64 +
+                             (size_t)(r % 16) * 4 + (size_t)((g % 8) / 4) * 2 + (size_t)((r % 32) / 16);
+            dst[o] = src[(size_t)r * groups_k + g];
+        }
+    return 0;
+}
+
+// ---------------------------------------------------------------- probe
+int qgemm_probe_words(void) { return qg::kProbeWords; }
+
+hipError_t qgemm_probe_mfma_layout(int32_t* dev_out, hipStream_t stream) {
+    if (!dev_out) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_probe(dev_out, stream);
+}
+
+const char* qgemm_version(void) { return "qgemm gfx950 1"; }
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// Instantiations and launchers of the LDS-staged tile kernel.
+#include "launch.hpp"
+
+namespace qg {
+
+namespace {
+template <int FMT, ScaleKind SK, BLay BL>
+hipError_t launch_tile(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
+    const dim3 grid(a.tiles_m * a.tiles_n, 1, batch);
+    const dim3 block(tile_threads<SK>());
+    if (bf16) tile_gemm_kernel<FMT, SK, BL, true><<<grid, block, 0, s>>>(a);
+    else tile_gemm_kernel<FMT, SK, BL, false><<<grid, block, 0, s>>>(a);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_tile_mx8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_tile<kFmtFp8, ScaleKind::MX, BLay::RAW>(a, batch, bf16, s);
+}
+hipError_t launch_tile_mx4_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_tile<kFmtFp4, ScaleKind::MX, BLay::RAW>(a, batch, bf16, s);
+}
+hipError_t launch_tile_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_tile<kFmtFp8, ScaleKind::BS8, BLay::W16>(a, batch, bf16, s);
+}
+hipError_t launch_tile_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_tile<kFmtFp8, ScaleKind::BSF32, BLay::KPANEL>(a, batch, bf16, s);
+}
+
+}  // namespace qg

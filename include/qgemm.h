@@ -1,0 +1,197 @@
+/*
+ * qgemm.h -- C ABI of the MI355X (gfx950) quantized-GEMM library
+ * (355_1_trans_amd/libqgemm.so).
+ *
+ * Every entry point is extern "C", takes plain pointers and sizes, launches
+ * asynchronously on the given HIP stream and returns a hipError_t code:
+ *   0  (hipSuccess)                     launched;
+ *   1  (hipErrorInvalidValue)           null pointer, bad flag, bad shape or
+ *                                       stride, int32 overflow, output
+ *                                       overlapping an input, or a workspace
+ *                                       that is too small;
+ *   98 (hipErrorInvalidDeviceFunction)  current device is not gfx950;
+ *   otherwise the launch status from hipGetLastError().
+ * No entry point allocates device memory or preprocesses inputs; the caller
+ * owns every buffer (reference contract:
+ * trace_block_scale_latest_20260914_040021/source_snapshot/
+ * gemm_a8w8_blockscale_bpreshuffle_launch.cc:29-30).
+ *
+ * Reference paths below are relative to /root/reference/:
+ *   BPS  = block_scale_gemm_bpreshuffle/
+ *   LBP  = block_scale_gemm_ldsbypass/
+ *   MX8  = mxfp8_gemm/
+ *   MX4  = mxfp4_gemm_4wave_20261112/
+ *   SNAP = trace_block_scale_latest_20260914_040021/source_snapshot/
+ */
+#ifndef QGEMM_H
+#define QGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * 96-byte kernel-argument block shared by every family. Field order and
+ * size are the reference ABI (SNAP/gemm_a8w8_mxfp8_scale_common.h:12-38,
+ * BPS/gemm_a8w8_blockscale_bpreshuffle_common.h:4-25,
+ * MX8/gemm_a8w8_mxfp8_common.h:4-25, MX4/gemm_a4w4_mxfp4_4wave_traits.hpp:7-27).
+ * Strides are in elements for FP8 operands and in bytes for packed FP4
+ * operands; scale strides are in scale elements.
+ */
+typedef struct opus_gemm_scale_kargs {
+    const void* ptr_a;
+    const void* ptr_b;
+    void* ptr_c;
+    int m;
+    int n;
+    int k;
+    int batch;
+    int stride_a;
+    int stride_b;
+    int stride_c;
+    int stride_a_batch;
+    int stride_b_batch;
+    int stride_c_batch;
+    const void* ptr_sfa;
+    const void* ptr_sfb;
+    int stride_sfa;
+    int stride_sfb;
+    int stride_sfa_batch;
+    int stride_sfb_batch;
+} opus_gemm_scale_kargs;
+
+/* The fp32-scale block-scale drivers name the same 96-byte block
+ * opus_gemm_kargs (BPS/gemm_a8w8_blockscale_bpreshuffle_common.h:4-25). */
+typedef opus_gemm_scale_kargs opus_gemm_kargs;
+
+/* LDS-bypass variant: ptr_b_pp (B'' fragment order) follows ptr_b and
+ * stride_b_pp_batch is appended (LBP/gemm_a8w8_blockscale_ldsbypass_common.h:4-27). */
+typedef struct opus_gemm_ldsbypass_kargs {
+    const void* ptr_a;
+    const void* ptr_b;
+    const void* ptr_b_pp;
+    void* ptr_c;
+    int m;
+    int n;
+    int k;
+    int batch;
+    int stride_a;
+    int stride_b;
+    int stride_c;
+    int stride_a_batch;
+    int stride_b_batch;
+    int stride_c_batch;
+    const void* ptr_sfa;
+    const void* ptr_sfb;
+    int stride_sfa;
+    int stride_sfb;
+    int stride_sfa_batch;
+    int stride_sfb_batch;
+    int stride_b_pp_batch;
+} opus_gemm_ldsbypass_kargs;
+
+/* Output dtype codes (the reference's output_bf16 flag: 1 = bf16, 0 = fp32). */
+#define QGEMM_OUT_FP32 0
+#define QGEMM_OUT_BF16 1
+
+/* ------------------------------------------------------------------ */
+/* Block-scale FP8, E8M0 scales: the reference's existing C ABI.        */
+/* ------------------------------------------------------------------ */
+/* Replaces SNAP/gemm_a8w8_blockscale_bpreshuffle_launch.cc:31-65 with the
+ * identical signature and contract: A e4m3 [batch,M,K]; B e4m3 in
+ * shuffle_weight(16,16) layout; SFA E8M0 bytes column-major [K/128,M]
+ * (stride_sfa = M); SFB E8M0 [N/128,K/128]; C bf16 or fp32 [M,N].
+ * M and N multiples of 256, K a multiple of 128, dense strides; `tiles`
+ * must be 0 (auto) or 1. */
+hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int output_bf16, int tiles,
+                                  hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Block-scale FP8, fp32 scales (1x128 activation, 128x128 weight).     */
+/* ------------------------------------------------------------------ */
+/* Replaces the launch in BPS/gemm_a8w8_blockscale_bpreshuffle_host.cc:275-284
+ * (kernel declared :14-15). A e4m3 [batch,M,K] (stride_a >= K); B e4m3 in
+ * K-panel layout [K/128][N][128] (stride_b = 128, BPS host.cc:92-111,263);
+ * SFB fp32 [ceil(N/128)][K/128] (stride_sfb = K/128). SFA fp32 is either
+ * the reference's column-major [K/128][M] (stride_sfa = M, BPS host.cc:270)
+ * or BASELINE's row-major [M][K/128] (stride_sfa = 1). C bf16/fp32 [M,N].
+ * Any M >= 1, N >= 1 (tails are masked), K a multiple of 128.
+ * `workspace` (fp32 split-K partials) may be NULL; then no split-K is used. */
+hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args);
+
+/* Replaces LBP/gemm_a8w8_blockscale_ldsbypass_host.cc:283-294 (main + repack
+ * launches). Same math as the bpreshuffle entry; B'' = ptr_b_pp holds B in
+ * this library's per-lane fragment order (qgemm_pack_b_ldsbypass), read
+ * straight from global memory into registers. ptr_b may be NULL. */
+hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args, int out_dtype, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args);
+/* GPU repack B' (K-panel, ptr_b) -> B'' (ptr_b_pp); the reference's
+ * gemm_a8w8_blockscale_ldsbypass_repack_kernel (LBP host.cc:289-294). */
+hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs* args, hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* MXFP8: e4m3 x e4m3 with one E8M0 scale per 32 K elements.            */
+/* ------------------------------------------------------------------ */
+/* Replaces the launch in MX8/gemm_a8w8_mxfp8_host.cc:287-296 (kernel
+ * MX8/gemm_a8w8_mxfp8_kernel_template.hpp:300-432). TN layout: A [M,K],
+ * B [N,K] K-contiguous; SFA [M,K/32], SFB [N,K/32] uint8 row-major
+ * (stride_sfa/stride_sfb = row pitch, MX8 host.cc:282-285). C bf16/fp32.
+ * Any M, N >= 1, K a multiple of 128. */
+hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
+
+/* ------------------------------------------------------------------ */
+/* MXFP4 A4W4: packed e2m1 x e2m1, E8M0 per 32 K elements.             */
+/* ------------------------------------------------------------------ */
+/* Replaces the launch in MX4/gemm_a4w4_mxfp4_4wave_host.cc:201-216. A [M,K/2],
+ * B [N,K/2] bytes (even k in the low nibble), strides in bytes; SFA [M,K/32],
+ * SFB [N,K/32] uint8 row-major. C bf16/fp32. Any M, N >= 1; K a multiple of
+ * 256. For skinny M the call splits K across workgroups when `workspace`
+ * is large enough (gemm_a4w4_mxfp4_workspace_bytes) and reduces the fp32
+ * partials in the same launch; the workspace's counter words must be zero
+ * before the first call and every call leaves them zero. */
+hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args);
+
+/* ------------------------------------------------------------------ */
+/* Offline layout helpers (host, CPU).                                  */
+/* ------------------------------------------------------------------ */
+/* K-panel pre-shuffle, BPS host.cc:92-111: dst[kt][n][ki] = src[n][kt*128+ki]. */
+int qgemm_shuffle_b_kpanel(const uint8_t* src, uint8_t* dst, int n, int k_bytes);
+/* shuffle_weight(16,16): SNAP host.cc:161-179 (fp8) and
+ * MX4/candidate_m10 host.cc:215-225 (fp4, over bytes). */
+int qgemm_shuffle_weight_16x16(const uint8_t* src, uint8_t* dst, int n, int k_bytes);
+/* aiter e8m0_shuffle, MX4/candidate_m10 host.cc:194-206. */
+size_t qgemm_e8m0_shuffle_bytes(int rows, int groups_k);
+int qgemm_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int groups_k);
+/* B'' for gemm_a8w8_blockscale_ldsbypass from raw B [N][K] (host pack, the
+ * role of LBP/gemm_a8w8_blockscale_ldsbypass_hostpack_host.cc:155-218). */
+size_t qgemm_ldsbypass_b_bytes(int n, int k);
+int qgemm_pack_b_ldsbypass(const uint8_t* b_raw, uint8_t* b_pp, int n, int k);
+
+/* ------------------------------------------------------------------ */
+/* Layout probe (the reference's mfma_layout_probe/ known answers).     */
+/* ------------------------------------------------------------------ */
+/* Launches the one-wave scaled-MFMA and LDS-DMA probes on `stream`;
+ * dev_out is device memory for qgemm_probe_words() int32 words (word map in
+ * 355_1_trans_amd/csrc/probe.hip). The reference's probes are
+ * mfma_layout_probe/probe_count.cu:1-63 and probe_scale_map.cu:1-86. */
+int qgemm_probe_words(void);
+hipError_t qgemm_probe_mfma_layout(int32_t* dev_out, hipStream_t stream);
+
+/* Library identification: "gfx950" build string. */
+const char* qgemm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

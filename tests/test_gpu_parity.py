@@ -1,0 +1,129 @@
+"""GPU parity of every entry point against the CPU oracle (seeded inputs,
+BASELINE tolerance |y-y_ref| <= 2^-7|y_ref| + 1e-3 rms(y_ref))."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, make_bs, make_mx4, make_mx8, out_to_f32, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+# ----------------------------------------------------------------- probes
+def test_probe_known_answers(qgemm, gpu):
+    w = qgemm.probe_mfma_layout(gpu).numpy()
+    lanes = np.arange(64)
+    # srcA row index i and srcB column index j of every (lane, reg) output.
+    i_of = w[0:256].reshape(64, 4) - 1
+    j_of = w[256:512].reshape(64, 4) - 1
+    exp_i = (4 * (lanes // 16))[:, None] + np.arange(4)[None, :]
+    exp_j = np.repeat((lanes % 16)[:, None], 4, axis=1)
+    assert np.array_equal(i_of, exp_i), f"srcA-row map {i_of}"
+    assert np.array_equal(j_of, exp_j), f"srcB-col map {j_of}"
+    # reference known answers: 480 (per-K-block scales), 128 (op_sel byte 1)
+    assert np.all(w[512:768] == 480)
+    assert np.all(w[768:1024] == 128)
+    # single-lane scale boost: +32 on exactly the boosted srcA row (BLOCK model)
+    d = w[1024:1280].reshape(64, 4)
+    assert np.all(d[i_of == 5] == 160) and np.all(d[i_of != 5] == 128)
+    assert np.all(w[1280:1536] == 128)
+    d4 = w[1536:1792].reshape(64, 4)
+    assert np.all(d4[i_of == 5] == 160) and np.all(d4[i_of != 5] == 128)
+    # LDS DMA: lane L's 16 bytes land at LDS offset 16*L
+    img = w[1792:2048].astype(np.int64).astype(np.uint32).view(np.uint8).reshape(64, 16)
+    pattern = ((7 * np.arange(1024) + 3) & 255).astype(np.uint8).reshape(64, 16)
+    src = (5 * lanes + 3) & 63
+    assert np.array_equal(img, pattern[src])
+    # fp8 register -> scale-block map: dwords 0-3 of lane group q carry K
+    # [16q, 16q+16), dwords 4-7 carry K [64+16q, 64+16q+16); scale block = K/32.
+    q0, d0 = np.arange(32) // 8, np.arange(32) % 8
+    exp8 = 2 ** np.where(d0 < 4, q0 // 2, 2 + q0 // 2)
+    assert np.array_equal(w[2048:2080], exp8), w[2048:2080]
+    # fp4: dwords 0-3 of lane group q carry K [32q, 32q+32) -> block q
+    assert np.array_equal(w[2080:2096], 2 ** (np.arange(16) // 4)), w[2080:2096]
+
+
+# ----------------------------------------------------------------- MXFP8
+MX8_SHAPES = [(256, 256, 128), (256, 512, 1024), (300, 520, 384), (1, 1536, 7168), (32, 1536, 7168),
+              (513, 272, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", MX8_SHAPES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mxfp8(qgemm, gpu, m, n, k, dtype):
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=m + n + k)
+    ref = O.gemm_mx8(qa, qb, ea, eb)
+    y = qgemm.gemm_a8w8_mxfp8(to_dev(qa, None, gpu).view(torch.float8_e4m3fn),
+                              to_dev(qb, None, gpu).view(torch.float8_e4m3fn),
+                              to_dev(ea, None, gpu), to_dev(eb, None, gpu), dtype=dtype)
+    assert_close(ref, out_to_f32(y), f"mxfp8 {m}x{n}x{k}")
+
+
+def test_mxfp8_k_pattern_scales(qgemm, gpu):
+    """Distinct per-K-group scales catch K-group misrouting (MX4 host.cc:185-187)."""
+    m, n, k = 256, 256, 1024
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=7)
+    ea = np.broadcast_to((120 + (np.arange(k // 32) % 13)).astype(np.uint8), ea.shape).copy()
+    ref = O.gemm_mx8(qa, qb, ea, eb)
+    y = qgemm.gemm_a8w8_mxfp8(to_dev(qa, None, gpu).view(torch.float8_e4m3fn),
+                              to_dev(qb, None, gpu).view(torch.float8_e4m3fn),
+                              to_dev(ea, None, gpu), to_dev(eb, None, gpu), dtype=torch.float32)
+    assert_close(ref, out_to_f32(y), "mxfp8 K-pattern")
+
+
+# ----------------------------------------------------------------- MXFP4
+MX4_SHAPES = [(256, 256, 256), (256, 512, 1024), (100, 300, 512), (1, 512, 2048), (257, 256, 768)]
+
+
+@pytest.mark.parametrize("m,n,k", MX4_SHAPES)
+def test_mxfp4(qgemm, gpu, m, n, k):
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=m * 3 + k)
+    ref = O.gemm_mx4(qa, qb, ea, eb)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.bfloat16)
+    assert_close(ref, out_to_f32(y), f"mxfp4 {m}x{n}x{k}")
+
+
+# ----------------------------------------------- block-scale, E8M0 (SNAP ABI)
+def _snap_inputs(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    a = O.e4m3_encode(rng.uniform(-1, 1, (m, k)).astype(np.float32))
+    b = O.e4m3_encode(rng.uniform(-1, 1, (n, k)).astype(np.float32))
+    sfa_km = rng.integers(124, 131, (k // 128, m)).astype(np.uint8)  # physical [K/128][M]
+    sfb = rng.integers(124, 131, (n // 128, k // 128)).astype(np.uint8)
+    return a, b, sfa_km, sfb
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 256, 1152), (256, 768, 640)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_blockscale_e8m0(qgemm, gpu, m, n, k, dtype):
+    a, b, sfa_km, sfb = _snap_inputs(m, n, k, seed=m + k)
+    ref = O.gemm_bs_e8m0(a, b, sfa_km, sfb)
+    bp = O.shuffle_weight_16x16(b)
+    A = to_dev(a, None, gpu).view(torch.float8_e4m3fn)
+    Bp = to_dev(bp, None, gpu)
+    A_scale = to_dev(sfa_km, None, gpu).t()          # logical [M, K/128], strides (1, M)
+    y = qgemm.blockscale_bpreshuffle.gemm_a8w8_blockscale_bpreshuffle(A, Bp, A_scale, to_dev(sfb, None, gpu),
+                                                                      dtype=dtype)
+    assert_close(ref, out_to_f32(y), f"bs-e8m0 {m}x{n}x{k}")
+
+
+# ----------------------------------------------- block-scale, fp32 scales
+BS_SHAPES = [(32, 1536, 7168), (256, 256, 128), (300, 520, 384), (1, 2112, 7168), (16, 4096, 1024),
+             (600, 384, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", BS_SHAPES)
+@pytest.mark.parametrize("sfa_layout", ["mk", "km"])
+def test_blockscale_fp32(qgemm, gpu, m, n, k, sfa_layout):
+    qa, qb, sa, sb = make_bs(m, n, k, seed=m + 2 * n + k)
+    ref = O.gemm_bs_fp32(qa, qb, sa, sb)
+    A = to_dev(qa, None, gpu).view(torch.float8_e4m3fn)
+    Bk = qgemm.shuffle_b_kpanel(to_dev(qb, None, gpu)).view(torch.float8_e4m3fn)
+    if sfa_layout == "mk":
+        A_scale = to_dev(sa, None, gpu)
+    else:
+        A_scale = to_dev(np.ascontiguousarray(sa.T), None, gpu).t()
+    y = qgemm.gemm_a8w8_bpreshuffle(A, Bk, A_scale, to_dev(sb, None, gpu), dtype=torch.bfloat16)
+    assert_close(ref, out_to_f32(y), f"bs-fp32 {m}x{n}x{k} {sfa_layout}")
