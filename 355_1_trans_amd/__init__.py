@@ -16,13 +16,16 @@ There is no CPU fallback: every wrapper raises if the library is missing or
 the tensors are not on a GPU.
 """
 import ctypes
+import os
 from functools import lru_cache
 from pathlib import Path
 
 import torch
 
 _PKG = Path(__file__).resolve().parent
-LIB_PATH = _PKG / "libqgemm.so"
+# QGEMM_LIB selects another build of the same library (A/B tests of kernel
+# variants); by default the in-tree build is loaded.
+LIB_PATH = Path(os.environ.get("QGEMM_LIB", str(_PKG / "libqgemm.so")))
 
 OUT_FP32 = 0
 OUT_BF16 = 1

@@ -92,6 +92,14 @@ void fill_common(TileArgs& t, const opus_gemm_scale_kargs& a, int kbytes) {
 
 bool flag01(int v) { return v == 0 || v == 1; }
 
+// 16-byte MX scale panels need 16-byte aligned scale rows and whole panels
+// (K/32 a multiple of 16, i.e. K % 512 == 0).
+bool mx_wide_panels(const opus_gemm_scale_kargs& a) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a.ptr_sfa), pb = reinterpret_cast<uintptr_t>(a.ptr_sfb);
+    return a.k % 512 == 0 && (pa & 15) == 0 && (pb & 15) == 0 && a.stride_sfa % 16 == 0 && a.stride_sfb % 16 == 0 &&
+           (a.batch == 1 || (a.stride_sfa_batch % 16 == 0 && a.stride_sfb_batch % 16 == 0));
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 // The kernels move A/B rows with 16-byte DMAs and scales with 4-byte DMAs.
@@ -157,7 +165,7 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     fill_common(t, *args, args->k);
     t.sfa_sm = args->stride_sfa;
     t.sfb_sn = args->stride_sfb;
-    return qg::launch_tile_mx8_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, stream);
+    return qg::launch_tile_mx8_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, mx_wide_panels(*args), stream);
 }
 
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
@@ -178,7 +186,7 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     fill_common(t, *args, args->k / 2);
     t.sfa_sm = args->stride_sfa;
     t.sfb_sn = args->stride_sfb;
-    return qg::launch_tile_mx4_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, stream);
+    return qg::launch_tile_mx4_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, mx_wide_panels(*args), stream);
 }
 
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {

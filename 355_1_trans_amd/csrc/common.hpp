@@ -40,24 +40,27 @@ __device__ __forceinline__ void dma4(const void* gsrc, QG_LDS void* lds_base) {
     __builtin_amdgcn_global_load_lds(gsrc, lds_base, 4, 0, 0);
 }
 
-// fp32 -> bf16, round to nearest even, NaN quieted (the rounding the
-// reference validates against: SNAP host.cc:185-193).
-__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
+// fp32 -> bf16 with round-to-nearest-even (the rounding the reference
+// validates against, SNAP host.cc:185-193): v_cvt_pk_bf16_f32 converts two
+// values per instruction in hardware.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return bf16_rne_bits(lo) | (bf16_rne_bits(hi) << 16);
+    const bf16x2_t b = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, b);
 }
+__device__ __forceinline__ uint16_t bf16_bits(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xffffu); }
 
 // Row swizzle of a 128-byte LDS row: logical 16-byte chunk c of row r lives
-// at physical chunk c ^ swz(r), where swz depends on r mod 16 only.  Within
-// any aligned group of 16 rows, the 16 lanes that read the same logical
-// chunk of the 16 rows touch 16 distinct 16-byte bank groups (64 banks x 4 B)
-// and each aligned 8-row half touches 8 distinct ones (32-bank view), so a
-// ds_read_b128 of one MFMA operand block is conflict free.
-__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// at physical chunk c ^ swz(r) (r taken mod 16).  Chosen per operand format
+// from SQ_LDS_BANK_CONFLICT measurements of the exact ds_read_b128 patterns
+// (16 rows x 4 lane groups per instruction, 256 B/clk LDS):
+//   fp8 reads chunks q and q+4  -> swz(r) = r & 7                 0 conflicts
+//   fp4 reads chunks 2q and 2q+1 -> swz(r) = (r & 7) ^ (r>>3 & 1) 0 conflicts
+// (each of the two costs one extra cycle per access on the other format).
+template <bool FP4>
+__device__ __forceinline__ int swz(int r) {
+    return FP4 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 7);
+}
 
 }  // namespace qg

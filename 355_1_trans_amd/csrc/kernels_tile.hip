@@ -4,21 +4,23 @@
 namespace qg {
 
 namespace {
-template <int FMT, ScaleKind SK, BLay BL>
+template <int FMT, ScaleKind SK, BLay BL, int PB = 16>
 hipError_t launch_tile(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     const dim3 grid(a.tiles_m * a.tiles_n, 1, batch);
     const dim3 block(tile_threads<SK>());
-    if (bf16) tile_gemm_kernel<FMT, SK, BL, true><<<grid, block, 0, s>>>(a);
-    else tile_gemm_kernel<FMT, SK, BL, false><<<grid, block, 0, s>>>(a);
+    if (bf16) tile_gemm_kernel<FMT, SK, BL, true, PB><<<grid, block, 0, s>>>(a);
+    else tile_gemm_kernel<FMT, SK, BL, false, PB><<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 }  // namespace
 
-hipError_t launch_tile_mx8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
-    return launch_tile<kFmtFp8, ScaleKind::MX, BLay::RAW>(a, batch, bf16, s);
+hipError_t launch_tile_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s) {
+    return wide_panels ? launch_tile<kFmtFp8, ScaleKind::MX, BLay::RAW, 16>(a, batch, bf16, s)
+                       : launch_tile<kFmtFp8, ScaleKind::MX, BLay::RAW, 4>(a, batch, bf16, s);
 }
-hipError_t launch_tile_mx4_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
-    return launch_tile<kFmtFp4, ScaleKind::MX, BLay::RAW>(a, batch, bf16, s);
+hipError_t launch_tile_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s) {
+    return wide_panels ? launch_tile<kFmtFp4, ScaleKind::MX, BLay::RAW, 16>(a, batch, bf16, s)
+                       : launch_tile<kFmtFp4, ScaleKind::MX, BLay::RAW, 8>(a, batch, bf16, s);
 }
 hipError_t launch_tile_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     return launch_tile<kFmtFp8, ScaleKind::BS8, BLay::W16>(a, batch, bf16, s);
