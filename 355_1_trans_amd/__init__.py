@@ -9,11 +9,21 @@ and launch on the current stream:
   reference's E8M0 block-scale adapter (SNAP blockscale_bpreshuffle.py:37-97);
 * ``gemm_a8w8_bpreshuffle`` -- block-scale FP8 with fp32 1x128 / 128x128
   scales and a K-panel pre-shuffled B (BPS host.cc:66-111, 254-284);
+* ``gemm_a8w8_ldsbypass`` -- the same GEMM with B in the fragment order
+  B'' that the LDS-bypass kernel streams straight into registers
+  (LBP host.cc:283-294), with ``ldsbypass_repack`` (GPU, from the K-panel
+  B') and ``ldsbypass_pack_b`` (CPU, from raw B) to build B'';
 * ``gemm_a8w8_mxfp8`` -- MXFP8 TN GEMM (MX8 host.cc:96-122, 266-296);
 * ``gemm_a4w4_mxfp4`` -- MXFP4 A4W4 GEMM (MX4 host.cc:96-115, 201-216).
 
 There is no CPU fallback: every wrapper raises if the library is missing or
 the tensors are not on a GPU.
+
+Skinny-M calls split K across workgroups and reduce the fp32 partials in the
+same launch; they need a workspace whose counter words start at zero (every
+call leaves them zero).  ``workspace=None`` uses one cached, zero-initialised
+buffer per (device, stream); pass a tensor to supply your own, or
+``workspace=False`` to run without split-K.
 """
 import ctypes
 import os
@@ -74,6 +84,12 @@ EXPORTS = {
     "gemm_a4w4_mxfp4": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),
     "gemm_a4w4_mxfp4_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "gemm_a8w8_blockscale_ldsbypass": (ctypes.c_int, [ctypes.POINTER(LdsBypassKargs), ctypes.c_int,
+                                                      ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a8w8_blockscale_ldsbypass_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LdsBypassKargs)]),
+    "gemm_a8w8_blockscale_ldsbypass_repack": (ctypes.c_int, [ctypes.POINTER(LdsBypassKargs), ctypes.c_void_p]),
+    "qgemm_ldsbypass_b_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "qgemm_pack_b_ldsbypass": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
     "qgemm_shuffle_b_kpanel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
     "qgemm_shuffle_weight_16x16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
     "qgemm_e8m0_shuffle_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
@@ -123,6 +139,35 @@ def _require_gpu(*tensors):
     return dev
 
 
+_WORKSPACES = {}
+
+
+def _workspace(query, args, workspace, dev, stream):
+    """(pointer, bytes) of the split-K workspace for this call.
+
+    ``query`` is the entry's *_workspace_bytes function; 0 means the call
+    does not split K.  The cached buffer is zero-filled on allocation (on the
+    call's stream, so it is ordered before the launch) and every launch
+    leaves its counter words zero again."""
+    if workspace is False:
+        return None, 0
+    need = query(ctypes.byref(args))
+    if workspace is not None:
+        return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    if need == 0:
+        return None, 0
+    key = (dev.index, stream.cuda_stream)
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < need:
+        buf = torch.zeros((need + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = buf
+    return buf.data_ptr(), buf.numel()
+
+
+def _ws_tensor(workspace):
+    return workspace if isinstance(workspace, torch.Tensor) else None
+
+
 def _u8(t):
     return t.view(torch.uint8) if t.dtype != torch.uint8 else t
 
@@ -143,7 +188,7 @@ def _out_code(dtype):
     raise ValueError("output dtype must be torch.bfloat16 or torch.float32")
 
 
-def gemm_a8w8_mxfp8(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None):
+def gemm_a8w8_mxfp8(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None, workspace=None):
     """MXFP8 TN GEMM: A [M,K] e4m3, B [N,K] e4m3, A_scale [M,K/32], B_scale [N,K/32] E8M0 bytes."""
     dev = _require_gpu(A, B, A_scale, B_scale)
     m, k = A.shape
@@ -160,8 +205,10 @@ def gemm_a8w8_mxfp8(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None):
                  A_scale.data_ptr(), B_scale.data_ptr(), k // 32, k // 32, m * (k // 32), n * (k // 32))
     with torch.cuda.device(dev):
         s = _stream(dev)
-        st = lib().gemm_a8w8_mxfp8(ctypes.byref(args), _out_code(dtype), None, 0, ctypes.c_void_p(s.cuda_stream))
-        _record(s, A, B, A_scale, B_scale, out)
+        ws_ptr, ws_bytes = _workspace(lib().gemm_a8w8_mxfp8_workspace_bytes, args, workspace, dev, s)
+        st = lib().gemm_a8w8_mxfp8(ctypes.byref(args), _out_code(dtype), ws_ptr, ws_bytes,
+                                   ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B, A_scale, B_scale, out, _ws_tensor(workspace))
     _check(st, "gemm_a8w8_mxfp8")
     return out
 
@@ -182,13 +229,12 @@ def gemm_a4w4_mxfp4(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None, work
     out = _out(out, (m, n), dtype, dev)
     args = Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
                  A_scale.data_ptr(), B_scale.data_ptr(), k // 32, k // 32, m * (k // 32), n * (k // 32))
-    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
-                                                             workspace.numel() * workspace.element_size())
     with torch.cuda.device(dev):
         s = _stream(dev)
+        ws_ptr, ws_bytes = _workspace(lib().gemm_a4w4_mxfp4_workspace_bytes, args, workspace, dev, s)
         st = lib().gemm_a4w4_mxfp4(ctypes.byref(args), _out_code(dtype), ws_ptr, ws_bytes,
                                    ctypes.c_void_p(s.cuda_stream))
-        _record(s, A, B, A_scale, B_scale, out, workspace)
+        _record(s, A, B, A_scale, B_scale, out, _ws_tensor(workspace))
     _check(st, "gemm_a4w4_mxfp4")
     return out
 
@@ -212,23 +258,91 @@ def gemm_a8w8_bpreshuffle(A, B_kpanel, A_scale, B_scale, dtype=torch.bfloat16, o
         raise ValueError("block scales must be fp32")
     if not (A.is_contiguous() and B_kpanel.is_contiguous() and B_scale.is_contiguous()):
         raise ValueError("A, B_kpanel and B_scale must be contiguous")
-    if A_scale.is_contiguous():
-        stride_sfa = 1 if m > 1 else m
-    elif A_scale.stride() == (1, m):
-        stride_sfa = m
-    else:
-        raise ValueError("A_scale must be row-major [M,K/128] or column-major with strides (1,M)")
+    stride_sfa = _sfa_stride(A_scale, m)
     out = _out(out, (m, n), dtype, dev)
     args = Kargs(A.data_ptr(), B_kpanel.data_ptr(), out.data_ptr(), m, n, k, 1, k, 128, n, m * k, n * k, m * n,
                  A_scale.data_ptr(), B_scale.data_ptr(), stride_sfa, kg, m * kg, B_scale.shape[0] * kg)
-    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
-                                                             workspace.numel() * workspace.element_size())
     with torch.cuda.device(dev):
         s = _stream(dev)
+        ws_ptr, ws_bytes = _workspace(lib().gemm_a8w8_blockscale_bpreshuffle_workspace_bytes, args, workspace,
+                                      dev, s)
         st = lib().gemm_a8w8_blockscale_bpreshuffle(ctypes.byref(args), _out_code(dtype), ws_ptr, ws_bytes,
                                                     ctypes.c_void_p(s.cuda_stream))
-        _record(s, A, B_kpanel, A_scale, B_scale, out, workspace)
+        _record(s, A, B_kpanel, A_scale, B_scale, out, _ws_tensor(workspace))
     _check(st, "gemm_a8w8_blockscale_bpreshuffle")
+    return out
+
+
+def _sfa_stride(A_scale, m):
+    if A_scale.is_contiguous():
+        return 1 if m > 1 else m
+    if A_scale.stride() == (1, m):
+        return m
+    raise ValueError("A_scale must be row-major [M,K/128] or column-major with strides (1,M)")
+
+
+def ldsbypass_b_bytes(n, k):
+    """Bytes of B'' for an [N, K] fp8 weight (N padded to a multiple of 16)."""
+    return lib().qgemm_ldsbypass_b_bytes(n, k)
+
+
+def ldsbypass_pack_b(B):
+    """Host pack of B'' from raw B [N, K] (CPU tensor, 1-byte elements)."""
+    if B.is_cuda or B.dim() != 2 or B.element_size() != 1 or not B.is_contiguous():
+        raise ValueError("B must be a contiguous CPU [N, K] tensor of 1-byte elements")
+    n, k = B.shape
+    nbytes = ldsbypass_b_bytes(n, k)
+    if nbytes == 0:
+        raise ValueError("requires N >= 1 and K % 128 == 0")
+    out = torch.empty(nbytes, dtype=torch.uint8)
+    _check(lib().qgemm_pack_b_ldsbypass(B.data_ptr(), out.data_ptr(), n, k), "qgemm_pack_b_ldsbypass")
+    return out
+
+
+def ldsbypass_repack(B_kpanel, out=None):
+    """GPU repack of the K-panel B' [K/128, N, 128] into B'' (LBP host.cc:289-294)."""
+    dev = _require_gpu(B_kpanel)
+    if B_kpanel.dim() != 3 or B_kpanel.shape[2] != 128 or not B_kpanel.is_contiguous():
+        raise ValueError("B_kpanel must be a contiguous [K/128, N, 128] tensor")
+    k, n = B_kpanel.shape[0] * 128, B_kpanel.shape[1]
+    out = _out(out, (ldsbypass_b_bytes(n, k),), torch.uint8, dev)
+    args = LdsBypassKargs(None, B_kpanel.data_ptr(), out.data_ptr(), None, 0, n, k, 1, 0, 128, 0, 0, n * k, 0,
+                          None, None, 0, 0, 0, 0, out.numel())
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        st = lib().gemm_a8w8_blockscale_ldsbypass_repack(ctypes.byref(args), ctypes.c_void_p(s.cuda_stream))
+        _record(s, B_kpanel, out)
+    _check(st, "gemm_a8w8_blockscale_ldsbypass_repack")
+    return out
+
+
+def gemm_a8w8_ldsbypass(A, B_pp, A_scale, B_scale, n, dtype=torch.bfloat16, out=None, workspace=None):
+    """Block-scale FP8 (fp32 scales) with B given as B'' (``ldsbypass_repack``
+    or ``ldsbypass_pack_b``); A, A_scale, B_scale as in gemm_a8w8_bpreshuffle."""
+    dev = _require_gpu(A, B_pp, A_scale, B_scale)
+    m, k = A.shape
+    kg = k // 128
+    if k % 128 or A_scale.shape != (m, kg) or B_scale.shape != ((n + 127) // 128, kg):
+        raise ValueError("requires K % 128 == 0, A_scale [M,K/128], B_scale [ceil(N/128),K/128]")
+    if A_scale.dtype != torch.float32 or B_scale.dtype != torch.float32:
+        raise ValueError("block scales must be fp32")
+    if B_pp.numel() * B_pp.element_size() != ldsbypass_b_bytes(n, k):
+        raise ValueError("B_pp must hold ldsbypass_b_bytes(N, K) bytes")
+    if not (A.is_contiguous() and B_pp.is_contiguous() and B_scale.is_contiguous()):
+        raise ValueError("A, B_pp and B_scale must be contiguous")
+    stride_sfa = _sfa_stride(A_scale, m)
+    out = _out(out, (m, n), dtype, dev)
+    args = LdsBypassKargs(A.data_ptr(), None, B_pp.data_ptr(), out.data_ptr(), m, n, k, 1, k, 128, n, m * k,
+                          n * k, m * n, A_scale.data_ptr(), B_scale.data_ptr(), stride_sfa, kg, m * kg,
+                          B_scale.shape[0] * kg, B_pp.numel() * B_pp.element_size())
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        ws_ptr, ws_bytes = _workspace(lib().gemm_a8w8_blockscale_ldsbypass_workspace_bytes, args, workspace,
+                                      dev, s)
+        st = lib().gemm_a8w8_blockscale_ldsbypass(ctypes.byref(args), _out_code(dtype), ws_ptr, ws_bytes,
+                                                  ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B_pp, A_scale, B_scale, out, _ws_tensor(workspace))
+    _check(st, "gemm_a8w8_blockscale_ldsbypass")
     return out
 
 

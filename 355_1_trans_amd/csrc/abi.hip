@@ -5,6 +5,7 @@
 // reference launcher, SNAP gemm_a8w8_blockscale_bpreshuffle_launch.cc:29-65).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <climits>
 #include <cstdint>
@@ -12,6 +13,7 @@
 
 #include "launch.hpp"
 #include "qgemm.h"
+#include "skinny_gemm.hpp"
 
 static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "reference kargs ABI");
@@ -20,6 +22,8 @@ static_assert(__builtin_offsetof(opus_gemm_ldsbypass_kargs, ptr_c) == 24, "ldsby
 
 namespace {
 
+using qg::SkinnyArgs;
+using qg::SkinnyKind;
 using qg::TileArgs;
 
 constexpr int kMaxDevices = 64;
@@ -112,6 +116,78 @@ bool dma_aligned(const opus_gemm_scale_kargs& a, bool scales_dword) {
     return true;
 }
 
+// ---------------------------------------------------------------- split-K plan
+// Skinny-M problems (too few 256 x 256 tiles to fill the GPU) run on the
+// skinny kernel.  One CU streams ~45-55 GB/s, so HBM bandwidth needs about
+// 200+ busy CUs (MI355X has 256): the plan takes the widest N tile (64, 32 or
+// 16 columns) that gives at least kMinTiles workgroups, and splits K across
+// workgroups only when 16-column tiles still give fewer, keeping >= 16
+// K-tiles per slice and the fp32 partials below a quarter of B's bytes.  The
+// plan depends on the shape only, so the workspace query and the launch
+// always agree.
+constexpr int kCUs = 256;
+constexpr int kMinTiles = 192;
+// Split-K runs only when the grid has fewer than kMinTiles tiles, so its
+// counters fit a fixed block at the start of the workspace; a fixed size
+// keeps the counters of any later call clear of earlier calls' partials.
+constexpr size_t kCounterBytes = 2 * kCUs * sizeof(unsigned);
+static_assert(kMinTiles <= 2 * kCUs, "counter block too small");
+
+struct Plan {
+    bool skinny = false;
+    int mb = 1, nb = 1, m_tiles = 1, n_tiles = 1, splitk = 1, kt_per_split = 1;
+    size_t ctr_bytes = 0, ws_bytes = 0;
+};
+
+Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny) {
+    Plan p;
+    const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    p.skinny = force_skinny || (m <= 256 && tiles256 < 128);
+    p.kt_per_split = k_tiles;
+    if (!p.skinny) return p;
+    p.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    p.m_tiles = ceil_div(m, 16 * p.mb);
+    for (int nb = 4; nb >= 1; nb /= 2) {
+        p.nb = nb;
+        p.n_tiles = ceil_div(n, 16 * nb);
+        if ((long long)p.n_tiles * p.m_tiles * batch >= kMinTiles) break;
+    }
+    const long long base = (long long)p.n_tiles * p.m_tiles * batch;
+    if (base >= kMinTiles) return p;
+    long long split = (kCUs + base - 1) / base;
+    split = std::min<long long>(split, k_tiles / 16);
+    split = std::min<long long>(split, b_bytes / (16LL * m * n));
+    if (split <= 1) return p;
+    p.kt_per_split = ceil_div(k_tiles, (int)split);
+    p.splitk = ceil_div(k_tiles, p.kt_per_split);
+    if (p.splitk > 1) {
+        p.ctr_bytes = kCounterBytes;    // base < kMinTiles counters
+        p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
+    }
+    return p;
+}
+
+// Launches the skinny kernel.  A NULL workspace runs one K slice (no
+// partials); a non-NULL one must hold plan.ws_bytes and be 256-byte aligned.
+hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bool bf16, void* ws,
+                      size_t ws_bytes, int k_tiles, hipStream_t stream) {
+    SkinnyArgs s{};
+    s.t = t;
+    if (pl.splitk > 1 && ws) {
+        if (ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return hipErrorInvalidValue;
+        s.counters = static_cast<unsigned*>(ws);
+        s.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl.ctr_bytes);
+    } else {
+        pl.splitk = 1;
+        pl.kt_per_split = k_tiles;
+    }
+    s.splitk = pl.splitk;
+    s.kt_per_split = pl.kt_per_split;
+    s.n_tiles = pl.n_tiles;
+    s.m_tiles = pl.m_tiles;
+    return qg::launch_skinny(kind, s, pl.mb, pl.nb, batch, bf16, stream);
+}
+
 // Validation shared by the MX entry points: dense or padded row-major A/B,
 // row-major scales, C [M, N] with stride_c >= N.
 hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kbytes_per_row, int k_align) {
@@ -148,6 +224,72 @@ hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kby
     return hipSuccess;
 }
 
+// fp32 block-scale operands (both B layouts): A [M,K] (stride_a >= K),
+// SFA column-major [K/128][M] (stride_sfa >= M) or row-major [M][K/128]
+// (stride_sfa == 1), SFB [ceil(N/128)][K/128] (stride_sfb >= K/128), C [M,N].
+// B is checked by the caller (b_data, b_bytes_per_batch).  Returns the SFA
+// element strides along M and K.
+hipError_t validate_bsf32(const opus_gemm_scale_kargs& a, const void* b_data, long long b_bytes_per_batch,
+                          int out_dtype, int* sfa_sm, int* sfa_sk) {
+    if (!a.ptr_a || !b_data || !a.ptr_c || !a.ptr_sfa || !a.ptr_sfb || !flag01(out_dtype))
+        return hipErrorInvalidValue;
+    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % 128) return hipErrorInvalidValue;
+    const int kg = a.k / 128, nbk = ceil_div(a.n, 128);
+    const bool sfa_rowmajor = (a.stride_sfa == 1 && a.m > 1);
+    if (a.stride_a < a.k || a.stride_c < a.n || a.stride_sfb < kg || (!sfa_rowmajor && a.stride_sfa < a.m))
+        return hipErrorInvalidValue;
+    if (!aligned(a.ptr_a, 16) || !aligned(b_data, 16) || a.stride_a % 16 || a.stride_a_batch % 16 ||
+        !aligned(a.ptr_sfa, 4) || !aligned(a.ptr_sfb, 4))
+        return hipErrorInvalidValue;
+    const long long outb = out_dtype ? 2 : 4;
+    const long long sfa_span = sfa_rowmajor ? (long long)a.m * kg : (long long)(kg - 1) * a.stride_sfa + a.m;
+    if (a.batch > 1 &&
+        ((long long)a.stride_a_batch < (long long)a.m * a.stride_a ||
+         (long long)a.stride_c_batch < (long long)a.m * a.stride_c || (long long)a.stride_sfa_batch < sfa_span ||
+         (long long)a.stride_sfb_batch < (long long)nbk * a.stride_sfb))
+        return hipErrorInvalidValue;
+    if (!bounded_count(a.m, a.stride_a, 1, 1) || !bounded_count(b_bytes_per_batch, 1, 1, 1) ||
+        !bounded_count(a.m, a.stride_c, 1, outb) || !bounded_count(sfa_span, 1, 1, 4) ||
+        !bounded_count(nbk, a.stride_sfb, 1, 4))
+        return hipErrorInvalidValue;
+    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb);
+    if (overlaps(a.ptr_c, cb, a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, a.k, 1)) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfa, span(a.batch, a.stride_sfa_batch, 1, 0, sfa_span, 4)) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfb, span(a.batch, a.stride_sfb_batch, nbk, a.stride_sfb, kg, 4)))
+        return hipErrorInvalidValue;
+    *sfa_sm = sfa_rowmajor ? kg : 1;
+    *sfa_sk = sfa_rowmajor ? 1 : a.stride_sfa;
+    return hipSuccess;
+}
+
+// B'' bytes of one batch: 16-row blocks, N padded up to a multiple of 16.
+size_t frag_bytes(int n, int k) { return (size_t)ceil_div(n, 16) * 16 * (size_t)k; }
+
+// The 96-byte view of the LDS-bypass arguments with B = B''.
+opus_gemm_scale_kargs from_ldsbypass(const opus_gemm_ldsbypass_kargs& l) {
+    opus_gemm_scale_kargs a{};
+    a.ptr_a = l.ptr_a;
+    a.ptr_b = l.ptr_b_pp;
+    a.ptr_c = l.ptr_c;
+    a.m = l.m;
+    a.n = l.n;
+    a.k = l.k;
+    a.batch = l.batch;
+    a.stride_a = l.stride_a;
+    a.stride_b = l.stride_b;
+    a.stride_c = l.stride_c;
+    a.stride_a_batch = l.stride_a_batch;
+    a.stride_b_batch = l.stride_b_pp_batch;
+    a.stride_c_batch = l.stride_c_batch;
+    a.ptr_sfa = l.ptr_sfa;
+    a.ptr_sfb = l.ptr_sfb;
+    a.stride_sfa = l.stride_sfa;
+    a.stride_sfb = l.stride_sfb;
+    a.stride_sfa_batch = l.stride_sfa_batch;
+    a.stride_sfb_batch = l.stride_sfb_batch;
+    return a;
+}
+
 }  // namespace
 
 extern "C" {
@@ -155,43 +297,49 @@ extern "C" {
 // ---------------------------------------------------------------- MXFP8
 hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     hipError_t st = validate_mx(args, out_dtype, args ? args->k : 0, 128);
     if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
+    const auto& a = *args;
     TileArgs t{};
-    fill_common(t, *args, args->k);
-    t.sfa_sm = args->stride_sfa;
-    t.sfb_sn = args->stride_sfb;
-    return qg::launch_tile_mx8_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, mx_wide_panels(*args), stream);
+    fill_common(t, a, a.k);
+    t.sfa_sm = a.stride_sfa;
+    t.sfb_sn = a.stride_sfb;
+    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
+    if (pl.skinny)
+        return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
+    return qg::launch_tile_mx8_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
 }
 
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
-    (void)args;
-    return 0;
+    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
+    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false).ws_bytes;
 }
 
 // ---------------------------------------------------------------- MXFP4
 hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256);
     if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
+    const auto& a = *args;
     TileArgs t{};
-    fill_common(t, *args, args->k / 2);
-    t.sfa_sm = args->stride_sfa;
-    t.sfb_sn = args->stride_sfb;
-    return qg::launch_tile_mx4_raw(t, args->batch, out_dtype == QGEMM_OUT_BF16, mx_wide_panels(*args), stream);
+    fill_common(t, a, a.k / 2);
+    t.sfa_sm = a.stride_sfa;
+    t.sfb_sn = a.stride_sfb;
+    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false);
+    if (pl.skinny)
+        return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);
+    return qg::launch_tile_mx4_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
 }
 
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
-    (void)args;
-    return 0;
+    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
+    return plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false).ws_bytes;
 }
 
 // ------------------------------------------------ block-scale FP8, E8M0 scales
@@ -231,53 +379,88 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
 // ------------------------------------------------ block-scale FP8, fp32 scales
 hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
                                             size_t workspace_bytes, hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
-    if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
-        !flag01(out_dtype))
-        return hipErrorInvalidValue;
+    if (!args) return hipErrorInvalidValue;
     const auto& a = *args;
-    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % 128) return hipErrorInvalidValue;
-    const int kg = a.k / 128, nbk = ceil_div(a.n, 128);
-    // B is K-panel [K/128][N][128] (stride_b = 128); SFA column-major
-    // [K/128][M] (stride_sfa >= M) or row-major [M][K/128] (stride_sfa == 1).
-    const bool sfa_rowmajor = (a.stride_sfa == 1 && a.m > 1);
-    if (a.stride_a < a.k || a.stride_b != 128 || a.stride_c < a.n || a.stride_sfb < kg ||
-        (!sfa_rowmajor && a.stride_sfa < a.m))
-        return hipErrorInvalidValue;
-    if (!dma_aligned(a, true)) return hipErrorInvalidValue;
-    const long long outb = out_dtype ? 2 : 4;
-    const long long sfa_elems = (long long)a.m * kg;
-    const long long sfa_span = sfa_rowmajor ? sfa_elems : (long long)(kg - 1) * a.stride_sfa + a.m;
-    if (a.batch > 1 &&
-        ((long long)a.stride_a_batch < (long long)a.m * a.stride_a ||
-         (long long)a.stride_b_batch < (long long)a.n * a.k ||
-         (long long)a.stride_c_batch < (long long)a.m * a.stride_c ||
-         (long long)a.stride_sfa_batch < sfa_span || (long long)a.stride_sfb_batch < (long long)nbk * a.stride_sfb))
-        return hipErrorInvalidValue;
-    if (!bounded_count(a.m, a.stride_a, 1, 1) || !bounded_count(a.n, a.k, 1, 1) ||
-        !bounded_count(a.m, a.stride_c, 1, outb) || !bounded_count(sfa_span, 1, 1, 4) ||
-        !bounded_count(nbk, a.stride_sfb, 1, 4))
-        return hipErrorInvalidValue;
-    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb);
-    if (overlaps(a.ptr_c, cb, a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, a.k, 1)) ||
-        overlaps(a.ptr_c, cb, a.ptr_b, span(a.batch, a.stride_b_batch, 1, 0, (long long)a.n * a.k, 1)) ||
-        overlaps(a.ptr_c, cb, a.ptr_sfa, span(a.batch, a.stride_sfa_batch, 1, 0, sfa_span, 4)) ||
-        overlaps(a.ptr_c, cb, a.ptr_sfb, span(a.batch, a.stride_sfb_batch, nbk, a.stride_sfb, kg, 4)))
-        return hipErrorInvalidValue;
-    hipError_t st = check_arch();
+    // B is K-panel [K/128][N][128] (stride_b = 128, BPS host.cc:263)
+    if (a.stride_b != 128) return hipErrorInvalidValue;
+    const long long bk = (long long)a.n * a.k;
+    int sfa_sm = 0, sfa_sk = 0;
+    hipError_t st = validate_bsf32(a, a.ptr_b, bk, out_dtype, &sfa_sm, &sfa_sk);
+    if (st != hipSuccess) return st;
+    if (a.batch > 1 && ((long long)a.stride_b_batch < bk || a.stride_b_batch % 16)) return hipErrorInvalidValue;
+    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, out_dtype ? 2 : 4);
+    if (overlaps(a.ptr_c, cb, a.ptr_b, span(a.batch, a.stride_b_batch, 1, 0, bk, 1))) return hipErrorInvalidValue;
+    st = check_arch();
     if (st != hipSuccess) return st;
     TileArgs t{};
     fill_common(t, a, a.k);
-    t.sfa_sm = sfa_rowmajor ? kg : 1;
-    t.sfa_sk = sfa_rowmajor ? 1 : a.stride_sfa;
+    t.sfa_sm = sfa_sm;
+    t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
-    return qg::launch_tile_bsf32_kpanel(t, a.batch, out_dtype == QGEMM_OUT_BF16, stream);
+    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bk, false);
+    if (pl.skinny)
+        return run_skinny(SkinnyKind::BSF32_KPANEL, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128,
+                          stream);
+    return qg::launch_tile_bsf32_kpanel(t, a.batch, bf16, stream);
 }
 
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {
-    (void)args;
-    return 0;
+    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
+    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false).ws_bytes;
+}
+
+// ------------------------------------------------ LDS-bypass block-scale FP8
+hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args, int out_dtype, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+    if (!args) return hipErrorInvalidValue;
+    const opus_gemm_scale_kargs a = from_ldsbypass(*args);
+    const long long bpp = a.n > 0 && a.k > 0 ? (long long)frag_bytes(a.n, a.k) : 0;
+    int sfa_sm = 0, sfa_sk = 0;
+    hipError_t st = validate_bsf32(a, args->ptr_b_pp, bpp, out_dtype, &sfa_sm, &sfa_sk);
+    if (st != hipSuccess) return st;
+    if (a.batch > 1 && ((long long)args->stride_b_pp_batch < bpp || args->stride_b_pp_batch % 16))
+        return hipErrorInvalidValue;
+    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, out_dtype ? 2 : 4);
+    if (overlaps(a.ptr_c, cb, args->ptr_b_pp, span(a.batch, args->stride_b_pp_batch, 1, 0, bpp, 1)))
+        return hipErrorInvalidValue;
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    TileArgs t{};
+    fill_common(t, a, a.k);
+    t.sfa_sm = sfa_sm;
+    t.sfa_sk = sfa_sk;
+    t.sfb_sn = a.stride_sfb;
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bpp, true);
+    return run_skinny(SkinnyKind::BSF32_FRAG, t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, workspace,
+                      workspace_bytes, a.k / 128, stream);
+}
+
+size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args) {
+    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
+    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), true)
+        .ws_bytes;
+}
+
+// B' (K-panel, ptr_b, stride_b = 128) -> B'' (ptr_b_pp) on the GPU.
+hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs* args, hipStream_t stream) {
+    if (!args || !args->ptr_b || !args->ptr_b_pp) return hipErrorInvalidValue;
+    const auto& l = *args;
+    if (l.n <= 0 || l.k <= 0 || l.k % 128 || l.batch <= 0 || l.stride_b != 128) return hipErrorInvalidValue;
+    const long long bk = (long long)l.n * l.k, bpp = (long long)frag_bytes(l.n, l.k);
+    if (!bounded_count(bpp, 1, 1, 1) || !aligned(l.ptr_b, 16) || !aligned(l.ptr_b_pp, 16))
+        return hipErrorInvalidValue;
+    if (l.batch > 1 &&
+        (l.stride_b_batch < bk || l.stride_b_pp_batch < bpp || l.stride_b_batch % 16 || l.stride_b_pp_batch % 16))
+        return hipErrorInvalidValue;
+    if (overlaps(l.ptr_b, span(l.batch, l.stride_b_batch, 1, 0, bk, 1), l.ptr_b_pp,
+                 span(l.batch, l.stride_b_pp_batch, 1, 0, bpp, 1)))
+        return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_repack_frag(static_cast<const uint8_t*>(l.ptr_b),
+                                  static_cast<uint8_t*>(const_cast<void*>(l.ptr_b_pp)), l.n, l.k, l.batch,
+                                  l.stride_b_batch, l.stride_b_pp_batch, stream);
 }
 
 // ---------------------------------------------------------------- layouts
@@ -316,6 +499,29 @@ int qgemm_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int groups_k)
                              (size_t)(r % 16) * 4 + (size_t)((g % 8) / 4) * 2 + (size_t)((r % 32) / 16);
             dst[o] = src[(size_t)r * groups_k + g];
         }
+    return 0;
+}
+
+size_t qgemm_ldsbypass_b_bytes(int n, int k) {
+    if (n <= 0 || k <= 0 || k % 128) return 0;
+    return frag_bytes(n, k);
+}
+
+// B'' = [ceil(N/16)][K/128][h][lane][16]: lane = 16q + r holds row 16nb + r,
+// 16-byte chunk q (h = 0) or q + 4 (h = 1) of the 128-byte K-tile; rows
+// past N are zero.
+int qgemm_pack_b_ldsbypass(const uint8_t* b_raw, uint8_t* b_pp, int n, int k) {
+    if (!b_raw || !b_pp || n <= 0 || k <= 0 || k % 128) return (int)hipErrorInvalidValue;
+    const int nk = k / 128, nblk = ceil_div(n, 16);
+    for (int nb = 0; nb < nblk; ++nb)
+        for (int kt = 0; kt < nk; ++kt)
+            for (int h = 0; h < 2; ++h)
+                for (int lane = 0; lane < 64; ++lane) {
+                    const int row = nb * 16 + (lane & 15), c = (lane >> 4) + 4 * h;
+                    uint8_t* d = b_pp + ((((size_t)nb * nk + kt) * 2 + h) * 64 + lane) * 16;
+                    if (row < n) std::memcpy(d, b_raw + (size_t)row * k + (size_t)kt * 128 + (size_t)c * 16, 16);
+                    else std::memset(d, 0, 16);
+                }
     return 0;
 }
 

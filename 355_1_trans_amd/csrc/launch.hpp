@@ -1,5 +1,5 @@
 // Host-side launch wrappers shared between the kernel translation units and
-// the C ABI layer (abi.cpp).  Each wrapper launches exactly one kernel.
+// the C ABI layer (abi.hip).  Each wrapper launches exactly one kernel.
 #pragma once
 #include <hip/hip_runtime.h>
 #include "tile_gemm.hpp"
@@ -13,6 +13,16 @@ hipError_t launch_tile_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wid
 hipError_t launch_tile_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
 hipError_t launch_tile_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 hipError_t launch_tile_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+
+// skinny_*.hip: skinny-M / split-K kernel (mb = M-tile rows / 16, nb = N-tile columns / 16)
+struct SkinnyArgs;
+enum class SkinnyKind : int { MX8_RAW, MX4_RAW, BSF32_KPANEL, BSF32_FRAG };
+hipError_t launch_skinny(SkinnyKind kind, const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s);
+hipError_t launch_skinny_mx8(const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s);
+hipError_t launch_skinny_mx4(const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s);
+// B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
+hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
+                              long long bpp_batch, hipStream_t s);
 
 // probe.hip
 hipError_t launch_probe(int32_t* dev_out, hipStream_t s);

@@ -120,7 +120,11 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
  * the reference's column-major [K/128][M] (stride_sfa = M, BPS host.cc:270)
  * or BASELINE's row-major [M][K/128] (stride_sfa = 1). C bf16/fp32 [M,N].
  * Any M >= 1, N >= 1 (tails are masked), K a multiple of 128.
- * `workspace` (fp32 split-K partials) may be NULL; then no split-K is used. */
+ * `workspace` (fp32 split-K partials) may be NULL; then no split-K is used.
+ * Split-K workspace (every entry with a *_workspace_bytes query): at least
+ * the queried bytes, 256-byte aligned; its first 2048 bytes are counter
+ * words that must be zero before the first call, and every call leaves them
+ * zero.  Calls that share a workspace must be ordered (same stream). */
 hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
                                      size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args);
@@ -155,9 +159,8 @@ size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
  * B [N,K/2] bytes (even k in the low nibble), strides in bytes; SFA [M,K/32],
  * SFB [N,K/32] uint8 row-major. C bf16/fp32. Any M, N >= 1; K a multiple of
  * 256. For skinny M the call splits K across workgroups when `workspace`
- * is large enough (gemm_a4w4_mxfp4_workspace_bytes) and reduces the fp32
- * partials in the same launch; the workspace's counter words must be zero
- * before the first call and every call leaves them zero. */
+ * is given (gemm_a4w4_mxfp4_workspace_bytes; contract as above) and reduces
+ * the fp32 partials in the same launch. */
 hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args);

@@ -45,8 +45,9 @@ def test_probe_known_answers(qgemm, gpu):
 
 
 # ----------------------------------------------------------------- MXFP8
+# M > 256 runs the 256 x 256 tile kernel, smaller M the skinny kernel
 MX8_SHAPES = [(256, 256, 128), (256, 512, 1024), (300, 520, 384), (1, 1536, 7168), (32, 1536, 7168),
-              (513, 272, 256)]
+              (513, 272, 256), (512, 512, 2048), (768, 1024, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", MX8_SHAPES)
@@ -62,7 +63,7 @@ def test_mxfp8(qgemm, gpu, m, n, k, dtype):
 
 def test_mxfp8_k_pattern_scales(qgemm, gpu):
     """Distinct per-K-group scales catch K-group misrouting (MX4 host.cc:185-187)."""
-    m, n, k = 256, 256, 1024
+    m, n, k = 512, 256, 1024
     qa, qb, ea, eb = make_mx8(m, n, k, seed=7)
     ea = np.broadcast_to((120 + (np.arange(k // 32) % 13)).astype(np.uint8), ea.shape).copy()
     ref = O.gemm_mx8(qa, qb, ea, eb)
@@ -73,7 +74,8 @@ def test_mxfp8_k_pattern_scales(qgemm, gpu):
 
 
 # ----------------------------------------------------------------- MXFP4
-MX4_SHAPES = [(256, 256, 256), (256, 512, 1024), (100, 300, 512), (1, 512, 2048), (257, 256, 768)]
+MX4_SHAPES = [(256, 256, 256), (256, 512, 1024), (100, 300, 512), (1, 512, 2048), (257, 256, 768),
+              (512, 512, 2048), (384, 1024, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", MX4_SHAPES)
@@ -111,7 +113,7 @@ def test_blockscale_e8m0(qgemm, gpu, m, n, k, dtype):
 
 # ----------------------------------------------- block-scale, fp32 scales
 BS_SHAPES = [(32, 1536, 7168), (256, 256, 128), (300, 520, 384), (1, 2112, 7168), (16, 4096, 1024),
-             (600, 384, 256)]
+             (600, 384, 256), (512, 768, 1024)]
 
 
 @pytest.mark.parametrize("m,n,k", BS_SHAPES)
