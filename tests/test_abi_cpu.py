@@ -1,0 +1,144 @@
+"""C ABI of libqgemm.so without a GPU: every symbol declared in
+include/qgemm.h is exported, argument validation rejects bad calls before
+any device call, the host layout helpers equal their numpy forms, and the
+split-K workspace queries follow the documented contract."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+ROOT = Path(__file__).resolve().parent.parent
+HIP_INVALID_VALUE = 1
+
+
+def _declared_functions():
+    text = (ROOT / "include" / "qgemm.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol(qgemm):
+    names = _declared_functions()
+    assert len(names) >= 18, names
+    L = ctypes.CDLL(str(qgemm.LIB_PATH))
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(names) <= set(qgemm.EXPORTS), set(names) - set(qgemm.EXPORTS)
+    assert qgemm.lib().qgemm_version().startswith(b"qgemm gfx950")
+
+
+def _kargs(qgemm, m=32, n=256, k=512, **kw):
+    buf = [ctypes.create_string_buffer(1 << 16) for _ in range(5)]
+    base = dict(ptr_a=ctypes.addressof(buf[0]), ptr_b=ctypes.addressof(buf[1]), ptr_c=ctypes.addressof(buf[2]),
+                m=m, n=n, k=k, batch=1, stride_a=k, stride_b=k, stride_c=n, stride_a_batch=m * k,
+                stride_b_batch=n * k, stride_c_batch=m * n, ptr_sfa=ctypes.addressof(buf[3]),
+                ptr_sfb=ctypes.addressof(buf[4]), stride_sfa=k // 32, stride_sfb=k // 32,
+                stride_sfa_batch=m * (k // 32), stride_sfb_batch=n * (k // 32))
+    base.update(kw)
+    a = qgemm.Kargs(**base)
+    a._keep = buf
+    return a
+
+
+@pytest.mark.parametrize("change", [
+    dict(ptr_a=None), dict(ptr_c=None), dict(k=100), dict(m=0), dict(n=-1), dict(batch=0),
+    dict(stride_a=256), dict(stride_c=100), dict(stride_sfa=8), dict(stride_b=520),
+])
+def test_mxfp8_rejects_bad_arguments(qgemm, change):
+    a = _kargs(qgemm, **change)
+    assert qgemm.lib().gemm_a8w8_mxfp8(ctypes.byref(a), 1, None, 0, None) == HIP_INVALID_VALUE
+
+
+def test_rejects_bad_flags_null_args_and_overlap(qgemm):
+    L = qgemm.lib()
+    a = _kargs(qgemm)
+    assert L.gemm_a8w8_mxfp8(None, 1, None, 0, None) == HIP_INVALID_VALUE
+    assert L.gemm_a8w8_mxfp8(ctypes.byref(a), 2, None, 0, None) == HIP_INVALID_VALUE
+    a.ptr_c = a.ptr_a + 64                                   # C overlapping A
+    assert L.gemm_a8w8_mxfp8(ctypes.byref(a), 1, None, 0, None) == HIP_INVALID_VALUE
+    a4 = _kargs(qgemm, k=384, stride_a=192, stride_b=192)    # K % 256 != 0 for fp4
+    assert L.gemm_a4w4_mxfp4(ctypes.byref(a4), 1, None, 0, None) == HIP_INVALID_VALUE
+
+
+def test_blockscale_e8m0_contract(qgemm):
+    """SNAP launcher: M, N multiples of 256, dense strides, tiles in {0, 1}."""
+    L = qgemm.lib()
+    ok = dict(m=256, n=256, k=256, stride_a=256, stride_b=256, stride_c=256, stride_a_batch=65536,
+              stride_b_batch=65536, stride_c_batch=65536, stride_sfa=256, stride_sfb=2, stride_sfa_batch=512,
+              stride_sfb_batch=4)
+    for bad in (dict(m=128), dict(n=384, stride_c=384), dict(stride_sfa=128), dict(k=200)):
+        a = _kargs(qgemm, **{**ok, **bad})
+        assert L.launch_blockscale_bpreshuffle(ctypes.byref(a), 1, 0, None) == HIP_INVALID_VALUE
+    a = _kargs(qgemm, **ok)
+    assert L.launch_blockscale_bpreshuffle(ctypes.byref(a), 1, 2, None) == HIP_INVALID_VALUE
+    assert L.launch_blockscale_bpreshuffle(ctypes.byref(a), 3, 0, None) == HIP_INVALID_VALUE
+
+
+def test_bpreshuffle_requires_kpanel_stride(qgemm):
+    a = _kargs(qgemm, stride_b=512, stride_sfa=32, stride_sfb=4)
+    assert qgemm.lib().gemm_a8w8_blockscale_bpreshuffle(ctypes.byref(a), 1, None, 0, None) == HIP_INVALID_VALUE
+
+
+def test_workspace_queries(qgemm):
+    L = qgemm.lib()
+    # large M runs the 256 x 256 tile kernel: no workspace
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=8192, n=8192, k=8192))) == 0
+    # decode with few 16-column tiles splits K: 2 KB of counters + splitk * M * N fp32 partials
+    for m, n, k in [(1, 1536, 7168), (32, 1536, 7168), (4, 2112, 7168)]:
+        a = _kargs(qgemm, m=m, n=n, k=k)
+        ws = L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(a))
+        assert ws >= 2048 + 2 * m * n * 4 and (ws - 2048) % (m * n * 4) == 0, (m, n, k, ws)
+    # enough N tiles: no split
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=7168, k=16384))) == 0
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(None) == 0
+    # fp4 K-tiles hold 256 elements: K = 16384 gives 64 of them, enough for 16-tile slices
+    assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=1536, k=16384))) > 0
+
+
+# ----------------------------------------------------------------- host layout helpers
+def test_product_layout_helpers_match_numpy(qgemm):
+    L = qgemm.lib()
+    rng = np.random.default_rng(21)
+    b = rng.integers(0, 256, (48, 384), dtype=np.uint8)
+    out = np.empty_like(b)
+    assert L.qgemm_shuffle_b_kpanel(b.ctypes.data, out.ctypes.data, 48, 384) == 0
+    assert np.array_equal(out.reshape(3, 48, 128), b.reshape(48, 3, 128).transpose(1, 0, 2))
+    assert L.qgemm_shuffle_weight_16x16(b.ctypes.data, out.ctypes.data, 48, 384) == 0
+    assert np.array_equal(out, b.reshape(3, 16, 24, 16).transpose(0, 2, 1, 3).reshape(48, 384))
+    e = rng.integers(0, 255, (64, 24), dtype=np.uint8)
+    nbytes = L.qgemm_e8m0_shuffle_bytes(64, 24)
+    eo = np.empty(nbytes, np.uint8)
+    assert L.qgemm_e8m0_shuffle(e.ctypes.data, eo.ctypes.data, 64, 24) == 0
+    assert np.array_equal(eo, e.reshape(2, 2, 16, 3, 2, 4).transpose(0, 3, 5, 2, 4, 1).reshape(-1))
+    assert L.qgemm_shuffle_b_kpanel(b.ctypes.data, out.ctypes.data, 48, 100) == HIP_INVALID_VALUE
+
+
+@pytest.mark.parametrize("n,k", [(48, 256), (37, 384), (16, 128)])
+def test_ldsbypass_host_pack_matches_permutation(qgemm, n, k):
+    """B'' = [ceil(N/16)][K/128][h][lane = 16q + r][16] with chunk q + 4h of row 16nb + r."""
+    b = np.random.default_rng(n * k).integers(0, 256, (n, k), dtype=np.uint8)
+    got = qgemm.ldsbypass_pack_b(torch.from_numpy(b)).numpy()
+    nb = (n + 15) // 16
+    pad = np.zeros((nb * 16, k), np.uint8)
+    pad[:n] = b
+    ref = pad.reshape(nb, 16, k // 128, 2, 4, 16).transpose(0, 2, 3, 4, 1, 5).reshape(-1)
+    assert got.size == qgemm.ldsbypass_b_bytes(n, k) == nb * 16 * k
+    assert np.array_equal(got, ref)
+
+
+def test_python_layout_helpers(qgemm):
+    b = torch.from_numpy(np.random.default_rng(22).integers(0, 256, (32, 256), dtype=np.uint8))
+    assert np.array_equal(qgemm.shuffle_b_kpanel(b).numpy(), O.shuffle_b_kpanel(b.numpy()))
+    assert np.array_equal(qgemm.shuffle_weight_16x16(b).numpy(), O.shuffle_weight_16x16(b.numpy()))
+
+
+def test_no_cpu_fallback(qgemm):
+    a = torch.zeros(16, 128, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    s = torch.zeros(16, 4, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="GPU"):
+        qgemm.gemm_a8w8_mxfp8(a, a, s, s)
