@@ -4,17 +4,25 @@ Default workload (the configuration the headline
 metric is quoted on): MXFP8 TN GEMM, M = N = K = 8192, e4m3 operands with one
 E8M0 scale per 32 K elements, bf16 output.  A "step" is one GEMM launch on
 synthetic N(0,1) data (seed 0) quantized per the BASELINE recipe; inputs are
-resident in HBM before the timed region.
+resident in HBM before the timed region.  Other workloads (--workload) cover
+configs[0] (block-scale FP8 decode, both B layouts), configs[3] (MXFP4
+8192^3) and configs[4] (MXFP4 decode).
+
+Launches go straight through the C ABI with prebuilt argument blocks.  The
+MFMA-bound 8192^3 workloads are timed launch by launch; the HBM-bound decode
+workloads are captured in a HIP graph over rotating copies of the weights
+(more bytes than the 256 MB last-level cache, so B streams from HBM) and the
+replays are timed.  Either way the timing is HIP events on the launch stream.
 
 Prints ONE JSON line with the metric, a roofline block for the GEMM kernel
-(achieved = algorithmic FLOPs / average launch time measured with HIP events
-on the launch stream) and a cpu_baseline block (the CPU oracle's restatement
-of the reference CPU GEMM, timed on a bounded row band on this host).
+(algorithmic FLOPs or bytes per launch / average launch time) and a
+cpu_baseline block (the CPU oracle's restatement of the reference CPU GEMM,
+timed on a bounded row band on this host).
 """
 import argparse
+import ctypes
 import importlib
 import json
-import os
 import re
 import sys
 import time
@@ -26,6 +34,17 @@ sys.path.insert(0, str(ROOT))
 METRIC = "TFLOPS and % of MI355X peak: block-FP8/MXFP8/MXFP4 GEMM at 8192^3 + decode M"
 PEAK_TFLOPS = {"fp8": 5000.0, "fp4": 10100.0}
 HBM_GBPS = 8000.0
+ROTATE_BYTES = 512 << 20
+
+WORKLOADS = {
+    # name: (family, M, N, K, BASELINE config index)
+    "mxfp8_8192": ("mx8", 8192, 8192, 8192, 1),
+    "mxfp4_8192": ("mx4", 8192, 8192, 8192, 3),
+    "bs_fp32_8192": ("bs", 8192, 8192, 8192, 2),
+    "bs_c0": ("bs", 32, 1536, 7168, 0),
+    "ldsbypass_c0": ("lbp", 32, 1536, 7168, 0),
+    "mxfp4_c4": ("mx4", 32, 7168, 16384, 4),
+}
 
 
 def parse():
@@ -33,10 +52,12 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=200)
-    p.add_argument("--workload", default="mxfp8_8192",
-                   choices=["mxfp8_8192", "mxfp4_8192", "bs_fp32_8192", "bs_c0"])
+    p.add_argument("--workload", default="mxfp8_8192", choices=sorted(WORKLOADS))
+    p.add_argument("--m", type=int, default=None, help="override M (decode sweeps)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run only a plain 256 MiB device copy 5 times (PMC byte-counter calibration)")
     return p.parse_args()
 
 
@@ -56,80 +77,153 @@ def main():
               "the multi-GPU sharding plan is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
     import torch
+
+    if args.copy_calibration:
+        # known traffic: 256 MiB read + 256 MiB written per copy launch; the
+        # FETCH_SIZE / WRITE_SIZE counters of these launches give the factors
+        # that turn the counters into bytes
+        x = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": 256 << 20, "bytes_written": 256 << 20,
+                                               "launches": 5}}), flush=True)
+        return
+
     import oracle as O
 
     q = importlib.import_module("355_1_trans_amd")
+    L = q.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
-    w = args.workload
-    if w in ("mxfp8_8192", "mxfp4_8192", "bs_fp32_8192"):
-        M = N = K = 8192
-    else:
-        M, N, K = 32, 1536, 7168
+    fam, M, N, K, cfg = WORKLOADS[args.workload]
+    if args.m:
+        M = args.m
+    hbm_bound = M <= 256
     a = O.randn((M, K), 0, 0)
     b = O.randn((N, K), 0, 1)
+    kg32, kg128 = K // 32, K // 128
 
-    if w == "mxfp8_8192":
-        qa, ea = O.quant_mx8(a)
-        qb, eb = O.quant_mx8(b)
-        A = torch.from_numpy(qa).to(dev).view(torch.float8_e4m3fn)
-        B = torch.from_numpy(qb).to(dev).view(torch.float8_e4m3fn)
-        SA, SB = torch.from_numpy(ea).to(dev), torch.from_numpy(eb).to(dev)
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        step = lambda: q.gemm_a8w8_mxfp8(A, B, SA, SB, out=out)
-        dtype, kind, tag = "fp8", "fp8", "mxfp8_8192"
-        workload = "MXFP8 TN GEMM M=N=K=8192, e4m3 x e4m3, E8M0 per 32 K, bf16 out (BASELINE configs[1])"
-        cpu_fn = lambda rows: O.gemm_mx8(qa[rows], qb, ea[rows], eb)
-    elif w == "mxfp4_8192":
-        qa, ea = O.quant_mx4(a)
-        qb, eb = O.quant_mx4(b)
-        A, B = torch.from_numpy(qa).to(dev), torch.from_numpy(qb).to(dev)
-        SA, SB = torch.from_numpy(ea).to(dev), torch.from_numpy(eb).to(dev)
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        step = lambda: q.gemm_a4w4_mxfp4(A, B, SA, SB, out=out)
-        dtype, kind, tag = "fp4", "fp4", "mxfp4_8192"
-        workload = "MXFP4 A4W4 GEMM M=N=K=8192, e2m1 x e2m1, E8M0 per 32 K, bf16 out (BASELINE configs[3])"
-        cpu_fn = lambda rows: O.gemm_mx4(qa[rows], qb, ea[rows], eb)
+    # quantize once on the host (BASELINE recipe); device copies of the operands
+    if fam == "mx8":
+        qa, sa = O.quant_mx8(a)
+        qb, sb = O.quant_mx8(b)
+    elif fam == "mx4":
+        qa, sa = O.quant_mx4(a)
+        qb, sb = O.quant_mx4(b)
     else:
         qa, sa = O.quant_bs_act(a)
         qb, sb = O.quant_bs_wgt(b)
-        A = torch.from_numpy(qa).to(dev).view(torch.float8_e4m3fn)
-        Bk = q.shuffle_b_kpanel(torch.from_numpy(qb).to(dev)).view(torch.float8_e4m3fn)
-        SA, SB = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        step = lambda: q.gemm_a8w8_bpreshuffle(A, Bk, SA, SB, out=out)
-        dtype, kind, tag = "fp8", "fp8", w
-        workload = (f"block-scale FP8 GEMM M={M} N={N} K={K}, fp32 1x128/128x128 scales, K-panel B, bf16 out "
-                    f"(BASELINE configs[{0 if w == 'bs_c0' else 2}])")
-        cpu_fn = lambda rows: O.gemm_bs_fp32(qa[rows], qb, sa[rows], sb)
-    torch.cuda.synchronize()
+    A = torch.from_numpy(qa).to(dev)
+    SA = torch.from_numpy(sa).to(dev)
+    B0 = torch.from_numpy(qb).to(dev)
+    SB0 = torch.from_numpy(sb).to(dev)
+    if fam == "bs":
+        B0 = q.shuffle_b_kpanel(B0)
+    elif fam == "lbp":
+        B0 = q.ldsbypass_repack(q.shuffle_b_kpanel(B0))
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    b_bytes = B0.numel() * B0.element_size() + SB0.numel() * SB0.element_size()
+    copies = max(2, ROTATE_BYTES // b_bytes + 1) if hbm_bound else 1
+    Bs = [B0] + [B0.clone() for _ in range(copies - 1)]
+    SBs = [SB0] + [SB0.clone() for _ in range(copies - 1)]
 
-    flops = 2.0 * M * N * K
-    for _ in range(args.warmup):
-        step()
+    kb = K // 2 if fam == "mx4" else K
+    calls = []
+    for B, SB in zip(Bs, SBs):
+        if fam in ("mx8", "mx4"):
+            args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, kb, kb, N, M * kb, N * kb, M * N,
+                            SA.data_ptr(), SB.data_ptr(), kg32, kg32, M * kg32, N * kg32)
+            fn = L.gemm_a8w8_mxfp8 if fam == "mx8" else L.gemm_a4w4_mxfp4
+            wq = L.gemm_a8w8_mxfp8_workspace_bytes if fam == "mx8" else L.gemm_a4w4_mxfp4_workspace_bytes
+        elif fam == "bs":
+            args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K, N * K, M * N,
+                            SA.data_ptr(), SB.data_ptr(), 1 if M > 1 else M, kg128, M * kg128, SB.numel())
+            fn, wq = L.gemm_a8w8_blockscale_bpreshuffle, L.gemm_a8w8_blockscale_bpreshuffle_workspace_bytes
+        else:
+            args_ = q.LdsBypassKargs(A.data_ptr(), None, B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K,
+                                     N * K, M * N, SA.data_ptr(), SB.data_ptr(), 1 if M > 1 else M, kg128,
+                                     M * kg128, SB.numel(), B.numel())
+            fn, wq = L.gemm_a8w8_blockscale_ldsbypass, L.gemm_a8w8_blockscale_ldsbypass_workspace_bytes
+        calls.append((fn, args_))
+    ws_bytes = max(1, wq(ctypes.byref(calls[0][1])))
+    ws = torch.zeros((ws_bytes + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+
+    stream = torch.cuda.Stream(dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    def launch(i):
+        fn, ka = calls[i % len(calls)]
+        st = fn(ctypes.byref(ka), 1, ws.data_ptr(), ws.numel(), sptr)
+        if st:
+            raise RuntimeError(f"{fn.__name__} failed: HIP error {st}")
+
+    with torch.cuda.stream(stream):
+        launch(0)
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
+    if hbm_bound:
+        # one graph of exactly `steps` launches over the rotating weight copies;
+        # a warm replay, then the timed replay
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(args.steps):
+                launch(i)
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                launch(i)
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    else:
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                launch(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            for i in range(args.steps):
+                launch(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    launches = args.steps
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+    ms = e0.elapsed_time(e1) / launches
+    flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
 
-    peak = PEAK_TFLOPS[kind]
-    roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(tag)}
+    kind = "fp4" if fam == "mx4" else "fp8"
+    tag = args.workload if args.m is None else f"{args.workload}_m{M}"
+    if hbm_bound:
+        # algorithmic bytes: A, B and both scale arrays read once, C written once
+        alg = (A.numel() * A.element_size() + SA.numel() * SA.element_size() + b_bytes + C.numel() * 2)
+        gbps = alg / (ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_GBPS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_GBPS, 4), "traffic": traffic_from_profiles(tag),
+                    "algorithmic_bytes": alg}
+    else:
+        peak = PEAK_TFLOPS[kind]
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                    "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(tag)}
 
     cpu = None
     if not args.no_cpu:
+        if fam == "mx8":
+            cpu_fn = lambda rows: O.gemm_mx8(qa[rows], qb, sa[rows], sb)
+        elif fam == "mx4":
+            cpu_fn = lambda rows: O.gemm_mx4(qa[rows], qb, sa[rows], sb)
+        else:
+            cpu_fn = lambda rows: O.gemm_bs_fp32(qa[rows], qb, sa[rows], sb)
         # bounded row band of the same GEMM on this host's cores, extrapolated per FLOP
         rows, elapsed = 1, 0.0
         while True:
@@ -144,11 +238,18 @@ def main():
                "sample": f"rows 0..{rows - 1} of the same {M}x{N}x{K} GEMM ({elapsed:.1f} s, extrapolated "
                          f"per FLOP); oracle restatement of the reference CPU gemm_ref, OpenMP"}
 
+    names = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
+             "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
+             "bs": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, K-panel B (bpreshuffle)",
+             "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)"}
     line = {
-        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": launches,
         "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": dtype, "data": "synthetic N(0,1) seed 0, BASELINE quantization recipe",
-        "config": {"workload": workload, "M": M, "N": N, "K": K, "out": "bf16"},
+        "vs_baseline": None, "dtype": kind, "data": "synthetic N(0,1) seed 0, BASELINE quantization recipe",
+        "config": {"workload": f"{names[fam]} M={M} N={N} K={K}, bf16 out (BASELINE configs[{cfg}])",
+                   "M": M, "N": N, "K": K, "out": "bf16",
+                   "timing": ("one HIP graph of the timed launches over %d rotating weight copies" % len(calls))
+                   if hbm_bound else "back-to-back launches"},
         "roofline": roofline, "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 4),
     }
