@@ -118,20 +118,22 @@ bool dma_aligned(const opus_gemm_scale_kargs& a, bool scales_dword) {
 
 // ---------------------------------------------------------------- split-K plan
 // Skinny-M problems (too few 256 x 256 tiles to fill the GPU) run on the
-// skinny kernel.  One CU streams ~45-55 GB/s, so HBM bandwidth needs about
-// 200+ busy CUs (MI355X has 256): the plan takes the widest N tile (64, 32 or
-// 16 columns) that gives at least kMinTiles workgroups, and splits K across
-// workgroups only when 16-column tiles still give fewer, keeping >= 16
+// skinny kernel (one 8-wave workgroup per CU).  One CU streams ~50 GB/s, so
+// HBM bandwidth needs most of the 256 CUs busy: the plan takes the widest N
+// tile (64, 32 or 16 columns) that gives at least kMinTiles workgroups.  When
+// even 16-column tiles give fewer than kSplitBelow, K is split across
+// workgroups -- only up to one round of workgroups (kCUs), keeping >= 16
 // K-tiles per slice and the fp32 partials below a quarter of B's bytes.  The
 // plan depends on the shape only, so the workspace query and the launch
 // always agree.
 constexpr int kCUs = 256;
 constexpr int kMinTiles = 192;
-// Split-K runs only when the grid has fewer than kMinTiles tiles, so its
-// counters fit a fixed block at the start of the workspace; a fixed size
-// keeps the counters of any later call clear of earlier calls' partials.
+constexpr int kSplitBelow = 128;
+// Split-K runs only with fewer than kSplitBelow tiles, so its counters fit a
+// fixed block at the start of the workspace; a fixed size keeps the counters
+// of any later call clear of earlier calls' partials.
 constexpr size_t kCounterBytes = 2 * kCUs * sizeof(unsigned);
-static_assert(kMinTiles <= 2 * kCUs, "counter block too small");
+static_assert(kSplitBelow <= 2 * kCUs, "counter block too small");
 
 struct Plan {
     bool skinny = false;
@@ -153,15 +155,15 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
         if ((long long)p.n_tiles * p.m_tiles * batch >= kMinTiles) break;
     }
     const long long base = (long long)p.n_tiles * p.m_tiles * batch;
-    if (base >= kMinTiles) return p;
-    long long split = (kCUs + base - 1) / base;
+    if (base >= kSplitBelow) return p;
+    long long split = kCUs / base;
     split = std::min<long long>(split, k_tiles / 16);
     split = std::min<long long>(split, b_bytes / (16LL * m * n));
     if (split <= 1) return p;
     p.kt_per_split = ceil_div(k_tiles, (int)split);
     p.splitk = ceil_div(k_tiles, p.kt_per_split);
     if (p.splitk > 1) {
-        p.ctr_bytes = kCounterBytes;    // base < kMinTiles counters
+        p.ctr_bytes = kCounterBytes;    // base < kSplitBelow counters
         p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
     }
     return p;

@@ -40,6 +40,15 @@ __device__ __forceinline__ void dma4(const void* gsrc, QG_LDS void* lds_base) {
     __builtin_amdgcn_global_load_lds(gsrc, lds_base, 4, 0, 0);
 }
 
+// Buffer -> LDS DMA (buffer_load_dwordx4 ... lds): lane L writes its 16
+// bytes at lds_base + 16L.  A lane whose offset falls outside the buffer
+// descriptor's range writes zeros and reads no memory.  (Kept out of lambdas:
+// the host pass of a kernel drops the kernel's launch stub when this builtin
+// appears in a lambda body.)
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, QG_LDS void* lds_base, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 16, voff, soff, 0, 0);
+}
+
 // fp32 -> bf16 with round-to-nearest-even (the rounding the reference
 // validates against, SNAP host.cc:185-193): v_cvt_pk_bf16_f32 converts two
 // values per instruction in hardware.

@@ -1,33 +1,50 @@
 // Skinny-M / split-K GEMM for gfx950 (decode shapes and the LDS-bypass path).
 //
-// Decode GEMMs stream B once and are HBM-bound.  On MI355X one CU sustains
-// only ~45-55 GB/s of streaming reads (8 waves, >= 64 KB in flight), so
-// reaching HBM bandwidth needs work on every one of the 256 CUs: the host
-// picks the N-tile width (16, 32 or 64 columns: NB blocks of 16) so that the
-// grid has about one workgroup per CU, and splits K across workgroups only
-// when even 16-column tiles leave CUs idle.
+// Decode GEMMs stream B once and are HBM-bound.  Two MI355X facts shape the
+// kernel (measured with streaming-read microbenchmarks):
+//  * one CU sustains only ~50 GB/s of streaming reads (8 waves, >= 64 KB in
+//    flight), so HBM bandwidth needs ~150-200 CUs streaming at once;
+//  * that per-CU rate is a rate of cache-line requests: a wave load that
+//    touches 16 half lines (the scaled-MFMA fragment order, lane 16q+r =
+//    row r) moves half the bytes of one that touches 8 whole lines.
+// So the host picks the N-tile width (16, 32 or 64 columns: NB blocks of 16)
+// to put work on as many CUs as possible in one round, splitting K across
+// workgroups only when 16-column tiles leave too many CUs idle, and B is
+// read in whole 128-byte lines:
+//  * row-major / K-panel B: buffer -> LDS DMA in whole-line order (8 rows x
+//    128 B per instruction), into a per-wave LDS ring, then ds_read_b128
+//    into MFMA fragments.  The 16-byte chunks of a row are XOR-swizzled on
+//    the way in (the DMA lane picks which chunk it fetches), which makes the
+//    fragment reads bank-conflict free;
+//  * B'' (LDS-bypass entry): already in fragment order and 1 KB contiguous
+//    per wave load, so it goes straight into registers.
+// A fragments (small, L2-resident) and scales are loaded into registers.
 //
 // A workgroup (8 wave64) owns NB*16 output columns, MB*16 rows and a slice
-// of the K-tiles (128 bytes of K each).  B is streamed straight from global
-// memory into MFMA fragments, and A fragments come from global memory too
-// (the small A operand is L2-resident).  Wave w takes K-tiles w, w+8, ... of
-// the slice; loads run D K-tiles ahead of the MFMAs in a register ring.
-// The eight waves' partial sums meet in LDS and are added in a fixed order
-// (the result does not depend on timing).  With split-K > 1 each workgroup
-// stores its fp32 partial tile into the caller's workspace and the last
-// workgroup of a tile (atomic counter) sums the partials in slice order,
-// rounds and re-arms the counter, all in the same launch.
+// of the K-tiles (128 bytes of K each).  Wave w takes K-tiles w, w+8, ... of
+// the slice; its loads run D K-tiles ahead of the MFMAs.  All loads are raw
+// buffer loads with a loop-invariant per-lane offset and a wave-uniform
+// K-tile offset; a ring slot past the wave's last K-tile loads through a
+// zero-range descriptor (zeros, no memory traffic), so the loads stay
+// unconditional and the compiler's wait counts stay exact.  The eight
+// waves' partial sums meet in LDS and are added in a fixed order (the result
+// does not depend on timing).  With split-K > 1 each workgroup stores its
+// fp32 partial tile into the caller's workspace and the last workgroup of a
+// tile (atomic counter) sums the partials in slice order, rounds and re-arms
+// the counter, all in the same launch.
 //
 // Register layout of the scaled MFMA (pinned by the layout probes): see
 // tile_gemm.hpp.  srcA = B fragment, srcB = A fragment; the accumulator of
 // lane L = 16q + r holds C[m = r][n = 4q .. 4q+3] of a 16 x 16 block.
 //
-// B layouts: RAW [N][Kbytes]; KPANEL [K/128][N][128]; W16 shuffle_weight(16,16);
-// FRAG (this library's B'' for the LDS-bypass entry): for every 16-row block
-// nb and K-tile kt, 2048 contiguous bytes [nb][kt][h][lane][16] where lane L
-// = 16q + r holds row 16nb + r and h selects the lane's first or second
-// 16-byte operand chunk, so each fragment load is one coalesced 1 KB read.
+// B layouts: RAW [N][Kbytes]; KPANEL [K/128][N][128]; FRAG (this library's
+// B'' for the LDS-bypass entry): for every 16-row block nb and K-tile kt,
+// 2048 contiguous bytes [nb][kt][h][lane][16] where lane L = 16q + r holds
+// row 16nb + r and h selects the lane's first or second 16-byte operand
+// chunk.
 #pragma once
+#include <utility>
+
 #include "tile_gemm.hpp"
 
 namespace qg {
@@ -48,12 +65,24 @@ struct SkinnyArgs {
 // Grid x = ceil(n_tiles / 8) * 8 * m_tiles; ids past n_tiles exit at once.
 __host__ __device__ inline int skinny_grid_x(int n_tiles, int m_tiles) { return (n_tiles + 7) / 8 * 8 * m_tiles; }
 
-// K-tiles in flight per wave: the register ring holds D stages of
-// 8*(MB+NB) operand dwords (+ scales) next to 4*MB*NB accumulators, within
-// the 256 VGPRs a wave gets at two waves per SIMD.
-__host__ __device__ constexpr int skinny_depth(int mb, int nb) {
-    const int d = (200 - 4 * mb * nb) / (8 * (mb + nb) + 4);
+// K-tiles in flight per wave.  Register budget: D stages of A fragments
+// (8*MB dwords + scales) next to 4*MB*NB accumulators (and, without the LDS
+// ring, 8*NB dwords of B per stage).  LDS budget (LDS ring): 8 waves x D
+// stages x NB*2 KB <= 152 KB.
+__host__ __device__ constexpr int skinny_depth(int mb, int nb, bool lds_b) {
+    int d = lds_b ? (150 - 8 * mb * nb) / (8 * mb + 6) : (150 - 4 * mb * nb) / (8 * (mb + nb) + 6);
+    if (lds_b && d > 152 * 1024 / (kSkinnyWaves * nb * 2048)) d = 152 * 1024 / (kSkinnyWaves * nb * 2048);
     return d > 8 ? 8 : (d < 2 ? 2 : d);
+}
+
+template <int N, class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
 template <int FMT, ScaleKind SK, BLay BL, int MB, int NB, bool BF16>
@@ -62,16 +91,55 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     static_assert(MB == 1 || MB == 2 || MB == 4, "16, 32 or 64 rows per M-tile");
     static_assert(NB == 1 || NB == 2 || NB == 4, "16, 32 or 64 columns per N-tile");
     static_assert(SK == ScaleKind::MX || SK == ScaleKind::BSF32, "E8M0 or fp32 block scales");
+    static_assert(BL == BLay::RAW || BL == BLay::KPANEL || BL == kBFrag, "row-major, K-panel or B''");
     constexpr bool FP4 = (FMT == kFmtFp4);
     constexpr bool MX = (SK == ScaleKind::MX);
     constexpr bool VALU_SCALE = (SK == ScaleKind::BSF32);
-    constexpr int D = skinny_depth(MB, NB);
+    constexpr bool LDS_B = (BL != kBFrag);
+    constexpr int D = skinny_depth(MB, NB, LDS_B);
     constexpr int ROWS = MB * 16, COLS = NB * 16;
-    constexpr int RP = COLS + 4;           // LDS row pitch in floats (breaks the bank period)
+    constexpr int RP = COLS + 4;           // reduction row pitch in floats (breaks the bank period)
     constexpr int REGION = ROWS * RP;
     constexpr int NT = W * 64;
-    __shared__ __attribute__((aligned(16))) float red[4 * REGION];
+    constexpr int SLOT = NB * 2048;        // one wave's B bytes per K-tile
+    constexpr int RING = LDS_B ? W * SLOT : 16;
+    // one LDS object per ring stage: the compiler tracks DMA completion per
+    // object, so reading stage d waits only for stage d's DMAs
+    __shared__ __attribute__((aligned(16))) uint8_t ring0[RING];
+    __shared__ __attribute__((aligned(16))) uint8_t ring1[D > 1 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t ring2[D > 2 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t ring3[D > 3 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t ring4[D > 4 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t ring5[D > 5 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t ring6[D > 6 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t ring7[D > 7 ? RING : 16];
+    // two reduction regions; with the LDS ring they reuse ring0 once every
+    // wave has left the K loop
+    constexpr int RED_BYTES = 2 * REGION * 4;
+    static_assert(!LDS_B || RED_BYTES <= RING, "reduction regions fit in ring0");
+    __shared__ __attribute__((aligned(16))) float red_own[LDS_B ? 4 : 2 * REGION];
     __shared__ int last_flag;
+    float* const red = LDS_B ? reinterpret_cast<float*>(ring0) : red_own;
+    // LDS-typed views, formed here in the kernel body (not inside lambdas)
+    QG_LDS uint8_t* const lr0 = (QG_LDS uint8_t*)ring0;
+    QG_LDS uint8_t* const lr1 = (QG_LDS uint8_t*)ring1;
+    QG_LDS uint8_t* const lr2 = (QG_LDS uint8_t*)ring2;
+    QG_LDS uint8_t* const lr3 = (QG_LDS uint8_t*)ring3;
+    QG_LDS uint8_t* const lr4 = (QG_LDS uint8_t*)ring4;
+    QG_LDS uint8_t* const lr5 = (QG_LDS uint8_t*)ring5;
+    QG_LDS uint8_t* const lr6 = (QG_LDS uint8_t*)ring6;
+    QG_LDS uint8_t* const lr7 = (QG_LDS uint8_t*)ring7;
+    auto ring = [&](auto dc) -> QG_LDS uint8_t* {
+        constexpr int d = decltype(dc)::value;
+        if constexpr (d == 0) return lr0;
+        else if constexpr (d == 1) return lr1;
+        else if constexpr (d == 2) return lr2;
+        else if constexpr (d == 3) return lr3;
+        else if constexpr (d == 4) return lr4;
+        else if constexpr (d == 5) return lr5;
+        else if constexpr (d == 6) return lr6;
+        else return lr7;
+    };
 
     const TileArgs& p = sp.t;
     const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
@@ -95,83 +163,80 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     const uint8_t* SFA = p.sfa + bz * p.sfa_batch * (VALU_SCALE ? 4 : 1);
     const uint8_t* SFB = p.sfb + bz * p.sfb_batch * (VALU_SCALE ? 4 : 1);
 
-    // ---- per-lane sources (32-bit offsets: the host bounds every operand below 2^31 bytes) ----
-    const int c0 = FP4 ? 2 * q : q;            // first 16-byte chunk of the lane
+    // ---- loop-invariant per-lane byte offsets (the host bounds every operand below 2^31 bytes) ----
+    const int c0 = FP4 ? 2 * q : q;            // first 16-byte chunk of the lane's fragment
     const int c1 = FP4 ? 2 * q + 1 : q + 4;    // second chunk
-    int arow[MB], sa_base[MB];
+    int aoff[MB][2], sa_voff[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
         const int m = min(m0 + i * 16 + l16, M - 1);
-        arow[i] = m * LDA;
-        if constexpr (MX) sa_base[i] = m * SFA_SM + (FP4 ? 2 * q : q);
-        else sa_base[i] = m * SFA_SM;
+        aoff[i][0] = m * LDA + c0 * 16;
+        aoff[i][1] = m * LDA + c1 * 16;
+        sa_voff[i] = MX ? m * SFA_SM + (FP4 ? 2 * q : q) : m * SFA_SM * 4;
     }
-    int bsrc[NB], sb_base[NB];
+    int boff[NB][2], sb_voff[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const int n = min(n0 + j * 16 + l16, N - 1);
-        if constexpr (BL == BLay::RAW) bsrc[j] = n * LDB;
-        else if constexpr (BL == BLay::KPANEL) bsrc[j] = n * BKB;
-        else if constexpr (BL == BLay::W16) bsrc[j] = (n >> 4) * 16 * KB + (n & 15) * 16;
-        else bsrc[j] = (n >> 4) * nk * 2048 + L * 16;
-        if constexpr (MX) sb_base[j] = n * SFB_SN + (FP4 ? 2 * q : q);
-        else sb_base[j] = (n >> 7) * SFB_SN;   // a tile never crosses a 128-column scale block
-    }
-    // Operands are read with raw buffer loads: per-lane byte offsets that do
-    // not change along K (VGPRs) plus a wave-uniform K-tile offset (SGPR).  A
-    // ring slot past the wave's last K-tile loads through a zero-range
-    // descriptor, which the hardware answers with zeros and no memory
-    // traffic; the loads stay unconditional, so the compiler's wait counts
-    // stay exact (a load inside a branch makes it wait for every
-    // outstanding load).
-    int boff[NB][2];               // B chunk h of block j at K-tile 0
+        sb_voff[j] = MX ? n * SFB_SN + (FP4 ? 2 * q : q) : ((n0 >> 7) * SFB_SN) * 4;   // a tile never crosses a 128-column scale block
+        if constexpr (LDS_B) {
+            // DMA instruction h of block j moves rows 8h .. 8h+7 in whole
+            // lines: lane L fetches row R = 8h + L/8, logical chunk
+            // (L % 8) ^ swz(R), landing at physical chunk L % 8 of row R
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if constexpr (BL == kBFrag) boff[j][h] = bsrc[j] + h * 1024;
-            else if constexpr (BL == BLay::W16) boff[j][h] = bsrc[j] + (h ? c1 : c0) * 256;
-            else boff[j][h] = bsrc[j] + (h ? c1 : c0) * 16;
+            for (int h = 0; h < 2; ++h) {
+                const int R = 8 * h + (L >> 3);
+                const int row = min(n0 + j * 16 + R, N - 1);
+                const int c = (L & 7) ^ swz<FP4>(R);
+                boff[j][h] = (BL == BLay::RAW ? row * LDB : row * BKB) + c * 16;
+            }
+        } else {
+            const int base = (n >> 4) * nk * 2048 + L * 16;
+            boff[j][0] = base;
+            boff[j][1] = base + 1024;
         }
+    }
     // bytes between consecutive K-tiles of B, A, and the scale arrays
     const int b_kstep = (BL == BLay::KPANEL) ? N * BKB : ((BL == BLay::RAW) ? BKB : 2048);
     const int s_kstep = MX ? (FP4 ? 8 : 4) : 4;
     const int sa_kstep = MX ? s_kstep : SFA_SK * 4;
+    // fragment-read offsets inside a wave's ring slot: row l16, chunks c0 / c1
+    const int frag0 = l16 * BKB + ((c0 ^ swz<FP4>(l16)) * 16);
+    const int frag1 = l16 * BKB + ((c1 ^ swz<FP4>(l16)) * 16);
+
     auto rsrc = [](const void* base, bool valid) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, valid ? 0x7FFFFFFF : 0, 0x00020000);
     };
     auto ld16 = [](__amdgpu_buffer_rsrc_t r, int voff, int soff) -> i32x4 {
         return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
     };
-    int sa_voff[MB], sb_voff[NB];
-#pragma unroll
-    for (int i = 0; i < MB; ++i) sa_voff[i] = MX ? sa_base[i] : sa_base[i] * 4;
-#pragma unroll
-    for (int j = 0; j < NB; ++j) sb_voff[j] = MX ? sb_base[j] : sb_base[j] * 4;
+    auto cat8 = [](i32x4 lo, i32x4 hi) { return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}; };
 
     struct Stage {
         i32x8 a[MB];
-        i32x8 b[NB];
+        i32x8 b[LDS_B ? 1 : NB];
         int sa[MB];
         int sb[NB];
         float fa[MB];
         float fb;
     };
-    auto load = [&](Stage& s, int kt, bool valid) {
+    auto load = [&](auto dc, Stage& s, int kt, bool valid) {
         const __amdgpu_buffer_rsrc_t rB = rsrc(B, valid), rA = rsrc(A, valid);
         const __amdgpu_buffer_rsrc_t rSA = rsrc(SFA, valid), rSB = rsrc(SFB, valid);
+        if constexpr (LDS_B) {
+            QG_LDS uint8_t* dst = ring(dc) + w * SLOT;
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const i32x4 lo = ld16(rB, boff[j][0], kt * b_kstep);
-            const i32x4 hi = ld16(rB, boff[j][1], kt * b_kstep);
-            s.b[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    dma16_buf(rB, dst + j * 2048 + h * 1024, boff[j][h], kt * b_kstep);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                s.b[j] = cat8(ld16(rB, boff[j][0], kt * b_kstep), ld16(rB, boff[j][1], kt * b_kstep));
         }
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
-            const i32x4 lo = ld16(rA, arow[i] + c0 * 16, kt * BKB);
-            const i32x4 hi = ld16(rA, arow[i] + c1 * 16, kt * BKB);
-            s.a[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+        for (int i = 0; i < MB; ++i) s.a[i] = cat8(ld16(rA, aoff[i][0], kt * BKB), ld16(rA, aoff[i][1], kt * BKB));
         if constexpr (MX) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
@@ -199,31 +264,39 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
         for (int j = 0; j < NB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int unit = p.unit_scale;
 
-    auto compute = [&](const Stage& s) {
+    auto mma = [&](int i, int j, const Stage& s, const i32x8& bf) {
+        if constexpr (FP4) {
+            const i32x8 b0 = i32x8{bf[0], bf[1], bf[2], bf[3], 0, 0, 0, 0};
+            const i32x8 b1 = i32x8{bf[4], bf[5], bf[6], bf[7], 0, 0, 0, 0};
+            const i32x8 a0 = i32x8{s.a[i][0], s.a[i][1], s.a[i][2], s.a[i][3], 0, 0, 0, 0};
+            const i32x8 a1 = i32x8{s.a[i][4], s.a[i][5], s.a[i][6], s.a[i][7], 0, 0, 0, 0};
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b0, a0, acc[i][j], kFmtFp4, kFmtFp4, 0,
+                                                                         s.sb[j], 0, s.sa[i]);
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b1, a1, acc[i][j], kFmtFp4, kFmtFp4, 1,
+                                                                         s.sb[j], 1, s.sa[i]);
+        } else if constexpr (VALU_SCALE) {
+            const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                bf, s.a[i], f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, unit, 0, unit);
+            const float sc = s.fa[i] * s.fb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(part[r], sc, acc[i][j][r]);
+        } else {
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, s.a[i], acc[i][j], kFmtFp8, kFmtFp8, 0,
+                                                                         s.sb[j], 0, s.sa[i]);
+        }
+    };
+    auto compute = [&](auto dc, const Stage& s) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-#pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                if constexpr (FP4) {
-                    const i32x8 b0 = i32x8{s.b[j][0], s.b[j][1], s.b[j][2], s.b[j][3], 0, 0, 0, 0};
-                    const i32x8 b1 = i32x8{s.b[j][4], s.b[j][5], s.b[j][6], s.b[j][7], 0, 0, 0, 0};
-                    const i32x8 a0 = i32x8{s.a[i][0], s.a[i][1], s.a[i][2], s.a[i][3], 0, 0, 0, 0};
-                    const i32x8 a1 = i32x8{s.a[i][4], s.a[i][5], s.a[i][6], s.a[i][7], 0, 0, 0, 0};
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        b0, a0, acc[i][j], kFmtFp4, kFmtFp4, 0, s.sb[j], 0, s.sa[i]);
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        b1, a1, acc[i][j], kFmtFp4, kFmtFp4, 1, s.sb[j], 1, s.sa[i]);
-                } else if constexpr (VALU_SCALE) {
-                    const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        s.b[j], s.a[i], f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, unit, 0, unit);
-                    const float sc = s.fa[i] * s.fb;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(part[r], sc, acc[i][j][r]);
-                } else {
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        s.b[j], s.a[i], acc[i][j], kFmtFp8, kFmtFp8, 0, s.sb[j], 0, s.sa[i]);
-                }
+            i32x8 bf;
+            if constexpr (LDS_B) {
+                const QG_LDS uint8_t* src = ring(dc) + w * SLOT + j * 2048;
+                bf = cat8(*(const QG_LDS i32x4*)(src + frag0), *(const QG_LDS i32x4*)(src + frag1));
+            } else {
+                bf = s.b[j];
             }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) mma(i, j, s, bf);
         }
     };
 
@@ -232,24 +305,27 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     const int ntw = (kt_end - kfirst + W - 1) / W;     // K-tiles of this wave
     if (ntw > 0) {
         Stage st[D];
-#pragma unroll
-        for (int d = 0; d < D; ++d) load(st[d], kfirst + W * d, d < ntw);
+        static_for<D>([&](auto dc) {
+            constexpr int d = decltype(dc)::value;
+            load(dc, st[d], kfirst + W * d, d < ntw);
+        });
         int i = 0;
         for (; i + D <= ntw; i += D) {
-#pragma unroll
-            for (int d = 0; d < D; ++d) {
-                compute(st[d]);
-                load(st[d], kfirst + W * (i + d + D), i + d + D < ntw);
+            static_for<D>([&](auto dc) {
+                constexpr int d = decltype(dc)::value;
+                compute(dc, st[d]);
+                load(dc, st[d], kfirst + W * (i + d + D), i + d + D < ntw);
                 __builtin_amdgcn_sched_barrier(0);   // keep the ring order
-            }
+            });
         }
-#pragma unroll
-        for (int d = 0; d < D - 1; ++d)
-            if (d < ntw - i) compute(st[d]);
+        static_for<D - 1>([&](auto dc) {
+            constexpr int d = decltype(dc)::value;
+            if (d < ntw - i) compute(dc, st[d]);
+        });
     }
 
     // ---- reduce the eight waves in LDS, in a fixed order:
-    // region r (r < 4) = acc(wave r + 4) + acc(wave r); tile = sum of regions 0..3
+    // region r (r < 2) = acc(6+r) + acc(4+r) + acc(2+r) + acc(r); tile = region 0 + region 1
     auto put = [&](int region, bool add) {
 #pragma unroll
         for (int i = 0; i < MB; ++i)
@@ -266,18 +342,21 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
                 }
             }
     };
-    if (w >= 4) put(w - 4, false);
+    wait_vmcnt<0>();                          // ring slots past the last K-tile still receive zeros
+    __syncthreads();                          // every wave has left the K loop (ring0 becomes red)
+    if (w >= 6) put(w - 6, false);
     __syncthreads();
-    if (w < 4) put(w, true);
+    if (w >= 4 && w < 6) put(w - 4, true);
+    __syncthreads();
+    if (w >= 2 && w < 4) put(w - 2, true);
+    __syncthreads();
+    if (w < 2) put(w, true);
     __syncthreads();
     auto tile_sum = [&](int e) -> f32x4 {    // e = row * COLS + col, col % 4 == 0
         const int o = (e / COLS) * RP + e % COLS;
         f32x4 v = *(const f32x4*)&red[o];
-#pragma unroll
-        for (int r2 = 1; r2 < 4; ++r2) {
-            const f32x4 u = *(const f32x4*)&red[r2 * REGION + o];
-            for (int r = 0; r < 4; ++r) v[r] += u[r];
-        }
+        const f32x4 u = *(const f32x4*)&red[REGION + o];
+        for (int r = 0; r < 4; ++r) v[r] += u[r];
         return v;
     };
 
