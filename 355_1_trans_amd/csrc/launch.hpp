@@ -14,6 +14,12 @@ hipError_t launch_tile_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wid
 hipError_t launch_tile_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 hipError_t launch_tile_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 
+// kernels_tile32.hip: the same tiles on the 32x32x64 scaled MFMA
+hipError_t launch_tile32_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
+hipError_t launch_tile32_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
+hipError_t launch_tile32_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+hipError_t launch_tile32_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+
 // skinny_*.hip: skinny-M / split-K kernel (mb = M-tile rows / 16, nb = N-tile columns / 16)
 struct SkinnyArgs;
 enum class SkinnyKind : int { MX8_RAW, MX4_RAW, BSF32_KPANEL, BSF32_FRAG };
@@ -26,6 +32,6 @@ hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int
 
 // probe.hip
 hipError_t launch_probe(int32_t* dev_out, hipStream_t s);
-constexpr int kProbeWords = 2096;
+constexpr int kProbeWords = 8264;
 
 }  // namespace qg

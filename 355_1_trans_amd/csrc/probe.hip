@@ -20,6 +20,19 @@
 //               belongs to (X has that single 1.0, Y is all 1.0, scale_a of
 //               lane group q is 2^q, so D[0][0] = 2^block).
 //   [2080,2096) same for fp4, dwords 0..3.
+// v_mfma_scale_f32_32x32x64_f8f6f4 (64 lanes x 16 accumulator registers per
+// section, out[base + lane*16 + reg]); every value is log2(D / 32), -1 for 0:
+//   [2096,3120) fp8: X = 1.0 on lanes 0..31 only, scale_a of lane t = 2^t,
+//               Y = 1.0 everywhere -> the srcA lane whose row lands in the slot
+//   [3120,4144) same with X on lanes 32..63 (scale_a of lane t = 2^(t-32))
+//   [4144,5168) fp8: Y = 1.0 on lanes 0..31 only, scale_b 2^t -> srcB lane
+//   [5168,6192) same with Y on lanes 32..63
+//   [6192,7216) fp4 version of [2096,3120)
+//   [7216,8240) fp4 version of [4144,5168)
+//   [8240,8256) fp8 K-block map: word 8*g0 + d0 = log2 of the scale applied
+//               to byte 0 of dword d0 of lane group g0 (lane 32*g0, row 0)
+//               when lane group g's scale is 2^g
+//   [8256,8264) fp4 K-block map, dwords 0..3.
 #include "launch.hpp"
 
 namespace qg {
@@ -100,6 +113,69 @@ __global__ __launch_bounds__(64) void probe_kernel(int32_t* out, int s127) {
     for (int r = 0; r < 4; ++r) out[1792 + L * 4 + r] = v[r];
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ int log2_or_neg(float v, int bias) {
+    return v == 0.f ? -1 : (int)((__builtin_bit_cast(uint32_t, v) >> 23) & 255) - 127 - bias;
+}
+
+// 32x32x64 probes (word map in the header comment).
+__global__ __launch_bounds__(64) void probe32_kernel(int32_t* out, int s127) {
+    const int L = threadIdx.x;
+    f32x16 z;
+    for (int r = 0; r < 16; ++r) z[r] = 0.f;
+    const int ones8 = 0x38383838, ones4 = 0x22222222;
+    i32x8 all8, all4, none;
+    for (int i = 0; i < 8; ++i) {
+        all8[i] = ones8;
+        all4[i] = i < 4 ? ones4 : 0;
+        none[i] = 0;
+    }
+    const int sc = s127 + (L & 31);
+    for (int half = 0; half < 2; ++half) {
+        const bool mine = (L >> 5) == half;
+        const f32x16 da = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(mine ? all8 : none, all8, z, kFmtFp8,
+                                                                           kFmtFp8, 0, sc, 0, s127);
+        const f32x16 db = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(all8, mine ? all8 : none, z, kFmtFp8,
+                                                                           kFmtFp8, 0, s127, 0, sc);
+        for (int r = 0; r < 16; ++r) {
+            out[2096 + half * 1024 + L * 16 + r] = log2_or_neg(da[r], 5);
+            out[4144 + half * 1024 + L * 16 + r] = log2_or_neg(db[r], 5);
+        }
+    }
+    {
+        const bool mine = L < 32;
+        const f32x16 da = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(mine ? all4 : none, all4, z, kFmtFp4,
+                                                                           kFmtFp4, 0, sc, 0, s127);
+        const f32x16 db = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(all4, mine ? all4 : none, z, kFmtFp4,
+                                                                           kFmtFp4, 0, s127, 0, sc);
+        for (int r = 0; r < 16; ++r) {
+            out[6192 + L * 16 + r] = log2_or_neg(da[r], 5);
+            out[7216 + L * 16 + r] = log2_or_neg(db[r], 5);
+        }
+    }
+}
+
+// K-block map of the 32x32x64 scale: one launch per probed element.
+__global__ __launch_bounds__(64) void probe32_kblock_kernel(int32_t* out, int s127, int t) {
+    const int L = threadIdx.x;
+    const bool fp4 = t >= 16;
+    const int g0 = fp4 ? (t - 16) / 4 : t / 8;
+    const int d0 = fp4 ? (t - 16) % 4 : t % 8;
+    f32x16 z;
+    for (int r = 0; r < 16; ++r) z[r] = 0.f;
+    i32x8 X, Y;
+    for (int i = 0; i < 8; ++i) {
+        X[i] = 0;
+        Y[i] = (fp4 && i >= 4) ? 0 : (fp4 ? 0x22222222 : 0x38383838);
+    }
+    if (L == 32 * g0) X[d0] = fp4 ? 0x2 : 0x38;
+    const int sc = s127 + (L >> 5);
+    const f32x16 d = fp4 ? __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(X, Y, z, kFmtFp4, kFmtFp4, 0, sc, 0, s127)
+                         : __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(X, Y, z, kFmtFp8, kFmtFp8, 0, sc, 0, s127);
+    if (L == 0) out[8240 + t] = log2_or_neg(d[0], 0);
+}
+
 }  // namespace
 
 hipError_t launch_probe(int32_t* dev_out, hipStream_t s) {
@@ -107,7 +183,14 @@ hipError_t launch_probe(int32_t* dev_out, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     probe_kernel<<<1, 64, 0, s>>>(dev_out, 127);
-    return hipGetLastError();
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    probe32_kernel<<<1, 64, 0, s>>>(dev_out, 127);
+    for (int t = 0; t < 24 && e == hipSuccess; ++t) {
+        probe32_kblock_kernel<<<1, 64, 0, s>>>(dev_out, 127, t);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 }  // namespace qg

@@ -43,6 +43,22 @@ def test_probe_known_answers(qgemm, gpu):
     # fp4: dwords 0-3 of lane group q carry K [32q, 32q+32) -> block q
     assert np.array_equal(w[2080:2096], 2 ** (np.arange(16) // 4)), w[2080:2096]
 
+    # 32x32x64: accumulator register r of lane L holds D[i][j] with srcA row
+    # i = 8*(r//4) + 4*(L//32) + r%4 and srcB row j = L%32; srcA / srcB lanes
+    # t and t+32 feed the same row (two halves of K)
+    r = np.arange(16)[None, :]
+    lane = np.arange(64)[:, None]
+    rows_a = np.broadcast_to(8 * (r // 4) + 4 * (lane // 32) + r % 4, (64, 16))
+    rows_b = np.broadcast_to(lane % 32, (64, 16))
+    for base, expect in [(2096, rows_a), (3120, rows_a), (4144, rows_b), (5168, rows_b),
+                         (6192, rows_a), (7216, rows_b)]:
+        got = w[base:base + 1024].reshape(64, 16)
+        assert np.array_equal(got, expect), f"32x32x64 map at word {base}:\n{got}"
+    # scale blocks of K=64: fp8 dwords 0-3 of either lane group are block 0
+    # (lane group 0's scale), dwords 4-7 block 1; fp4 lane group g is block g
+    assert w[8240:8256].tolist() == [0, 0, 0, 0, 1, 1, 1, 1] * 2, w[8240:8256]
+    assert w[8256:8264].tolist() == [0, 0, 0, 0, 1, 1, 1, 1], w[8256:8264]
+
 
 # ----------------------------------------------------------------- MXFP8
 # M > 256 runs the 256 x 256 tile kernel, smaller M the skinny kernel
