@@ -312,7 +312,7 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
-    return qg::launch_tile_mx8_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
+    return qg::launch_wide_mx8_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
 }
 
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
@@ -375,7 +375,7 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
     fill_common(t, a, a.k);
     t.sfa_sk = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
-    return qg::launch_tile_bs8_w16(t, a.batch, output_bf16 == 1, stream);
+    return qg::launch_wide_bs8_w16(t, a.batch, output_bf16 == 1, stream);
 }
 
 // ------------------------------------------------ block-scale FP8, fp32 scales

@@ -48,6 +48,9 @@ __device__ __forceinline__ void dma4(const void* gsrc, QG_LDS void* lds_base) {
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, QG_LDS void* lds_base, int voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 16, voff, soff, 0, 0);
 }
+__device__ __forceinline__ void dma4_buf(__amdgpu_buffer_rsrc_t r, QG_LDS void* lds_base, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 4, voff, soff, 0, 0);
+}
 
 // fp32 -> bf16 with round-to-nearest-even (the rounding the reference
 // validates against, SNAP host.cc:185-193): v_cvt_pk_bf16_f32 converts two

@@ -143,7 +143,11 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
     const int q = L >> 4, l16 = L & 15;
 
     const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
-    const uint8_t* B = p.b + bz * p.b_batch;
+    // B rebased to the tile's first column, so per-lane DMA offsets stay
+    // within 32 bits (256 rows of one K-tile, or one K-panel)
+    const uint8_t* B = p.b + bz * p.b_batch +
+                       (BL == BLay::RAW ? (long long)n0 * LDB
+                                        : BL == BLay::KPANEL ? (long long)n0 * BKB : (long long)(n0 >> 4) * 16 * KB);
     const uint8_t* SFA = p.sfa + bz * p.sfa_batch * (VALU_SCALE ? 4 : 1);
     const uint8_t* SFB = p.sfb + bz * p.sfb_batch * (VALU_SCALE ? 4 : 1);
 
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
         const int r = (w * DMA_PER_WAVE + t) * 8 + (L >> 3);
         const int c = (L & 7) ^ swz<FP4>(r);
         aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
-        const int gn = min(n0 + r, N - 1);
+        const int gn = min(n0 + r, N - 1) - n0;
         if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
         else if constexpr (BL == BLay::KPANEL) boff[t] = gn * BKB + c * 16;
         else boff[t] = (gn >> 4) * 16 * KB + (gn & 15) * 16 + c * 256;
@@ -237,18 +241,37 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
         }
     };
 
-    auto issue = [&](int kt, QG_LDS uint8_t* sA, QG_LDS uint8_t* sB, QG_LDS uint8_t* sSA,
-                     QG_LDS uint8_t* sSB) {
+    // DMA of K-tile kt into one stage, in BLK_M parts: part j moves the
+    // operand rows of this wave's DMAs t with t*BLK_M/DMA_PER_WAVE == j, of
+    // A and B (part 0 also the scales).  The parts are issued between the
+    // MFMA groups of the previous K-tile, so no wave stalls on a long run
+    // of DMA issues while its SIMD's matrix core idles.
+    // Operand DMAs go through buffer descriptors whose range is empty when
+    // `valid` is false: the DMA then reads nothing and writes zeros into a
+    // stage no wave reads again, so the issue needs no branch (a branch would
+    // split the schedule the MFMAs are interleaved into).
+    auto issue_part = [&](int kt, int j, bool valid, QG_LDS uint8_t* sA, QG_LDS uint8_t* sB,
+                          QG_LDS uint8_t* sSA, QG_LDS uint8_t* sSB) {
         const uint8_t* Ak = A + kt * BKB;
         const uint8_t* Bk;
         if constexpr (BL == BLay::RAW) Bk = B + kt * BKB;
         else if constexpr (BL == BLay::KPANEL) Bk = B + (long long)kt * N * BKB;
         else Bk = B + kt * 2048;
+        const unsigned nrec = valid ? 0x7FFFFFFFu : 0u;
+        const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(Ak), 0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(Bk), 0, nrec, 0x00020000);
+        if (j == 0 && valid) issue_scales(kt, sSA, sSB);
 #pragma unroll
-        for (int t = 0; t < DMA_PER_WAVE; ++t) dma16(Ak + aoff[t], sA + (w * DMA_PER_WAVE + t) * 8 * BKB);
+        for (int t = 0; t < DMA_PER_WAVE; ++t) {
+            if (t * BLK_M / DMA_PER_WAVE != j) continue;
+            dma16_buf(rA, sA + (w * DMA_PER_WAVE + t) * 8 * BKB, aoff[t], 0);
+            dma16_buf(rB, sB + (w * DMA_PER_WAVE + t) * 8 * BKB, boff[t], 0);
+        }
+    };
+    auto issue = [&](int kt, QG_LDS uint8_t* sA, QG_LDS uint8_t* sB, QG_LDS uint8_t* sSA,
+                     QG_LDS uint8_t* sSB) {
 #pragma unroll
-        for (int t = 0; t < DMA_PER_WAVE; ++t) dma16(Bk + boff[t], sB + (w * DMA_PER_WAVE + t) * 8 * BKB);
-        issue_scales(kt, sSA, sSB);
+        for (int j = 0; j < BLK_M; ++j) issue_part(kt, j, true, sA, sB, sSA, sSB);
     };
 
     f32x4 acc[BLK_M][BLK_N];
@@ -264,7 +287,7 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
     const int unit = p.unit_scale;
 
     auto compute = [&](int kt, const QG_LDS uint8_t* sA, const QG_LDS uint8_t* sB,
-                       const QG_LDS uint8_t* sSA, const QG_LDS uint8_t* sSB) {
+                       const QG_LDS uint8_t* sSA, const QG_LDS uint8_t* sSB, auto&& hook) {
         int sa[BLK_M], sb[BLK_N];
         float fs[BLK_M];
         if constexpr (MX) {
@@ -291,41 +314,42 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
 #pragma unroll
             for (int j = 0; j < BLK_N; ++j) sb[j] = unit;
         }
-        i32x8 af[BLK_M];
+        // The wave's BLK_N B fragments stay in registers for the K-tile and
+        // the A fragments stream through one block at a time (fewer live
+        // registers than the other way round, BLK_M >= BLK_N); hook(i) runs
+        // before A block i's MFMAs.
+        auto read_frag = [&](const QG_LDS uint8_t* blk) -> i32x8 {
+            const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd0);
+            const i32x4 hi = *(const QG_LDS i32x4*)(blk + rd1);
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        i32x8 bfr[BLK_N];
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j) bfr[j] = read_frag(sB + (wn * BLK_N * 16 + j * 16) * BKB);
 #pragma unroll
         for (int i = 0; i < BLK_M; ++i) {
-            const QG_LDS uint8_t* blk = sA + (wm * BLK_M * 16 + i * 16) * BKB;
-            const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd0);
-            const i32x4 hi = *(const QG_LDS i32x4*)(blk + rd1);
-            af[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+            hook(i);
+            const i32x8 af = read_frag(sA + (wm * BLK_M * 16 + i * 16) * BKB);
 #pragma unroll
-        for (int j = 0; j < BLK_N; ++j) {
-            const QG_LDS uint8_t* blk = sB + (wn * BLK_N * 16 + j * 16) * BKB;
-            const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd0);
-            const i32x4 hi = *(const QG_LDS i32x4*)(blk + rd1);
-#pragma unroll
-            for (int i = 0; i < BLK_M; ++i) {
+            for (int j = 0; j < BLK_N; ++j) {
+                const i32x8& bf = bfr[j];
                 if constexpr (FP4) {
-                    const i32x8 b0 = i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
-                    const i32x8 b1 = i32x8{hi[0], hi[1], hi[2], hi[3], 0, 0, 0, 0};
-                    const i32x8 a0 = i32x8{af[i][0], af[i][1], af[i][2], af[i][3], 0, 0, 0, 0};
-                    const i32x8 a1 = i32x8{af[i][4], af[i][5], af[i][6], af[i][7], 0, 0, 0, 0};
+                    const i32x8 b0 = i32x8{bf[0], bf[1], bf[2], bf[3], 0, 0, 0, 0};
+                    const i32x8 b1 = i32x8{bf[4], bf[5], bf[6], bf[7], 0, 0, 0, 0};
+                    const i32x8 a0 = i32x8{af[0], af[1], af[2], af[3], 0, 0, 0, 0};
+                    const i32x8 a1 = i32x8{af[4], af[5], af[6], af[7], 0, 0, 0, 0};
                     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                         b0, a0, acc[i][j], kFmtFp4, kFmtFp4, 0, sb[j], 0, sa[i]);
                     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                         b1, a1, acc[i][j], kFmtFp4, kFmtFp4, 1, sb[j], 1, sa[i]);
-                } else {
-                    const i32x8 bf = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    if constexpr (VALU_SCALE) {
-                        const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                            bf, af[i], f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, sb[j], 0, sa[i]);
+                } else if constexpr (VALU_SCALE) {
+                    const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        bf, af, f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, sb[j], 0, sa[i]);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(part[r], fs[i], acc[i][j][r]);
-                    } else {
-                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                            bf, af[i], acc[i][j], kFmtFp8, kFmtFp8, 0, sb[j], 0, sa[i]);
-                    }
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(part[r], fs[i], acc[i][j][r]);
+                } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        bf, af, acc[i][j], kFmtFp8, kFmtFp8, 0, sb[j], 0, sa[i]);
                 }
             }
         }
@@ -342,8 +366,9 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
 
     // One loop body with a runtime stage select keeps the accumulators
     // resident (two copies of the body make the register allocator shuffle
-    // them).  DMA(kt+1) is issued right after the barrier that retires every
-    // read of K-tile kt-1 from the same stage.  The barrier is s_barrier
+    // them).  DMA(kt+1) is issued in parts during compute(kt), after the
+    // barrier that retires every read of K-tile kt-1 from the same stage.
+    // The barrier is s_barrier
     // behind an explicit lgkmcnt(0): __syncthreads() would also wait for the
     // LDS DMA issued just before (vmcnt(0)) on the next iteration's path.
     const int nk = KB / BKB;
@@ -352,8 +377,14 @@ __global__ __launch_bounds__(tile_threads<SK>(), 1) void tile_gemm_kernel(const 
         wait_vmcnt<0>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const int s = kt & 1;
-        if (kt + 1 < nk) issue(kt + 1, s ? pA0 : pA1, s ? pB0 : pB1, s ? pSA0 : pSA1, s ? pSB0 : pSB1);
-        compute(kt, s ? pA1 : pA0, s ? pB1 : pB0, s ? pSA1 : pSA0, s ? pSB1 : pSB0);
+        const bool more = kt + 1 < nk;
+        QG_LDS uint8_t* nA = s ? pA0 : pA1;
+        QG_LDS uint8_t* nB = s ? pB0 : pB1;
+        QG_LDS uint8_t* nSA = s ? pSA0 : pSA1;
+        QG_LDS uint8_t* nSB = s ? pSB0 : pSB1;
+        compute(kt, s ? pA1 : pA0, s ? pB1 : pB0, s ? pSA1 : pSA0, s ? pSB1 : pSB0, [&](int j) {
+            issue_part(kt + 1, j, more, nA, nB, nSA, nSB);
+        });
     }
 
     // ---- epilogue: lane holds C[m][n..n+3] for each (i, j) block ----

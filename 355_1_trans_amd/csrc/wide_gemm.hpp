@@ -1,0 +1,358 @@
+// Four-wave 256 x 256 tile GEMM for gfx950 on the scaled MFMA 16x16x128 (fp8).
+//
+// One workgroup of 4 wave64 (one per SIMD) computes a 256 x 256 tile of C;
+// wave (wm, wn) owns the 128 x 128 sub-tile of 8 x 8 16x16 blocks, whose 256
+// fp32 accumulators live in AGPRs.  Against the 8-wave tile kernel this halves
+// the LDS bytes read per MFMA (each wave reads 128 + 128 rows per K-tile for 64
+// MFMAs instead of 128 + 64 rows for 32), and it keeps the global->LDS DMA
+// stream from draining at every K-tile:
+//
+//  * operands are staged in registers: the wave's A rows and B rows of one
+//    K-tile are four register halves (A blocks 0-3 / 4-7, B blocks 0-3 / 4-7,
+//    32 VGPRs each).  A K-tile runs as four quadrants of 4 x 4 blocks (16
+//    MFMAs) in Gray-code order over (A half, B half), so consecutive
+//    quadrants share one half; the order rotates by one quadrant per K-tile.
+//    A half is reloaded with the next K-tile's rows as soon as its last
+//    quadrant has issued, so the next K-tile's LDS reads run under this
+//    K-tile's MFMAs: two halves during quadrants 3-4, two during quadrant 1
+//    of the next K-tile;
+//  * two LDS stages hold K-tiles t+1 (being read) and t+2 (being written).
+//    Barrier B1 after quadrant 1 (every read of K-tile t done) frees K-tile
+//    t's stage for the DMA of t+2, issued during quadrants 2-3; barrier B2
+//    after quadrant 2 waits only for K-tile t+1's DMA (vmcnt = the DMAs of
+//    t+2 issued in quadrant 2), so the DMA queue never runs empty;
+//  * DMAs go through buffer descriptors whose range is empty past the last
+//    K-tile, so the steady-state code has no branches around them.
+//
+// Operand layout in LDS, register layout of the MFMA and the scale policies
+// (MX panels, BS8) are those of the 8-wave tile kernel (tile_gemm.hpp).
+#pragma once
+#include "tile_gemm.hpp"
+
+namespace qg {
+
+namespace wide {
+// Gray-code cycle over (A half, B half): (0,0) (0,1) (1,1) (1,0)
+constexpr int qa(int g) { return (g & 3) >= 2 ? 1 : 0; }
+constexpr int qb(int g) { return ((g & 3) == 1 || (g & 3) == 2) ? 1 : 0; }
+// quadrant k of the K-tile in phase P runs cycle entry (k + P) & 3; the half
+// shared by quadrants k and k+1: {is_a, half}
+constexpr bool shared_is_a(int P, int k) { return qa((k + P) & 3) == qa((k + 1 + P) & 3); }
+constexpr int shared_half(int P, int k) {
+    return shared_is_a(P, k) ? qa((k + P) & 3) : qb((k + P) & 3);
+}
+template <int V>
+struct I {
+    static constexpr int value = V;
+};
+// acc += scaled fp8 MFMA with the accumulator pinned to AGPRs (the "a"
+// constraint): left to the register allocator, 256 accumulators plus 128
+// operand registers get shuffled between AGPRs, VGPRs and scratch.  The
+// compiler's hazard tracking does not look inside inline asm, so the
+// statement opens with the wait states a VALU write of an operand VGPR needs
+// before an MFMA reads it; they issue while the previous MFMA occupies the
+// matrix core.
+__device__ __forceinline__ void mfma_fp8(f32x4& acc, const i32x8& b, const i32x8& a, int sb, int sa) {
+    asm("s_nop 3\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
+        : "+a"(acc)
+        : "v"(b), "v"(a), "v"(sb), "v"(sa));
+}
+}  // namespace wide
+
+template <int FMT, ScaleKind SK, BLay BL, bool BF16, int PB = 16>
+__global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
+    static_assert(FMT == kFmtFp8 && SK != ScaleKind::BSF32, "fp8 with MFMA-applied scales");
+    constexpr bool MX = (SK == ScaleKind::MX);
+    constexpr int BKB = 128, BM = 256;
+    constexpr int KT_BYTES = 4;  // MX scale bytes per row per K-tile
+    static_assert(PB == 16 || PB == KT_BYTES, "panel width");
+    constexpr int SPAN = MX ? PB / KT_BYTES : 1;  // K-tiles per scale DMA
+    constexpr int PANEL = 256 * 16;
+    constexpr int SA_BYTES = MX ? 2 * PANEL : 2 * 256;  // BS8: a 256-byte slot per stage
+    constexpr int SB_BYTES = MX ? 2 * PANEL : 2 * 4 * 256;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lA0[BM * BKB];
+    __shared__ __attribute__((aligned(1024))) uint8_t lA1[BM * BKB];
+    __shared__ __attribute__((aligned(1024))) uint8_t lB0[BM * BKB];
+    __shared__ __attribute__((aligned(1024))) uint8_t lB1[BM * BKB];
+    __shared__ __attribute__((aligned(256))) uint8_t lSA[SA_BYTES];
+    __shared__ __attribute__((aligned(256))) uint8_t lSB[SB_BYTES];
+    // BS8: landing slots of the no-op SFA DMAs of waves 1-3 (an empty-range
+    // buffer DMA still writes zeros to its LDS destination)
+    __shared__ __attribute__((aligned(256))) uint8_t lJunk[MX ? 4 : 1024];
+
+    // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
+    const int T = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+    const int gfull = p.group_m * p.tiles_n;
+    const int g = bid / gfull;
+    const int first_m = g * p.group_m;
+    const int gm = min(p.tiles_m - first_m, p.group_m);
+    const int within = bid - g * gfull;
+    const int tm = first_m + within % gm;
+    const int tn = within / gm;
+    const int bz = blockIdx.z;
+    const int m0 = tm * BM, n0 = tn * BM;
+
+    const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
+    const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
+    const int wm = w >> 1, wn = w & 1;
+    const int q = L >> 4, l16 = L & 15;
+
+    const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
+    const uint8_t* B = p.b + bz * p.b_batch +
+                       (BL == BLay::RAW ? (long long)n0 * LDB
+                                        : BL == BLay::KPANEL ? (long long)n0 * BKB : (long long)(n0 >> 4) * 16 * KB);
+    const uint8_t* SFA = p.sfa + bz * p.sfa_batch;
+    const uint8_t* SFB = p.sfb + bz * p.sfb_batch;
+
+    // ---- per-lane DMA offsets: wave w fills rows [64w, 64w + 64) of A and
+    // B, eight 8-row DMAs each; lane L writes row +L/8, physical chunk L%8 =
+    // logical chunk (L%8) ^ swz(row) ----
+    int aoff[8], boff[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int r = (w * 8 + t) * 8 + (L >> 3);
+        const int c = (L & 7) ^ swz<false>(r);
+        aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
+        const int gn = min(n0 + r, N - 1) - n0;
+        if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
+        else if constexpr (BL == BLay::KPANEL) boff[t] = gn * BKB + c * 16;
+        else boff[t] = (gn >> 4) * 16 * KB + (gn & 15) * 16 + c * 256;
+    }
+
+    // ---- scale sources (buffer DMAs; empty range = no-op) ----
+    // MX panels: wave w moves the panel rows of A quarter w and B quarter w
+    // (lane L = row 64w + L)
+    const uint8_t* SFA_t = SFA + (long long)m0 * (MX ? SFA_SM : 1);
+    const uint8_t* SFB_t = SFB + (MX ? (long long)n0 * SFB_SN : 0ll);
+    const int mx_voff_a = (min(m0 + w * 64 + L, M - 1) - m0) * SFA_SM;
+    const int mx_voff_b = (min(n0 + w * 64 + L, N - 1) - n0) * SFB_SN;
+    // BS8: SFA's 256 row bytes of a K-tile by wave 0; SFB's byte of the
+    // wave's 128-column block as the aligned dword holding it
+    const long long bs_b_idx = (long long)min((n0 >> 7) + wn, (N - 1) >> 7) * SFB_SN;
+
+    QG_LDS uint8_t* pA0 = (QG_LDS uint8_t*)lA0;
+    QG_LDS uint8_t* pA1 = (QG_LDS uint8_t*)lA1;
+    QG_LDS uint8_t* pB0 = (QG_LDS uint8_t*)lB0;
+    QG_LDS uint8_t* pB1 = (QG_LDS uint8_t*)lB1;
+    QG_LDS uint8_t* pSA = (QG_LDS uint8_t*)lSA;
+    QG_LDS uint8_t* pSB = (QG_LDS uint8_t*)lSB;
+    QG_LDS uint8_t* pJunk = (QG_LDS uint8_t*)lJunk;
+
+    const int nk = KB / BKB;
+
+    auto rsrc = [&](const uint8_t* base, bool valid) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
+                                                 0x00020000);
+    };
+    auto b_ktile = [&](int kt) __attribute__((always_inline)) -> const uint8_t* {
+        if constexpr (BL == BLay::RAW) return B + kt * BKB;
+        else if constexpr (BL == BLay::KPANEL) return B + (long long)kt * N * BKB;
+        else return B + kt * 2048;
+    };
+    auto dma_a = [&](int kt, bool valid, QG_LDS uint8_t* sA) __attribute__((always_inline)) {
+        const auto r = rsrc(A + kt * BKB, valid);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dma16_buf(r, sA + (w * 8 + t) * 8 * BKB, aoff[t], 0);
+    };
+    auto dma_b = [&](int kt, bool valid, QG_LDS uint8_t* sB) __attribute__((always_inline)) {
+        const auto r = rsrc(b_ktile(kt), valid);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dma16_buf(r, sB + (w * 8 + t) * 8 * BKB, boff[t], 0);
+    };
+    // scale DMAs that go with K-tile kt (MX: only when kt starts a panel,
+    // which the callers know at compile time); `valid` false = no-op DMAs
+    auto dma_scales = [&](int kt, bool valid) __attribute__((always_inline)) {
+        if constexpr (MX) {
+            const int buf = ((kt / SPAN) & 1) * PANEL;
+            const auto ra = rsrc(SFA_t + kt * KT_BYTES, valid);
+            const auto rb = rsrc(SFB_t + kt * KT_BYTES, valid);
+            if constexpr (PB == 16) {
+                dma16_buf(ra, pSA + buf + w * 1024, mx_voff_a, 0);
+                dma16_buf(rb, pSB + buf + w * 1024, mx_voff_b, 0);
+            } else {
+                dma4_buf(ra, pSA + buf + w * 256, mx_voff_a, 0);
+                dma4_buf(rb, pSB + buf + w * 256, mx_voff_b, 0);
+            }
+        } else {
+            const int st = kt & 1;
+            const auto ra = rsrc(SFA_t + (long long)kt * SFA_SK, valid && w == 0);
+            const auto rb = rsrc(SFB + ((bs_b_idx + kt) & ~3ll), valid);
+            dma4_buf(ra, w == 0 ? pSA + st * 256 : pJunk + w * 256, 4 * L, 0);
+            dma4_buf(rb, pSB + st * 1024 + w * 256, 0, 0);
+        }
+    };
+    // scale bytes of K-tile kt for lane group q: A block x (sa[x]) and B
+    // block x (sb[x]); BS8 has one B scale per wave, read with x = 0
+    auto read_scale = [&](int kt, int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
+        if constexpr (MX) {
+            const int buf = ((kt / SPAN) & 1) * PANEL;
+            const int col = PB == 16 ? (kt % SPAN) * KT_BYTES + q : q;
+            sa[x] = pSA[buf + (wm * 128 + x * 16 + l16) * PB + col];
+            sb[x] = pSB[buf + (wn * 128 + x * 16 + l16) * PB + col];
+        } else {
+            const int st = kt & 1;
+            sa[x] = pSA[st * 256 + wm * 128 + x * 16 + l16];
+            if (x == 0) {
+                const int v = pSB[st * 1024 + w * 256 + (int)((bs_b_idx + kt) & 3)];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sb[j] = v;
+            }
+        }
+    };
+
+    // per-lane operand read offsets inside a 16-row block: chunks q and q+4
+    const int rd0 = l16 * BKB + ((q ^ swz<false>(l16)) << 4);
+    const int rd1 = rd0 ^ 64;
+    auto read_frag = [&](const QG_LDS uint8_t* blk) __attribute__((always_inline)) -> i32x8 {
+        const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd0);
+        const i32x4 hi = *(const QG_LDS i32x4*)(blk + rd1);
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    f32x4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    i32x8 ah[2][4], bh[2][4];
+
+    // fragment x of register half h of A (is_a) or B
+    auto read_one = [&](bool is_a, int h, int x, const QG_LDS uint8_t* sA,
+                        const QG_LDS uint8_t* sB) __attribute__((always_inline)) {
+        if (is_a) ah[h][x] = read_frag(sA + (wm * 128 + (4 * h + x) * 16) * BKB);
+        else bh[h][x] = read_frag(sB + (wn * 128 + (4 * h + x) * 16) * BKB);
+    };
+    // quadrant (ha, hb): 16 MFMAs; after MFMA k, fill(k) issues this step's
+    // share of LDS reads and DMAs.  Each step is fenced so the order stays
+    // as written: the LDS reads and DMAs spread between MFMAs, and no read
+    // of a register half moves above the last MFMA that uses its old rows.
+    auto quadrant = [&](int ha, int hb, const int (&sa)[8], const int (&sb)[8],
+                        auto&& fill) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                wide::mfma_fp8(acc[4 * ha + i][4 * hb + j], bh[hb][j], ah[ha][i], sb[4 * hb + j], sa[4 * ha + i]);
+                __builtin_amdgcn_sched_barrier(0);
+                fill(4 * i + j);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    };
+
+    // One K-tile t in phase P = t % 4 (LDS stage P & 1 holds t and then
+    // t + 2).  sa/sb: this K-tile's scales; san/sbn receive K-tile t + 1's.
+    auto ktile = [&](auto PC, int t, const int (&sa)[8], const int (&sb)[8], int (&san)[8],
+                     int (&sbn)[8]) __attribute__((always_inline)) {
+        constexpr int P = decltype(PC)::value;
+        QG_LDS uint8_t* sA = (P & 1) ? pA1 : pA0;
+        QG_LDS uint8_t* sB = (P & 1) ? pB1 : pB0;
+        QG_LDS uint8_t* nA = (P & 1) ? pA0 : pA1;
+        QG_LDS uint8_t* nB = (P & 1) ? pB0 : pB1;
+        constexpr bool r1a = wide::shared_is_a(P, 1), r2a = wide::shared_is_a(P, 2), r0a = wide::shared_is_a(P, 0);
+        constexpr int r1 = wide::shared_half(P, 1), r2 = wide::shared_half(P, 2), r0 = wide::shared_half(P, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // quadrant 1: K-tile t's two halves freed at the end of the previous
+        // K-tile, one fragment after each of the first 8 MFMAs
+        quadrant(wide::qa(P), wide::qb(P), sa, sb, [&](int k) __attribute__((always_inline)) {
+            if (k < 4) read_one(r1a, r1, k, sA, sB);
+            else if (k < 8) read_one(r2a, r2, k - 4, sA, sB);
+        });
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1: stage P&1 is free
+        // quadrant 2: scales and A rows of K-tile t + 2 into this K-tile's
+        // stage (the scales first: B2's vmcnt then covers them)
+        const bool more = t + 2 < nk;
+        if constexpr ((P + 2) % SPAN == 0) dma_scales(t + 2, more);
+        const auto rA = rsrc(A + (t + 2) * BKB, more);
+        quadrant(wide::qa(P + 1), wide::qb(P + 1), sa, sb, [&](int k) __attribute__((always_inline)) {
+            if (k < 8) dma16_buf(rA, sA + (w * 8 + k) * 8 * BKB, aoff[k], 0);
+        });
+        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");  // B2: K-tile t + 1 landed
+        // quadrant 3: B rows of t + 2; first half of t + 1
+        const auto rB = rsrc(b_ktile(t + 2), more);
+        quadrant(wide::qa(P + 2), wide::qb(P + 2), sa, sb, [&](int k) __attribute__((always_inline)) {
+            if (k < 8) dma16_buf(rB, sB + (w * 8 + k) * 8 * BKB, boff[k], 0);
+            if (k < 8 && (k & 1) == 0) read_one(r0a, r0, k >> 1, nA, nB);
+        });
+        // quadrant 4: second half and scales of t + 1
+        quadrant(wide::qa(P + 3), wide::qb(P + 3), sa, sb, [&](int k) __attribute__((always_inline)) {
+            if (k < 4) read_one(r1a, r1, k, nA, nB);
+            if (k < 8) read_scale(t + 1, k, san, sbn);
+        });
+    };
+
+    // ---- prologue: DMA K-tiles 0 and 1 (scales of 1 first, so vmcnt(16)
+    // leaves only the operand DMAs of K-tile 1 outstanding) ----
+    dma_scales(0, true);
+    dma_a(0, true, pA0);
+    dma_b(0, true, pB0);
+    if constexpr (SPAN == 1) dma_scales(1, nk > 1);
+    dma_a(1, nk > 1, pA1);
+    dma_b(1, nk > 1, pB1);
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    // halves and scales used by quadrant 1 of K-tile 0
+    int s0a[8], s0b[8], s1a[8], s1b[8];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        read_one(wide::shared_is_a(0, 3), wide::shared_half(0, 3), x, pA0, pB0);
+        read_one(wide::shared_is_a(0, 0), wide::shared_half(0, 0), x, pA0, pB0);
+    }
+#pragma unroll
+    for (int x = 0; x < 8; ++x) read_scale(0, x, s0a, s0b);
+
+    int t = 0;
+    for (; t + 4 <= nk; t += 4) {
+        ktile(wide::I<0>{}, t, s0a, s0b, s1a, s1b);
+        ktile(wide::I<1>{}, t + 1, s1a, s1b, s0a, s0b);
+        ktile(wide::I<2>{}, t + 2, s0a, s0b, s1a, s1b);
+        ktile(wide::I<3>{}, t + 3, s1a, s1b, s0a, s0b);
+    }
+    if (t < nk) ktile(wide::I<0>{}, t, s0a, s0b, s1a, s1b);
+    if (t + 1 < nk) ktile(wide::I<1>{}, t + 1, s1a, s1b, s0a, s0b);
+    if (t + 2 < nk) ktile(wide::I<2>{}, t + 2, s0a, s0b, s1a, s1b);
+    wait_vmcnt<0>();
+    // the accumulators come from inline-asm MFMAs, which the compiler's hazard
+    // tracking does not see: cover the MFMA-result-to-VALU-read latency
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+    // ---- epilogue: lane holds C[m][n..n+3] for each (i, j) block ----
+    const int mrow0 = m0 + wm * 128 + l16;
+    const int ncol0 = n0 + wn * 128 + 4 * q;
+    const bool vec_ok = (LDC & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int mm = mrow0 + i * 16;
+        if (mm < M) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int nn = ncol0 + j * 16;
+                const f32x4 v = acc[i][j];
+                if constexpr (BF16) {
+                    uint16_t* crow = (uint16_t*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                    if (vec_ok && nn + 3 < N) {
+                        *(u32x2*)(crow + nn) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    } else {
+                        for (int r = 0; r < 4; ++r)
+                            if (nn + r < N) crow[nn + r] = bf16_bits(v[r]);
+                    }
+                } else {
+                    float* crow = (float*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                    if (vec_ok && nn + 3 < N) {
+                        *(f32x4*)(crow + nn) = v;
+                    } else {
+                        for (int r = 0; r < 4; ++r)
+                            if (nn + r < N) crow[nn + r] = v[r];
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+}  // namespace qg
