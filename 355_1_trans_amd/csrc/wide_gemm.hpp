@@ -324,6 +324,44 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     const int mrow0 = m0 + wm * 128 + l16;
     const int ncol0 = n0 + wn * 128 + 4 * q;
     const bool vec_ok = (LDC & 3) == 0;
+    if (vec_ok && m0 + BM <= M && n0 + BM <= N) {
+        if constexpr (BF16) {
+            // Whole tile inside C, bf16: the wave's 128 x 128 block goes
+            // through its own 32 KB of LDS (one operand stage, rows of 256 B,
+            // 16-byte chunks XOR-swizzled by row) so that every global store
+            // writes whole 128-byte lines: 16 B per lane, 4 rows of 256 B
+            // per instruction, instead of 16 rows x 32 B.
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            QG_LDS uint8_t* img = w == 0 ? pA0 : w == 1 ? pA1 : w == 2 ? pB0 : pB1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int r = i * 16 + l16;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int c = (2 * j + (q >> 1)) ^ (r & 15);
+                    *(QG_LDS u32x2*)(img + r * 256 + c * 16 + (q & 1) * 8) =
+                        u32x2{pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+                }
+            }
+            const int rr = L >> 4, cc = L & 15;
+            uint16_t* cbase = (uint16_t*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128 + rr) * LDC +
+                              n0 + wn * 128 + cc * 8;
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                const int r = u * 4 + rr;
+                const i32x4 v = *(const QG_LDS i32x4*)(img + r * 256 + ((cc ^ (r & 15)) << 4));
+                *(i32x4*)(cbase + (long long)u * 4 * LDC) = v;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float* crow = (float*)p.c + (long long)bz * p.c_batch + (long long)(mrow0 + i * 16) * LDC + ncol0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) *(f32x4*)(crow + j * 16) = acc[i][j];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int mm = mrow0 + i * 16;
