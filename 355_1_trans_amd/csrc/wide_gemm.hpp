@@ -18,7 +18,7 @@
 //    of the next K-tile;
 //  * two LDS stages hold K-tiles t+1 (being read) and t+2 (being written).
 //    Barrier B1 after quadrant 1 (every read of K-tile t done) frees K-tile
-//    t's stage for the DMA of t+2, issued during quadrants 2-3; barrier B2
+//    t's stage for the DMA of t+2, spread over quadrants 2-4; barrier B2
 //    after quadrant 2 waits only for K-tile t+1's DMA (vmcnt = the DMAs of
 //    t+2 issued in quadrant 2), so the DMA queue never runs empty;
 //  * DMAs go through buffer descriptors whose range is empty past the last
@@ -49,11 +49,11 @@ struct I {
 // constraint): left to the register allocator, 256 accumulators plus 128
 // operand registers get shuffled between AGPRs, VGPRs and scratch.  The
 // compiler's hazard tracking does not look inside inline asm, so the
-// statement opens with the wait states a VALU write of an operand VGPR needs
-// before an MFMA reads it; they issue while the previous MFMA occupies the
-// matrix core.
+// statement opens with the two wait states a VALU write of an operand VGPR
+// needs before an MFMA reads it; they issue while the previous MFMA occupies
+// the matrix core.
 __device__ __forceinline__ void mfma_fp8(f32x4& acc, const i32x8& b, const i32x8& a, int sb, int sa) {
-    asm("s_nop 3\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
+    asm("s_nop 1\n\tv_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
         : "+a"(acc)
         : "v"(b), "v"(a), "v"(sb), "v"(sa));
 }
@@ -264,23 +264,32 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             else if (k < 8) read_one(r2a, r2, k - 4, sA, sB);
         });
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1: stage P&1 is free
-        // quadrant 2: scales and A rows of K-tile t + 2 into this K-tile's
-        // stage (the scales first: B2's vmcnt then covers them)
+        // quadrants 2-4: the 16 operand DMAs of K-tile t + 2 (A rows 0-7,
+        // then B rows 0-7, in 8-row groups) into this K-tile's stage, one
+        // after every third MFMA, so the CU's texture path is never asked
+        // for more than it streams (a wave blocks on a DMA it cannot queue);
+        // the scale DMAs go first, so B2's vmcnt covers them
         const bool more = t + 2 < nk;
         if constexpr ((P + 2) % SPAN == 0) dma_scales(t + 2, more);
         const auto rA = rsrc(A + (t + 2) * BKB, more);
-        quadrant(wide::qa(P + 1), wide::qb(P + 1), sa, sb, [&](int k) __attribute__((always_inline)) {
-            if (k < 8) dma16_buf(rA, sA + (w * 8 + k) * 8 * BKB, aoff[k], 0);
-        });
-        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");  // B2: K-tile t + 1 landed
-        // quadrant 3: B rows of t + 2; first half of t + 1
         const auto rB = rsrc(b_ktile(t + 2), more);
+        auto dma_op = [&](int d) __attribute__((always_inline)) {
+            if (d < 8) dma16_buf(rA, sA + (w * 8 + d) * 8 * BKB, aoff[d], 0);
+            else dma16_buf(rB, sB + (w * 8 + d - 8) * 8 * BKB, boff[d - 8], 0);
+        };
+        // quadrant 2: DMAs 0-5
+        quadrant(wide::qa(P + 1), wide::qb(P + 1), sa, sb, [&](int k) __attribute__((always_inline)) {
+            if (k % 3 == 0) dma_op(k / 3);
+        });
+        asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");  // B2: K-tile t + 1 landed
+        // quadrant 3: DMAs 6-10; first half of t + 1
         quadrant(wide::qa(P + 2), wide::qb(P + 2), sa, sb, [&](int k) __attribute__((always_inline)) {
-            if (k < 8) dma16_buf(rB, sB + (w * 8 + k) * 8 * BKB, boff[k], 0);
+            if (k % 3 == 2) dma_op(6 + k / 3);
             if (k < 8 && (k & 1) == 0) read_one(r0a, r0, k >> 1, nA, nB);
         });
-        // quadrant 4: second half and scales of t + 1
+        // quadrant 4: DMAs 11-15; second half and scales of t + 1
         quadrant(wide::qa(P + 3), wide::qb(P + 3), sa, sb, [&](int k) __attribute__((always_inline)) {
+            if (k % 3 == 1) dma_op(11 + k / 3);
             if (k < 4) read_one(r1a, r1, k, nA, nB);
             if (k < 8) read_scale(t + 1, k, san, sbn);
         });
