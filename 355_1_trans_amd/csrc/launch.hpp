@@ -21,6 +21,7 @@ hipError_t launch_tile32_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStr
 hipError_t launch_tile32_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
+hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 
 // skinny_*.hip: skinny-M / split-K kernel (mb = M-tile rows / 16, nb = N-tile columns / 16)

@@ -1,21 +1,23 @@
-// Four-wave 256 x 256 tile GEMM for gfx950 on the scaled MFMA 16x16x128 (fp8).
+// Four-wave 256 x 256 tile GEMM for gfx950: fp8 on the scaled MFMA 16x16x128,
+// fp4 on the scaled MFMA 32x32x64.
 //
 // One workgroup of 4 wave64 (one per SIMD) computes a 256 x 256 tile of C;
-// wave (wm, wn) owns the 128 x 128 sub-tile of 8 x 8 16x16 blocks, whose 256
-// fp32 accumulators live in AGPRs.  Against the 8-wave tile kernel this halves
-// the LDS bytes read per MFMA (each wave reads 128 + 128 rows per K-tile for 64
-// MFMAs instead of 128 + 64 rows for 32), and it keeps the global->LDS DMA
-// stream from draining at every K-tile:
+// wave (wm, wn) owns a 128 x 128 sub-tile, whose 256 fp32 accumulators live in
+// AGPRs (fp8: 8 x 8 blocks of 16 x 16; fp4: 4 x 4 blocks of 32 x 32).  Against
+// the 8-wave tile kernel this halves the LDS bytes read per MFMA (each wave
+// reads 128 + 128 rows per K-tile for 64 MFMA-slots instead of 128 + 64 rows
+// for 32), and it keeps the global->LDS DMA stream from draining at every
+// K-tile:
 //
 //  * operands are staged in registers: the wave's A rows and B rows of one
-//    K-tile are four register halves (A blocks 0-3 / 4-7, B blocks 0-3 / 4-7,
-//    32 VGPRs each).  A K-tile runs as four quadrants of 4 x 4 blocks (16
-//    MFMAs) in Gray-code order over (A half, B half), so consecutive
-//    quadrants share one half; the order rotates by one quadrant per K-tile.
-//    A half is reloaded with the next K-tile's rows as soon as its last
-//    quadrant has issued, so the next K-tile's LDS reads run under this
-//    K-tile's MFMAs: two halves during quadrants 3-4, two during quadrant 1
-//    of the next K-tile;
+//    128-byte K-tile are four register halves (A rows 0-63 / 64-127, B rows
+//    0-63 / 64-127, 32 VGPRs each).  A K-tile runs as four quadrants of
+//    64 x 64 outputs (16 MFMAs) in Gray-code order over (A half, B half), so
+//    consecutive quadrants share one half; the order rotates by one quadrant
+//    per K-tile.  A half is reloaded with the next K-tile's rows as soon as
+//    its last quadrant has issued, so the next K-tile's LDS reads run under
+//    this K-tile's MFMAs: two halves during quadrants 3-4, two during
+//    quadrant 1 of the next K-tile;
 //  * two LDS stages hold K-tiles t+1 (being read) and t+2 (being written).
 //    Barrier B1 after quadrant 1 (every read of K-tile t done) frees K-tile
 //    t's stage for the DMA of t+2, spread over quadrants 2-4; barrier B2
@@ -24,12 +26,27 @@
 //  * DMAs go through buffer descriptors whose range is empty past the last
 //    K-tile, so the steady-state code has no branches around them.
 //
-// Operand layout in LDS, register layout of the MFMA and the scale policies
-// (MX panels, BS8) are those of the 8-wave tile kernel (tile_gemm.hpp).
+// Register layouts of the two MFMAs (pinned by the layout probes,
+// csrc/probe.hip; srcA = B rows, srcB = A rows):
+//  * 16x16x128 fp8: lane L = 16q + r holds row r, 16-byte chunks q and q+4
+//    of the 128-byte row; scale byte of lane group q covers K [32q, 32q+32);
+//    accumulator of lane L holds C[m = L%16][n = 4(L/16) + 0..3];
+//  * 32x32x64 fp4 (K = 64 = 32 bytes per instruction, 4 per K-tile): lane
+//    L = 32g + r holds row r, 16-byte chunk g of the 32-byte sub-tile, scaled
+//    by its own lane group's byte; accumulator register v of lane L holds
+//    C[m = L%32][n = 8(v/4) + 4(L/32) + v%4].
+// Operand LDS rows are 128 bytes with 16-byte chunks XOR-swizzled per row
+// (fp8: r & 7; fp4: (r >> 1) & 7) so both the DMA writes and the fragment
+// reads are conflict free.  Scale policies (MX panels, BS8) are those of the
+// 8-wave tile kernel (tile_gemm.hpp).
 #pragma once
+#include <type_traits>
+
 #include "tile_gemm.hpp"
 
 namespace qg {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace wide {
 // Gray-code cycle over (A half, B half): (0,0) (0,1) (1,1) (1,0)
@@ -45,7 +62,7 @@ template <int V>
 struct I {
     static constexpr int value = V;
 };
-// acc += scaled fp8 MFMA with the accumulator pinned to AGPRs (the "a"
+// acc += scaled MFMA with the accumulator pinned to AGPRs (the "a"
 // constraint): left to the register allocator, 256 accumulators plus 128
 // operand registers get shuffled between AGPRs, VGPRs and scratch.  The
 // compiler's hazard tracking does not look inside inline asm, so the
@@ -57,19 +74,39 @@ __device__ __forceinline__ void mfma_fp8(f32x4& acc, const i32x8& b, const i32x8
         : "+a"(acc)
         : "v"(b), "v"(a), "v"(sb), "v"(sa));
 }
+// fp4 32x32x64; OPS2 selects byte 2 (else byte 0) of both scale registers
+template <bool OPS2>
+__device__ __forceinline__ void mfma_fp4(f32x16& acc, const i32x4& b, const i32x4& a, int sb, int sa) {
+    if constexpr (OPS2)
+        asm("s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,1,0] cbsz:4 blgp:4"
+            : "+a"(acc)
+            : "v"(b), "v"(a), "v"(sb), "v"(sa));
+    else
+        asm("s_nop 1\n\tv_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] cbsz:4 blgp:4"
+            : "+a"(acc)
+            : "v"(b), "v"(a), "v"(sb), "v"(sa));
+}
 }  // namespace wide
 
 template <int FMT, ScaleKind SK, BLay BL, bool BF16, int PB = 16>
 __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
-    static_assert(FMT == kFmtFp8 && SK != ScaleKind::BSF32, "fp8 with MFMA-applied scales");
+    constexpr bool FP4 = (FMT == kFmtFp4);
+    static_assert(SK != ScaleKind::BSF32 && (!FP4 || SK == ScaleKind::MX), "MFMA-applied scales");
     constexpr bool MX = (SK == ScaleKind::MX);
     constexpr int BKB = 128, BM = 256;
-    constexpr int KT_BYTES = 4;  // MX scale bytes per row per K-tile
+    constexpr int RB = FP4 ? 32 : 16;          // rows per MFMA block
+    constexpr int NBLK = 128 / RB;             // blocks per wave and operand
+    constexpr int KT_BYTES = FP4 ? 8 : 4;      // MX scale bytes per row per K-tile
     static_assert(PB == 16 || PB == KT_BYTES, "panel width");
     constexpr int SPAN = MX ? PB / KT_BYTES : 1;  // K-tiles per scale DMA
     constexpr int PANEL = 256 * 16;
     constexpr int SA_BYTES = MX ? 2 * PANEL : 2 * 256;  // BS8: a 256-byte slot per stage
     constexpr int SB_BYTES = MX ? 2 * PANEL : 2 * 4 * 256;
+    // a register half: fp8 4 fragments of 8 VGPRs (one per 16-row block);
+    // fp4 8 of 4 VGPRs (2 32-row blocks x 4 sub-tiles)
+    using Frag = std::conditional_t<FP4, i32x4, i32x8>;
+    constexpr int NF = FP4 ? 8 : 4;
+    using Acc = std::conditional_t<FP4, f32x16, f32x4>;
 
     __shared__ __attribute__((aligned(1024))) uint8_t lA0[BM * BKB];
     __shared__ __attribute__((aligned(1024))) uint8_t lA1[BM * BKB];
@@ -86,10 +123,10 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     int bid = blockIdx.x;
     if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
     const int gfull = p.group_m * p.tiles_n;
-    const int g = bid / gfull;
-    const int first_m = g * p.group_m;
+    const int gi = bid / gfull;
+    const int first_m = gi * p.group_m;
     const int gm = min(p.tiles_m - first_m, p.group_m);
-    const int within = bid - g * gfull;
+    const int within = bid - gi * gfull;
     const int tm = first_m + within % gm;
     const int tn = within / gm;
     const int bz = blockIdx.z;
@@ -101,7 +138,6 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
     const int wm = w >> 1, wn = w & 1;
-    const int q = L >> 4, l16 = L & 15;
 
     const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
     const uint8_t* B = p.b + bz * p.b_batch +
@@ -112,12 +148,12 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
 
     // ---- per-lane DMA offsets: wave w fills rows [64w, 64w + 64) of A and
     // B, eight 8-row DMAs each; lane L writes row +L/8, physical chunk L%8 =
-    // logical chunk (L%8) ^ swz(row) ----
+    // logical chunk (L%8) ^ swizzle(row) ----
     int aoff[8], boff[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const int r = (w * 8 + t) * 8 + (L >> 3);
-        const int c = (L & 7) ^ swz<false>(r);
+        const int c = (L & 7) ^ (FP4 ? ((r >> 1) & 7) : (r & 7));
         aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
         const int gn = min(n0 + r, N - 1) - n0;
         if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
@@ -166,7 +202,9 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         for (int t = 0; t < 8; ++t) dma16_buf(r, sB + (w * 8 + t) * 8 * BKB, boff[t], 0);
     };
     // scale DMAs that go with K-tile kt (MX: only when kt starts a panel,
-    // which the callers know at compile time); `valid` false = no-op DMAs
+    // which the callers know at compile time); `valid` false = no-op DMAs.
+    // MX panel images: PB = 16: [row][16 B]; PB = 4 (fp8): [row][4 B];
+    // PB = 8 (fp4): [2 halves][row][4 B]
     auto dma_scales = [&](int kt, bool valid) __attribute__((always_inline)) {
         if constexpr (MX) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
@@ -178,6 +216,10 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             } else {
                 dma4_buf(ra, pSA + buf + w * 256, mx_voff_a, 0);
                 dma4_buf(rb, pSB + buf + w * 256, mx_voff_b, 0);
+                if constexpr (PB == 8) {
+                    dma4_buf(ra, pSA + buf + 1024 + w * 256, mx_voff_a + 4, 0);
+                    dma4_buf(rb, pSB + buf + 1024 + w * 256, mx_voff_b + 4, 0);
+                }
             }
         } else {
             const int st = kt & 1;
@@ -187,14 +229,34 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             dma4_buf(rb, pSB + st * 1024 + w * 256, 0, 0);
         }
     };
-    // scale bytes of K-tile kt for lane group q: A block x (sa[x]) and B
-    // block x (sb[x]); BS8 has one B scale per wave, read with x = 0
+    // Scale registers of K-tile kt, x = 0..7 (A and B rows of the wave):
+    //  fp8: block x's byte for lane group q (sa[x], sb[x]); BS8 has one B
+    //       scale per wave, read with x = 0;
+    //  fp4: block x/2, word x%2, which holds the lane group's blocks of
+    //       instructions 2(x%2) (byte 0) and 2(x%2)+1 (byte 2) once
+    //       finish_scale has shifted the lane group's bytes down.  The shift
+    //       is a separate step, issued a few MFMAs after the read, so the
+    //       wave does not stall on the LDS latency.
+    const int q = L >> 4, l16 = L & 15, g = L >> 5, l32 = L & 31;
     auto read_scale = [&](int kt, int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
-        if constexpr (MX) {
+        if constexpr (MX && !FP4) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
             const int col = PB == 16 ? (kt % SPAN) * KT_BYTES + q : q;
             sa[x] = pSA[buf + (wm * 128 + x * 16 + l16) * PB + col];
             sb[x] = pSB[buf + (wn * 128 + x * 16 + l16) * PB + col];
+        } else if constexpr (MX) {
+            const int buf = ((kt / SPAN) & 1) * PANEL;
+            const int ra = wm * 128 + (x >> 1) * 32 + l32, rb = wn * 128 + (x >> 1) * 32 + l32;
+            int oa, ob;
+            if constexpr (PB == 16) {
+                oa = ra * 16 + (kt % SPAN) * KT_BYTES + (x & 1) * 4;
+                ob = rb * 16 + (kt % SPAN) * KT_BYTES + (x & 1) * 4;
+            } else {
+                oa = (x & 1) * 1024 + ra * 4;
+                ob = (x & 1) * 1024 + rb * 4;
+            }
+            sa[x] = (int)*(const QG_LDS uint32_t*)(pSA + buf + oa);
+            sb[x] = (int)*(const QG_LDS uint32_t*)(pSB + buf + ob);
         } else {
             const int st = kt & 1;
             sa[x] = pSA[st * 256 + wm * 128 + x * 16 + l16];
@@ -205,44 +267,75 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             }
         }
     };
-
-    // per-lane operand read offsets inside a 16-row block: chunks q and q+4
-    const int rd0 = l16 * BKB + ((q ^ swz<false>(l16)) << 4);
-    const int rd1 = rd0 ^ 64;
-    auto read_frag = [&](const QG_LDS uint8_t* blk) __attribute__((always_inline)) -> i32x8 {
-        const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd0);
-        const i32x4 hi = *(const QG_LDS i32x4*)(blk + rd1);
-        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    auto finish_scale = [&](int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
+        if constexpr (FP4) {
+            sa[x] = (int)((uint32_t)sa[x] >> (8 * g));
+            sb[x] = (int)((uint32_t)sb[x] >> (8 * g));
+        }
     };
 
-    f32x4 acc[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    i32x8 ah[2][4], bh[2][4];
+    // per-lane operand read offsets: fp8 chunks q and q+4 of row l16 of a
+    // 16-row block; fp4 chunk 2s+g of row l32 of a 32-row block
+    const int rd8 = l16 * BKB + ((q ^ (l16 & 7)) << 4);
+    auto rd4 = [&](int s) __attribute__((always_inline)) {
+        return l32 * BKB + (((2 * s + g) ^ ((l32 >> 1) & 7)) << 4);
+    };
 
-    // fragment x of register half h of A (is_a) or B
+    Acc acc[NBLK][NBLK];
+#pragma unroll
+    for (int i = 0; i < NBLK; ++i)
+#pragma unroll
+        for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+            for (int v = 0; v < (FP4 ? 16 : 4); ++v) acc[i][j][v] = 0.f;
+    Frag ah[2][NF], bh[2][NF];
+
+    // read unit x (0..3) of register half h of A (is_a) or B: two
+    // ds_read_b128 -- fp8: the 16-row block x; fp4: sub-tiles 2(x%2) and
+    // 2(x%2)+1 of the 32-row block x/2
     auto read_one = [&](bool is_a, int h, int x, const QG_LDS uint8_t* sA,
                         const QG_LDS uint8_t* sB) __attribute__((always_inline)) {
-        if (is_a) ah[h][x] = read_frag(sA + (wm * 128 + (4 * h + x) * 16) * BKB);
-        else bh[h][x] = read_frag(sB + (wn * 128 + (4 * h + x) * 16) * BKB);
+        const QG_LDS uint8_t* base = is_a ? sA + wm * 128 * BKB : sB + wn * 128 * BKB;
+        Frag(&dst)[2][NF] = is_a ? ah : bh;
+        if constexpr (FP4) {
+            const QG_LDS uint8_t* blk = base + (2 * h + (x >> 1)) * 32 * BKB;
+            const int s0 = 2 * (x & 1);
+            dst[h][4 * (x >> 1) + s0] = *(const QG_LDS i32x4*)(blk + rd4(s0));
+            dst[h][4 * (x >> 1) + s0 + 1] = *(const QG_LDS i32x4*)(blk + rd4(s0 + 1));
+        } else {
+            const QG_LDS uint8_t* blk = base + (4 * h + x) * 16 * BKB;
+            const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd8);
+            const i32x4 hi = *(const QG_LDS i32x4*)(blk + (rd8 ^ 64));
+            dst[h][x] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
     };
     // quadrant (ha, hb): 16 MFMAs; after MFMA k, fill(k) issues this step's
     // share of LDS reads and DMAs.  Each step is fenced so the order stays
     // as written: the LDS reads and DMAs spread between MFMAs, and no read
     // of a register half moves above the last MFMA that uses its old rows.
+    // fp4 walks the 4 sub-tiles outermost, so consecutive MFMAs never chain
+    // on one accumulator.
     auto quadrant = [&](int ha, int hb, const int (&sa)[8], const int (&sb)[8],
                         auto&& fill) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
+        for (int k = 0; k < 16; ++k) {
+            if constexpr (FP4) {
+                const int s = k >> 2, bi = (k >> 1) & 1, bj = k & 1;
+                const int i = 2 * ha + bi, j = 2 * hb + bj;
+                if (s & 1)
+                    wide::mfma_fp4<true>(acc[i][j], bh[hb][4 * bj + s], ah[ha][4 * bi + s], sb[2 * j + (s >> 1)],
+                                         sa[2 * i + (s >> 1)]);
+                else
+                    wide::mfma_fp4<false>(acc[i][j], bh[hb][4 * bj + s], ah[ha][4 * bi + s], sb[2 * j + (s >> 1)],
+                                          sa[2 * i + (s >> 1)]);
+            } else {
+                const int i = k >> 2, j = k & 3;
                 wide::mfma_fp8(acc[4 * ha + i][4 * hb + j], bh[hb][j], ah[ha][i], sb[4 * hb + j], sa[4 * ha + i]);
-                __builtin_amdgcn_sched_barrier(0);
-                fill(4 * i + j);
-                __builtin_amdgcn_sched_barrier(0);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            fill(k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // One K-tile t in phase P = t % 4 (LDS stage P & 1 holds t and then
@@ -258,7 +351,7 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         constexpr int r1 = wide::shared_half(P, 1), r2 = wide::shared_half(P, 2), r0 = wide::shared_half(P, 0);
         __builtin_amdgcn_sched_barrier(0);
         // quadrant 1: K-tile t's two halves freed at the end of the previous
-        // K-tile, one fragment after each of the first 8 MFMAs
+        // K-tile, one read unit after each of the first 8 MFMAs
         quadrant(wide::qa(P), wide::qb(P), sa, sb, [&](int k) __attribute__((always_inline)) {
             if (k < 4) read_one(r1a, r1, k, sA, sB);
             else if (k < 8) read_one(r2a, r2, k - 4, sA, sB);
@@ -292,6 +385,7 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             if (k % 3 == 1) dma_op(11 + k / 3);
             if (k < 4) read_one(r1a, r1, k, nA, nB);
             if (k < 8) read_scale(t + 1, k, san, sbn);
+            else finish_scale(k - 8, san, sbn);
         });
     };
 
@@ -313,6 +407,8 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     }
 #pragma unroll
     for (int x = 0; x < 8; ++x) read_scale(0, x, s0a, s0b);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) finish_scale(x, s0a, s0b);
 
     int t = 0;
     for (; t + 4 <= nk; t += 4) {
@@ -329,9 +425,16 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     // tracking does not see: cover the MFMA-result-to-VALU-read latency
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
-    // ---- epilogue: lane holds C[m][n..n+3] for each (i, j) block ----
-    const int mrow0 = m0 + wm * 128 + l16;
-    const int ncol0 = n0 + wn * 128 + 4 * q;
+    // ---- epilogue ----
+    // Output element (r, c) of the wave's 128 x 128 block for accumulator
+    // element 4*v4 + e of block (i, j):
+    //   fp8: r = 16i + l16, c = 16j + 4q + e            (v4 = 0)
+    //   fp4: r = 32i + l32, c = 32j + 8*v4 + 4g + e     (v4 = 0..3)
+    auto out_row = [&](int i) __attribute__((always_inline)) { return FP4 ? 32 * i + l32 : 16 * i + l16; };
+    auto out_col = [&](int j, int v4) __attribute__((always_inline)) {
+        return FP4 ? 32 * j + 8 * v4 + 4 * g : 16 * j + 4 * q;
+    };
+    constexpr int NV4 = FP4 ? 4 : 1;
     const bool vec_ok = (LDC & 3) == 0;
     if (vec_ok && m0 + BM <= M && n0 + BM <= N) {
         if constexpr (BF16) {
@@ -343,15 +446,17 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             QG_LDS uint8_t* img = w == 0 ? pA0 : w == 1 ? pA1 : w == 2 ? pB0 : pB1;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int r = i * 16 + l16;
+            for (int i = 0; i < NBLK; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int c = (2 * j + (q >> 1)) ^ (r & 15);
-                    *(QG_LDS u32x2*)(img + r * 256 + c * 16 + (q & 1) * 8) =
-                        u32x2{pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
-                }
-            }
+                for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+                    for (int v4 = 0; v4 < NV4; ++v4) {
+                        const int r = out_row(i), cbyte = 2 * out_col(j, v4);
+                        const int c = (cbyte >> 4) ^ (r & 15);
+                        const Acc& a = acc[i][j];
+                        *(QG_LDS u32x2*)(img + r * 256 + c * 16 + (cbyte & 15)) =
+                            u32x2{pack_bf16x2(a[4 * v4], a[4 * v4 + 1]), pack_bf16x2(a[4 * v4 + 2], a[4 * v4 + 3])};
+                    }
             const int rr = L >> 4, cc = L & 15;
             uint16_t* cbase = (uint16_t*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128 + rr) * LDC +
                               n0 + wn * 128 + cc * 8;
@@ -362,41 +467,50 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
                 *(i32x4*)(cbase + (long long)u * 4 * LDC) = v;
             }
         } else {
+            float* cw = (float*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128) * LDC + n0 + wn * 128;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float* crow = (float*)p.c + (long long)bz * p.c_batch + (long long)(mrow0 + i * 16) * LDC + ncol0;
+            for (int i = 0; i < NBLK; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) *(f32x4*)(crow + j * 16) = acc[i][j];
-            }
+                for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+                    for (int v4 = 0; v4 < NV4; ++v4) {
+                        const Acc& a = acc[i][j];
+                        *(f32x4*)(cw + (long long)out_row(i) * LDC + out_col(j, v4)) =
+                            f32x4{a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]};
+                    }
         }
         return;
     }
+    // edge tiles: masked element stores
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int mm = mrow0 + i * 16;
+    for (int i = 0; i < NBLK; ++i) {
+        const int mm = m0 + wm * 128 + out_row(i);
         if (mm < M) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int nn = ncol0 + j * 16;
-                const f32x4 v = acc[i][j];
-                if constexpr (BF16) {
-                    uint16_t* crow = (uint16_t*)p.c + bz * p.c_batch + (long long)mm * LDC;
-                    if (vec_ok && nn + 3 < N) {
-                        *(u32x2*)(crow + nn) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+                for (int v4 = 0; v4 < NV4; ++v4) {
+                    const int nn = n0 + wn * 128 + out_col(j, v4);
+                    const Acc& a = acc[i][j];
+                    const f32x4 v = f32x4{a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]};
+                    if constexpr (BF16) {
+                        uint16_t* crow = (uint16_t*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                        if (vec_ok && nn + 3 < N) {
+                            *(u32x2*)(crow + nn) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        } else {
+                            for (int r = 0; r < 4; ++r)
+                                if (nn + r < N) crow[nn + r] = bf16_bits(v[r]);
+                        }
                     } else {
-                        for (int r = 0; r < 4; ++r)
-                            if (nn + r < N) crow[nn + r] = bf16_bits(v[r]);
-                    }
-                } else {
-                    float* crow = (float*)p.c + bz * p.c_batch + (long long)mm * LDC;
-                    if (vec_ok && nn + 3 < N) {
-                        *(f32x4*)(crow + nn) = v;
-                    } else {
-                        for (int r = 0; r < 4; ++r)
-                            if (nn + r < N) crow[nn + r] = v[r];
+                        float* crow = (float*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                        if (vec_ok && nn + 3 < N) {
+                            *(f32x4*)(crow + nn) = v;
+                        } else {
+                            for (int r = 0; r < 4; ++r)
+                                if (nn + r < N) crow[nn + r] = v[r];
+                        }
                     }
                 }
-            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
