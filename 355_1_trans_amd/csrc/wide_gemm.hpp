@@ -247,16 +247,20 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         } else if constexpr (MX) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
             const int ra = wm * 128 + (x >> 1) * 32 + l32, rb = wn * 128 + (x >> 1) * 32 + l32;
-            int oa, ob;
             if constexpr (PB == 16) {
-                oa = ra * 16 + (kt % SPAN) * KT_BYTES + (x & 1) * 4;
-                ob = rb * 16 + (kt % SPAN) * KT_BYTES + (x & 1) * 4;
+                // both words of the block in one read (x even; x odd is a no-op)
+                if ((x & 1) == 0) {
+                    const i32x2 va = *(const QG_LDS i32x2*)(pSA + buf + ra * 16 + (kt % SPAN) * KT_BYTES);
+                    const i32x2 vb = *(const QG_LDS i32x2*)(pSB + buf + rb * 16 + (kt % SPAN) * KT_BYTES);
+                    sa[x] = va[0];
+                    sa[x + 1] = va[1];
+                    sb[x] = vb[0];
+                    sb[x + 1] = vb[1];
+                }
             } else {
-                oa = (x & 1) * 1024 + ra * 4;
-                ob = (x & 1) * 1024 + rb * 4;
+                sa[x] = (int)*(const QG_LDS uint32_t*)(pSA + buf + (x & 1) * 1024 + ra * 4);
+                sb[x] = (int)*(const QG_LDS uint32_t*)(pSB + buf + (x & 1) * 1024 + rb * 4);
             }
-            sa[x] = (int)*(const QG_LDS uint32_t*)(pSA + buf + oa);
-            sb[x] = (int)*(const QG_LDS uint32_t*)(pSB + buf + ob);
         } else {
             const int st = kt & 1;
             sa[x] = pSA[st * 256 + wm * 128 + x * 16 + l16];
