@@ -2,22 +2,12 @@
 // the C ABI layer (abi.hip).  Each wrapper launches exactly one kernel.
 #pragma once
 #include <hip/hip_runtime.h>
-#include "tile_gemm.hpp"
+#include "tile_args.hpp"
 
 namespace qg {
 
-// kernels_tile.hip
-// wide_panels: MX scale rows are 16-byte aligned and K % 512 == 0, so the
-// kernel may move 16-byte scale panels (4 fp8 / 2 fp4 K-tiles per DMA).
-hipError_t launch_tile_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
-hipError_t launch_tile_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
-hipError_t launch_tile_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
-hipError_t launch_tile_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 
 // kernels_tile32.hip: the same tiles on the 32x32x64 scaled MFMA
-hipError_t launch_tile32_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
-hipError_t launch_tile32_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
-hipError_t launch_tile32_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 hipError_t launch_tile32_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);

@@ -33,9 +33,13 @@
 // tile (atomic counter) sums the partials in slice order, rounds and re-arms
 // the counter, all in the same launch.
 //
-// Register layout of the scaled MFMA (pinned by the layout probes): see
-// tile_gemm.hpp.  srcA = B fragment, srcB = A fragment; the accumulator of
-// lane L = 16q + r holds C[m = r][n = 4q .. 4q+3] of a 16 x 16 block.
+// Register layout of the scaled MFMA 16x16x128 (pinned by the layout probes,
+// probe.hip): operand lane L = 16q + r holds row r; fp8 dwords 0-3 carry K
+// [16q, 16q+16) and dwords 4-7 K [64+16q, 64+16q+16) (16-byte chunks q and
+// q+4 of a 128-byte row), fp4 dwords 0-3 carry K [32q, 32q+32) (chunk 2q, then
+// 2q+1 in the second instruction); lane group q's scale byte covers K [32q,
+// 32q+32).  srcA = B fragment, srcB = A fragment; the accumulator of lane
+// L = 16q + r holds C[m = r][n = 4q .. 4q+3] of a 16 x 16 block.
 //
 // B layouts: RAW [N][Kbytes]; KPANEL [K/128][N][128]; FRAG (this library's
 // B'' for the LDS-bypass entry): for every 16-row block nb and K-tile kt,
@@ -45,7 +49,7 @@
 #pragma once
 #include <utility>
 
-#include "tile_gemm.hpp"
+#include "tile_args.hpp"
 
 namespace qg {
 

@@ -1,10 +1,14 @@
 // LDS-staged tile GEMM for gfx950 on the scaled MFMA 32x32x64.
 //
-// Same tile, K pipeline and scale policies as tile_gemm.hpp (256 x 256 tile,
-// 8 wave64, 128-byte K-tiles moved global -> LDS by DMA into two stages),
-// but the matrix instruction is v_mfma_scale_f32_32x32x64_f8f6f4: on MI355X
-// it runs fp4 at about twice the rate of 16x16x128 (register-only
-// measurements: ~7.5-8 PF vs ~4.5-6 PF) and halves the MFMA count for fp8.
+// One workgroup of 8 wave64 (2 per SIMD) computes a 256 x 256 tile of C on
+// v_mfma_scale_f32_32x32x64_f8f6f4.  The K loop walks 128-byte K-tiles,
+// moved global -> LDS by DMA (global_load_lds_dwordx4) into two LDS stages:
+// the copy of K-tile t+1 is in flight while K-tile t is multiplied, and one
+// barrier per K-tile retires a stage.  The library runs the fp32 block-scale
+// policy (BSF32) here: its VALU rescale of every partial product keeps the
+// accumulators in VGPRs, which the 8-wave layout (128 accumulators per
+// wave) leaves room for; the MFMA-scaled policies run on the four-wave
+// kernel (wide_gemm.hpp).  Scale policies and B layouts: tile_args.hpp.
 //
 // Register layout (pinned by the layout probes, csrc/probe.hip):
 //   * operand lane L = 32g + r holds row r; lanes r and 32 + r split K;
@@ -29,7 +33,7 @@
 #pragma once
 #include <utility>
 
-#include "tile_gemm.hpp"
+#include "tile_args.hpp"
 
 namespace qg {
 
@@ -101,7 +105,9 @@ __global__ __launch_bounds__(512, 1) void tile32_gemm_kernel(const TileArgs p) {
     const int bz = blockIdx.z;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    // kernel arguments copied into locals once (see tile_gemm.hpp)
+    // kernel arguments copied into locals once: lambdas must not read the
+    // argument block inside the K loop (vector loads whose vmcnt wait would
+    // also drain the DMA queue)
     const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
     const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
 
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(512, 1) void tile32_gemm_kernel(const TileArgs p) {
         else boff[t] = (gn >> 4) * 16 * KB + (gn & 15) * 16 + c * 256;
     }
 
-    // ---- scale sources (as tile_gemm.hpp) ----
+    // ---- scale sources ----
     const int nblk_last = (N - 1) >> 7;
     const int wave_nblk = min((n0 >> 7) + ((wn * BLK_N * 32) >> 7), nblk_last);
     constexpr int MX_TASKS = 8;
@@ -311,8 +317,11 @@ __global__ __launch_bounds__(512, 1) void tile32_gemm_kernel(const TileArgs p) {
     QG_LDS uint8_t* pSB0 = (QG_LDS uint8_t*)lSB0;
     QG_LDS uint8_t* pSB1 = (QG_LDS uint8_t*)lSB1;
 
-    // K loop as in tile_gemm.hpp: one body with a runtime stage select,
-    // DMA(kt+1) right after the barrier that retires the reads of kt-1.
+    // One loop body with a runtime stage select keeps the accumulators
+    // resident (two copies of the body make the register allocator shuffle
+    // them).  DMA(kt+1) goes right after the barrier that retires the reads
+    // of kt-1; the barrier is s_barrier behind explicit waits, because
+    // __syncthreads() would also drain the DMA just issued.
     const int nk = KB / BKB;
     issue(0, pA0, pB0, pSA0, pSB0);
     for (int kt = 0; kt < nk; ++kt) {

@@ -1,0 +1,49 @@
+// Arguments, scale policies and B layouts shared by the tile kernels
+// (wide_gemm.hpp, tile32_gemm.hpp) and the skinny kernel (skinny_gemm.hpp).
+//
+// Scale policies (one K-tile = 128 bytes of K):
+//   MX    one E8M0 per 32 K elements, row-major [rows][K/32] (MX8 host.cc:282-285,
+//         MX4 host.cc:207-208).  A row's scales of one K-tile are 4 (fp8) or
+//         8 (fp4) bytes of a different cache line per row, so the tile kernels
+//         move them as 16-byte panels covering 4 (fp8) or 2 (fp4) K-tiles,
+//         double buffered: one L1 request per row per panel instead of per
+//         K-tile (narrow 4- or 8-byte panels when K % 512 != 0).
+//   BS8   one E8M0 per 128 K elements: SFA column-major [K/128][M], SFB
+//         [N/128][K/128] (SNAP gemm_a8w8_mxfp8_scale_common.h:28-35), broadcast
+//         to the four 32-element lane groups in the matrix core.
+//   BSF32 fp32 scales per 1x128 (A) and 128x128 (B) block (BPS host.cc:66-90):
+//         the MFMA runs unscaled (E8M0 127 = 1.0) into a fresh fp32 partial
+//         and the VALU adds partial * (sfa*sfb) into the accumulator, the
+//         reference's order of operations (scale each K-group, then sum).
+// B layouts: RAW [N][Kbytes]; KPANEL [Kbytes/128][N][128] (BPS host.cc:92-111);
+//            W16 shuffle_weight(16,16) [N/16][Kbytes/16][16][16] (SNAP host.cc:161-179).
+#pragma once
+#include "common.hpp"
+
+namespace qg {
+
+enum class ScaleKind : int { MX = 0, BS8 = 1, BSF32 = 2 };
+enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2 };
+
+struct TileArgs {
+    const uint8_t* a;
+    const uint8_t* b;
+    void* c;
+    const uint8_t* sfa;
+    const uint8_t* sfb;
+    int m, n;
+    int kbytes;          // bytes of K per row: K (fp8) or K/2 (fp4); multiple of 128
+    int lda, ldb;        // row pitch in bytes (ldb: RAW only)
+    int ldc;             // row pitch of C in elements
+    long long a_batch, b_batch, c_batch, sfa_batch, sfb_batch;  // batch strides (bytes / elements)
+    // scale addressing (in scale elements):
+    //   MX    : sfa(m, g) = sfa[m*sfa_sm + g], sfb(n, g) = sfb[n*sfb_sn + g]
+    //   BS8   : sfa(m, kt) = sfa[kt*sfa_sk + m], sfb(nb, kt) = sfb[nb*sfb_sn + kt]
+    //   BSF32 : sfa(m, kt) = sfa[kt*sfa_sk + m*sfa_sm], sfb(nb, kt) = sfb[nb*sfb_sn + kt]
+    int sfa_sm, sfa_sk, sfb_sn;
+    int tiles_m, tiles_n;
+    int group_m;         // tile-rows per raster group
+    int unit_scale;      // E8M0 127, passed at run time
+};
+
+}  // namespace qg

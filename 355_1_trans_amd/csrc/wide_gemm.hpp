@@ -37,12 +37,12 @@
 //    C[m = L%32][n = 8(v/4) + 4(L/32) + v%4].
 // Operand LDS rows are 128 bytes with 16-byte chunks XOR-swizzled per row
 // (fp8: r & 7; fp4: (r >> 1) & 7) so both the DMA writes and the fragment
-// reads are conflict free.  Scale policies (MX panels, BS8) are those of the
-// 8-wave tile kernel (tile_gemm.hpp).
+// reads are conflict free.  Scale policies (MX panels, BS8) and B layouts:
+// tile_args.hpp.
 #pragma once
 #include <type_traits>
 
-#include "tile_gemm.hpp"
+#include "tile_args.hpp"
 
 namespace qg {
 
