@@ -13,7 +13,7 @@
 
 #include "launch.hpp"
 #include "qgemm.h"
-#include "skinny_gemm.hpp"
+#include "decode_gemm.hpp"
 
 static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "reference kargs ABI");
@@ -137,11 +137,56 @@ static_assert(kSplitBelow <= 2 * kCUs, "counter block too small");
 
 struct Plan {
     bool skinny = false;
-    int mb = 1, nb = 1, m_tiles = 1, n_tiles = 1, splitk = 1, kt_per_split = 1;
+    bool decode = false;     // skinny shape with M <= 64 on an LDS-staged B layout
+    int mb = 1, nb = 1, nw = 8, m_tiles = 1, n_tiles = 1, splitk = 1, kt_per_split = 1;
     size_t ctr_bytes = 0, ws_bytes = 0;
 };
 
-Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny) {
+// Decode plan (M <= 64): workgroups of nw waves own 16*nw columns and all
+// rows.  K is split while the tiles leave more than half of the CUs idle,
+// keeping >= kDecodeMinKt K-tiles per slice and the fp32 partials below a
+// quarter of B's bytes; of 8 and 4 waves the one that puts more workgroups
+// in flight wins (8 on a tie: A is shared by more columns).
+constexpr int kDecodeMinKt = 8;
+
+void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_bytes) {
+    p.decode = true;
+    p.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    p.m_tiles = 1;
+    long long best = -1;
+    for (int nw : {8, 4}) {
+        const long long tiles = (long long)ceil_div(n, 16 * nw) * batch;
+        long long split = 1;
+        if (tiles < kCUs / 2) {
+            split = std::min<long long>(kCUs / tiles, k_tiles / kDecodeMinKt);
+            split = std::min<long long>(split, b_bytes / (16LL * m * n));
+            split = std::max<long long>(split, 1);
+        }
+        const int kt_per = ceil_div(k_tiles, (int)split);
+        const int sk = ceil_div(k_tiles, kt_per);
+        const long long wgs = tiles * sk;
+        if (wgs > best) {
+            best = wgs;
+            p.nw = nw;
+            p.n_tiles = ceil_div(n, 16 * nw);
+            p.kt_per_split = kt_per;
+            p.splitk = sk;
+        }
+    }
+    if (p.splitk > 1) {
+        p.ctr_bytes = kCounterBytes;    // split only below kCUs / 2 tiles
+        p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
+    } else {
+        p.kt_per_split = k_tiles;
+    }
+}
+
+// decode_ok: the B layout can go through the decode kernel's LDS stages.
+// The decode kernel (waves split N, A shared through LDS) runs the fp8
+// decode shapes whose N is too narrow for the skinny kernel without a K
+// split; with enough N tiles the skinny kernel (waves split K) streams
+// row-major B with better DRAM page locality and needs no split.
+Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny, bool decode_ok = true) {
     Plan p;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
     p.skinny = force_skinny || (m <= 256 && tiles256 < 128);
@@ -155,6 +200,10 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
         if ((long long)p.n_tiles * p.m_tiles * batch >= kMinTiles) break;
     }
     const long long base = (long long)p.n_tiles * p.m_tiles * batch;
+    if (decode_ok && m <= 64 && base < kSplitBelow) {
+        plan_decode(p, m, n, k_tiles, batch, b_bytes);
+        return p;
+    }
     if (base >= kSplitBelow) return p;
     long long split = kCUs / base;
     split = std::min<long long>(split, k_tiles / 16);
@@ -169,20 +218,35 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
     return p;
 }
 
-// Launches the skinny kernel.  A NULL workspace runs one K slice (no
-// partials); a non-NULL one must hold plan.ws_bytes and be 256-byte aligned.
+// Launches the skinny or decode kernel.  A NULL workspace runs one K slice
+// (no partials); a non-NULL one must hold plan.ws_bytes and be 256-byte
+// aligned.
 hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bool bf16, void* ws,
                       size_t ws_bytes, int k_tiles, hipStream_t stream) {
-    SkinnyArgs s{};
-    s.t = t;
+    unsigned* counters = nullptr;
+    float* partials = nullptr;
     if (pl.splitk > 1 && ws) {
         if (ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return hipErrorInvalidValue;
-        s.counters = static_cast<unsigned*>(ws);
-        s.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl.ctr_bytes);
+        counters = static_cast<unsigned*>(ws);
+        partials = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl.ctr_bytes);
     } else {
         pl.splitk = 1;
         pl.kt_per_split = k_tiles;
     }
+    if (pl.decode) {
+        qg::DecodeArgs d{};
+        d.t = t;
+        d.ws = partials;
+        d.counters = counters;
+        d.splitk = pl.splitk;
+        d.kt_per_split = pl.kt_per_split;
+        d.n_tiles = pl.n_tiles;
+        return qg::launch_decode(kind, d, pl.mb, pl.nw, batch, bf16, stream);
+    }
+    SkinnyArgs s{};
+    s.t = t;
+    s.counters = counters;
+    s.ws = partials;
     s.splitk = pl.splitk;
     s.kt_per_split = pl.kt_per_split;
     s.n_tiles = pl.n_tiles;
@@ -333,7 +397,7 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false);
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false);
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);
     return qg::launch_wide_mx4_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
@@ -341,7 +405,7 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
 
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false).ws_bytes;
+    return plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false, false).ws_bytes;
 }
 
 // ------------------------------------------------ block-scale FP8, E8M0 scales
@@ -436,14 +500,14 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bpp, true);
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bpp, true, false);
     return run_skinny(SkinnyKind::BSF32_FRAG, t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, workspace,
                       workspace_bytes, a.k / 128, stream);
 }
 
 size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), true)
+    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), true, false)
         .ws_bytes;
 }
 

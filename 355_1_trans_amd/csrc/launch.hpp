@@ -20,6 +20,9 @@ enum class SkinnyKind : int { MX8_RAW, MX4_RAW, BSF32_KPANEL, BSF32_FRAG };
 hipError_t launch_skinny(SkinnyKind kind, const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s);
 hipError_t launch_skinny_mx8(const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s);
 hipError_t launch_skinny_mx4(const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s);
+// kernels_decode.hip: decode kernel (M <= 64, mb row blocks, nw waves of 16 columns)
+struct DecodeArgs;
+hipError_t launch_decode(SkinnyKind kind, const DecodeArgs& a, int mb, int nw, int batch, bool bf16, hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);

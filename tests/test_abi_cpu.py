@@ -88,13 +88,17 @@ def test_workspace_queries(qgemm):
     L = qgemm.lib()
     # large M runs the 256 x 256 tile kernel: no workspace
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=8192, n=8192, k=8192))) == 0
-    # decode with few 16-column tiles splits K: 2 KB of counters + splitk * M * N fp32 partials
-    for m, n, k in [(1, 1536, 7168), (32, 1536, 7168), (4, 1000, 7168)]:
+    # decode (M <= 64) with too few N tiles for the skinny kernel: the decode
+    # kernel splits K -- 2 KB of counters + splitk * M * N fp32 partials
+    for m, n, k in [(1, 1536, 7168), (32, 1536, 7168), (4, 1000, 7168), (64, 1536, 7168)]:
         a = _kargs(qgemm, m=m, n=n, k=k)
         ws = L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(a))
         assert ws >= 2048 + 2 * m * n * 4 and (ws - 2048) % (m * n * 4) == 0, (m, n, k, ws)
-    # enough N tiles: no split
+    # enough N tiles for the skinny kernel -> no split
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=7168, k=16384))) == 0
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=4096))) == 0
+    # too few K-tiles to split (8 per slice at least)
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=1536, k=1024))) == 0
     assert L.gemm_a8w8_mxfp8_workspace_bytes(None) == 0
     # fp4 K-tiles hold 256 elements: K = 16384 gives 64 of them, enough for 16-tile slices
     assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=1536, k=16384))) > 0
