@@ -19,8 +19,12 @@ def _fp8(x, dev):
 
 
 # ----------------------------------------------------------------- MXFP8
+# M <= 64 with too few N tiles for the skinny kernel runs the decode kernel
+# (rows 1..64 in 1, 2 or 4 blocks; 64- or 128-column workgroups; split-K),
+# the rest the skinny kernel
 MX8_DECODE = [(1, 2112, 7168), (8, 1024, 2048), (16, 7168, 512), (17, 1000, 1024), (33, 4096, 1024),
-              (64, 2112, 7168), (128, 1536, 2048), (256, 512, 1024)]
+              (64, 2112, 7168), (128, 1536, 2048), (256, 512, 1024),
+              (1, 1536, 7168), (40, 1200, 4096), (64, 1536, 7168), (5, 300, 26624)]
 
 
 @pytest.mark.parametrize("m,n,k", MX8_DECODE)
@@ -83,6 +87,7 @@ def test_mxfp4_skinny(qgemm, gpu, m, n, k, split):
 
 # ----------------------------------------------- block-scale, fp32 scales
 BS_DECODE = [(1, 2112, 7168), (1, 7168, 2048), (4, 24576, 1536), (32, 2112, 7168), (48, 300, 1024),
+             (32, 1536, 7168), (64, 1536, 7168), (17, 1000, 4096), (2, 200, 26624),
              (64, 7168, 512), (128, 4096, 1024)]
 
 
