@@ -468,10 +468,9 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
     if (pl.skinny)
         return run_skinny(SkinnyKind::BSF32_KPANEL, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128,
                           stream);
-    // fp32 block scales run the 32x32x64 tile kernel: its partial products
-    // need half the MFMA issues per rescale and measure ~10% faster at
-    // 8192^3; the MX and E8M0 scale paths are faster on the 16x16x128 kernel
-    return qg::launch_tile32_bsf32_kpanel(t, a.batch, bf16, stream);
+    // fp32 block scales: the eight-wave kernel with VGPR accumulators and a
+    // VALU rescale per K-tile (bsf32_gemm.hpp)
+    return qg::launch_bsf32_kpanel(t, a.batch, bf16, stream);
 }
 
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {

@@ -7,8 +7,8 @@
 namespace qg {
 
 
-// kernels_tile32.hip: the same tiles on the 32x32x64 scaled MFMA
-hipError_t launch_tile32_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+// kernels_bsf32.hip: eight-wave 256 x 256 tiles, fp32 block scales (B in K-panel layout)
+hipError_t launch_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
 hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);

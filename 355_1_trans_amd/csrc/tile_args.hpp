@@ -1,5 +1,5 @@
 // Arguments, scale policies and B layouts shared by the tile kernels
-// (wide_gemm.hpp, tile32_gemm.hpp) and the skinny kernel (skinny_gemm.hpp).
+// (wide_gemm.hpp, bsf32_gemm.hpp) and the skinny kernel (skinny_gemm.hpp).
 //
 // Scale policies (one K-tile = 128 bytes of K):
 //   MX    one E8M0 per 32 K elements, row-major [rows][K/32] (MX8 host.cc:282-285,

@@ -145,3 +145,16 @@ def test_blockscale_fp32(qgemm, gpu, m, n, k, sfa_layout):
         A_scale = to_dev(np.ascontiguousarray(sa.T), None, gpu).t()
     y = qgemm.gemm_a8w8_bpreshuffle(A, Bk, A_scale, to_dev(sb, None, gpu), dtype=torch.bfloat16)
     assert_close(ref, out_to_f32(y), f"bs-fp32 {m}x{n}x{k} {sfa_layout}")
+
+
+# tile-kernel cases: one K-tile, an odd K-tile count (the loop runs two
+# K-tiles per iteration), whole and ragged tiles, fp32 output
+@pytest.mark.parametrize("m,n,k", [(520, 300, 128), (264, 1000, 640), (512, 512, 1408), (768, 256, 256)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_blockscale_fp32_tile(qgemm, gpu, m, n, k, dtype):
+    qa, qb, sa, sb = make_bs(m, n, k, seed=3 * m + n + k)
+    ref = O.gemm_bs_fp32(qa, qb, sa, sb)
+    A = to_dev(qa, None, gpu).view(torch.float8_e4m3fn)
+    Bk = qgemm.shuffle_b_kpanel(to_dev(qb, None, gpu)).view(torch.float8_e4m3fn)
+    y = qgemm.gemm_a8w8_bpreshuffle(A, Bk, to_dev(sa, None, gpu), to_dev(sb, None, gpu), dtype=dtype)
+    assert_close(ref, out_to_f32(y), f"bs-fp32 tile {m}x{n}x{k} {dtype}")

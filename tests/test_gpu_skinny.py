@@ -157,7 +157,7 @@ def test_mxfp8_batched(qgemm, gpu, m, n, k):
         assert_close(O.gemm_mx8(*d), C[i].cpu().numpy(), f"batch {i}")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 2112, 2048), (24, 640, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1, 2112, 2048), (24, 640, 1024), (300, 520, 384)])
 def test_blockscale_fp32_batched(qgemm, gpu, m, n, k):
     batch = 2
     data = [make_bs(m, n, k, seed=70 + i) for i in range(batch)]
