@@ -157,7 +157,7 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
     for (int nw : {8, 4}) {
         const long long tiles = (long long)ceil_div(n, 16 * nw) * batch;
         long long split = 1;
-        if (tiles < kCUs / 2) {
+        if (tiles < kCUs / 2 && (long long)m * n < (1LL << 29)) {    // partial offsets are 32-bit bytes
             split = std::min<long long>(kCUs / tiles, k_tiles / kDecodeMinKt);
             split = std::min<long long>(split, b_bytes / (16LL * m * n));
             split = std::max<long long>(split, 1);
@@ -205,6 +205,7 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
         return p;
     }
     if (base >= kSplitBelow) return p;
+    if ((long long)m * n >= (1LL << 29)) return p;    // partial offsets are 32-bit bytes
     long long split = kCUs / base;
     split = std::min<long long>(split, k_tiles / 16);
     split = std::min<long long>(split, b_bytes / (16LL * m * n));

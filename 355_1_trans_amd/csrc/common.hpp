@@ -52,6 +52,33 @@ __device__ __forceinline__ void dma4_buf(__amdgpu_buffer_rsrc_t r, QG_LDS void* 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 4, voff, soff, 0, 0);
 }
 
+// Split-K partial tiles cross workgroups that run on different XCDs, whose
+// L2 caches are not coherent with each other.  An acquire/release counter
+// would cost a write-back of the whole L2 before the atomic and an L2
+// invalidate after it; instead the partials are written and read with
+// device-coherent accesses (cache policy sc1: the instructions the compiler
+// emits for relaxed agent-scope atomic stores and loads), the counter is a
+// relaxed agent-scope atomic issued only after every partial store of the
+// workgroup has completed (s_waitcnt vmcnt(0), then a barrier), and the
+// last workgroup reads the partials only after its atomic has returned.
+constexpr int kCoherent = 16;    // buffer-instruction cache policy: sc1
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ void store_partial4(__amdgpu_buffer_rsrc_t r, int elem, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, elem * 4, 0, kCoherent);
+}
+__device__ __forceinline__ void store_partial1(__amdgpu_buffer_rsrc_t r, int elem, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, elem * 4, 0, kCoherent);
+}
+__device__ __forceinline__ f32x4 load_partial4(__amdgpu_buffer_rsrc_t r, int elem) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, elem * 4, 0, kCoherent));
+}
+__device__ __forceinline__ float load_partial1(__amdgpu_buffer_rsrc_t r, int elem) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, elem * 4, 0, kCoherent));
+}
+
 // fp32 -> bf16 with round-to-nearest-even (the rounding the reference
 // validates against, SNAP host.cc:185-193): v_cvt_pk_bf16_f32 converts two
 // values per instruction in hardware.

@@ -284,56 +284,63 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
     }
 
     // split-K: store this slice's partial tile; the last workgroup of the
-    // tile sums all slices in slice order.  Publication is one acq_rel
-    // counter atomic per workgroup, after a barrier that follows every
-    // wave's stores.
+    // tile sums all slices in slice order.  Publication: device-coherent
+    // partial stores, completed before a barrier, then one relaxed counter
+    // atomic per workgroup (see store_partial4 in common.hpp).
     const long long plane = (long long)M * N;
     const int batch = gridDim.z;
     const long long split_stride = (long long)batch * plane;
-    float* part = dp.ws + ((long long)sk * batch + bz) * plane;
+    const auto part = partial_rsrc(dp.ws + ((long long)sk * batch + bz) * plane);
     const bool vec_ok = (N & 3) == 0;
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
         const int m = i * 16 + l16;
         if (m >= M) continue;
-        float* dst = part + (long long)m * N + n;
+        const int e = m * N + n;
         if (n + 3 < N && vec_ok) {
-            *(f32x4*)dst = acc[i];
+            store_partial4(part, e, acc[i]);
         } else {
             for (int r = 0; r < 4; ++r)
-                if (n + r < N) dst[r] = acc[i][r];
+                if (n + r < N) store_partial1(part, e + r, acc[i][r]);
         }
     }
     wait_vmcnt<0>();
     __syncthreads();
     unsigned* ctr = dp.counters + (long long)bz * dp.n_tiles + nt;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                     (unsigned)(dp.splitk - 1);
     __syncthreads();
     if (!last_flag) return;
     const float* ws0 = dp.ws + (long long)bz * plane;
-    for (int e = tid * 4; e < ROWS * COLS; e += NT * 4) {
-        const int row = e / COLS, col = e % COLS;
+    // MB passes of 4 columns per thread, unrolled so that every pass's
+    // partial loads are in flight together
+    static_assert(ROWS * COLS == MB * NT * 4, "reduction passes");
+#pragma unroll
+    for (int it = 0; it < MB; ++it) {
+        const int x = tid * 4 + it * NT * 4;
+        const int row = x / COLS, col = x % COLS;
         const int m = row, nn = n0 + col;
         if (m >= M) continue;
-        const float* src = ws0 + (long long)m * N + nn;
+        const int e = m * N + nn;
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
         if (nn + 3 < N && vec_ok) {
             for (int s0 = 0; s0 < dp.splitk; s0 += 8) {
                 f32x4 u[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
-                    if (s0 + t < dp.splitk) u[t] = *(const f32x4*)(src + (s0 + t) * split_stride);
+                    if (s0 + t < dp.splitk) u[t] = load_partial4(partial_rsrc(ws0 + (s0 + t) * split_stride), e);
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
                     if (s0 + t < dp.splitk)
                         for (int r = 0; r < 4; ++r) v[r] += u[t][r];
             }
         } else {
-            for (int s0 = 0; s0 < dp.splitk; ++s0)
+            for (int s0 = 0; s0 < dp.splitk; ++s0) {
+                const auto src = partial_rsrc(ws0 + s0 * split_stride);
                 for (int r = 0; r < 4; ++r)
-                    if (nn + r < N) v[r] += src[s0 * split_stride + r];
+                    if (nn + r < N) v[r] += load_partial1(src, e + r);
+            }
         }
         // the thread's 4 columns start at nn
         if constexpr (BF16) {

@@ -392,32 +392,31 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     }
 
     // split-K: store this slice's partial tile, then the last workgroup of
-    // the tile reduces all slices in order 0..splitk-1.  Publication is one
-    // acq_rel counter atomic per workgroup (its L2 write-back / invalidate
-    // is what makes the partials visible across XCDs); every wave's stores
-    // have completed before the barrier that precedes it.
+    // the tile reduces all slices in order 0..splitk-1.  Publication:
+    // device-coherent partial stores, completed before a barrier, then one
+    // relaxed counter atomic per workgroup (see store_partial4, common.hpp).
     const long long plane = (long long)M * N;
     const int batch = gridDim.z;
     const long long split_stride = (long long)batch * plane;
-    float* part = sp.ws + ((long long)sk * batch + bz) * plane;
+    const auto part = partial_rsrc(sp.ws + ((long long)sk * batch + bz) * plane);
     const bool vec_ok = (N & 3) == 0;
     for (int e = tid * 4; e < ROWS * COLS; e += NT * 4) {
         const int m = m0 + e / COLS, n = n0 + e % COLS;
         if (m >= M) continue;
         const f32x4 v = tile_sum(e);
-        float* dst = part + (long long)m * N + n;
+        const int x = m * N + n;
         if (n + 3 < N && vec_ok) {
-            *(f32x4*)dst = v;
+            store_partial4(part, x, v);
         } else {
             for (int r = 0; r < 4; ++r)
-                if (n + r < N) dst[r] = v[r];
+                if (n + r < N) store_partial1(part, x + r, v[r]);
         }
     }
     wait_vmcnt<0>();
     __syncthreads();
     unsigned* ctr = sp.counters + ((long long)bz * sp.m_tiles + mt) * sp.n_tiles + nt;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                     (unsigned)(sp.splitk - 1);
     __syncthreads();
     if (!last_flag) return;
@@ -426,7 +425,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
         const int row = e / COLS, col = e % COLS;
         const int m = m0 + row, n = n0 + col;
         if (m >= M) continue;
-        const float* src = ws0 + (long long)m * N + n;
+        const int x = m * N + n;
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
         if (n + 3 < N && vec_ok) {
             // eight slices in flight per batch of loads, summed in slice order
@@ -434,16 +433,18 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
                 f32x4 u[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
-                    if (s0 + t < sp.splitk) u[t] = *(const f32x4*)(src + (s0 + t) * split_stride);
+                    if (s0 + t < sp.splitk) u[t] = load_partial4(partial_rsrc(ws0 + (s0 + t) * split_stride), x);
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
                     if (s0 + t < sp.splitk)
                         for (int r = 0; r < 4; ++r) v[r] += u[t][r];
             }
         } else {
-            for (int s0 = 0; s0 < sp.splitk; ++s0)
+            for (int s0 = 0; s0 < sp.splitk; ++s0) {
+                const auto src = partial_rsrc(ws0 + s0 * split_stride);
                 for (int r = 0; r < 4; ++r)
-                    if (n + r < N) v[r] += src[s0 * split_stride + r];
+                    if (n + r < N) v[r] += load_partial1(src, x + r);
+            }
         }
         store4(row, col, v);
     }
