@@ -471,7 +471,7 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
                           stream);
     // fp32 block scales: the eight-wave kernel with VGPR accumulators and a
     // VALU rescale per K-tile (bsf32_gemm.hpp)
-    return qg::launch_bsf32_kpanel(t, a.batch, bf16, stream);
+    return qg::launch_bsf32(t, a.batch, bf16, false, stream);
 }
 
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {
@@ -500,14 +500,17 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bpp, true, false);
+    // small M: the skinny kernel streams B'' straight into registers; large
+    // M: the eight-wave tile kernel stages B'' blocks through LDS like B'
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bpp, false, false);
+    if (!pl.skinny) return qg::launch_bsf32(t, a.batch, out_dtype == QGEMM_OUT_BF16, true, stream);
     return run_skinny(SkinnyKind::BSF32_FRAG, t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, workspace,
                       workspace_bytes, a.k / 128, stream);
 }
 
 size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), true, false)
+    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), false, false)
         .ws_bytes;
 }
 

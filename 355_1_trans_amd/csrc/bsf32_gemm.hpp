@@ -63,8 +63,10 @@ __device__ __forceinline__ f32x4 mfma_part(const i32x8& b, const i32x8& a) {
 }
 }  // namespace bsf
 
-template <bool BF16>
+template <bool BF16, BLay BL>
 __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
+    static_assert(BL == BLay::KPANEL || BL == BLay::FRAG, "K-panel B' or fragment-order B''");
+    constexpr bool FRAG = (BL == BLay::FRAG);
     constexpr int BKB = 128, BM = 256;
     constexpr int A_BYTES = BM * BKB;       // 32 KB
     constexpr int SA_OFF = A_BYTES;         // 256 fp32 row scales
@@ -103,9 +105,11 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     const int wm = w >> 1, wn = w & 1;
     const int q = L >> 4, l16 = L & 15;
 
+    const int nk = KB / BKB;
     const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
-    // B in K-panel layout: K-tile kt is [N][128 B] at kt * N * 128
-    const uint8_t* B = p.b + bz * p.b_batch + (long long)n0 * BKB;
+    // B' (K-panel): K-tile kt is [N][128 B] at kt * N * 128.  B'' (FRAG):
+    // block nb of 16 rows, K-tile kt at (nb * nk + kt) * 2048
+    const uint8_t* B = p.b + bz * p.b_batch + (FRAG ? (long long)(n0 >> 4) * nk * 2048 : (long long)n0 * BKB);
     const uint8_t* SFA = p.sfa + 4ll * bz * p.sfa_batch;
     const uint8_t* SFB = p.sfb + 4ll * bz * p.sfb_batch;
 
@@ -125,17 +129,26 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
             aoff[pt][u] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
             adst[pt][u] = r0 * BKB;
         }
-    // B half jh, DMA u of wave w: slot rows 8(2w + u) + L/8; slot row s holds
-    // tile column (s / 64) * 128 + jh * 64 + s % 64
+    // B half jh, DMA u of wave w fills slot bytes [1024 (2w + u), +1024):
+    //  B': slot rows 8(2w + u) + L/8; slot row s holds tile column
+    //      (s / 64) * 128 + jh * 64 + s % 64;
+    //  B'': half u of the 2 KB operand block of slot block w (16 slot rows,
+    //      the same columns), copied as is
     int boff[2][2];
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int s = (2 * w + u) * 8 + (L >> 3);
-            const int n = (s >> 6) * 128 + jh * 64 + (s & 63);
-            const int c = (L & 7) ^ (s & 7);
-            boff[jh][u] = (min(n0 + n, N - 1) - n0) * BKB + c * 16;
+            if constexpr (FRAG) {
+                const int tb = (w >> 2) * 8 + jh * 4 + (w & 3);    // 16-column block of the tile
+                const int nb = min((n0 >> 4) + tb, ((N + 15) >> 4) - 1) - (n0 >> 4);
+                boff[jh][u] = nb * nk * 2048 + u * 1024 + L * 16;
+            } else {
+                const int s = (2 * w + u) * 8 + (L >> 3);
+                const int n = (s >> 6) * 128 + jh * 64 + (s & 63);
+                const int c = (L & 7) ^ (s & 7);
+                boff[jh][u] = (min(n0 + n, N - 1) - n0) * BKB + c * 16;
+            }
         }
     // scales: waves 0-3 move the fp32 row scales of A rows [64w, 64w + 64)
     // (lane L: row 64w + L); wave 4 + j the weight scale of the tile's
@@ -158,7 +171,6 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
         return s == 0 ? pB0 : s == 1 ? pB1 : s == 2 ? pB2 : pB3;
     };
 
-    const int nk = KB / BKB;
     auto rsrc = [&](const uint8_t* base, bool valid) __attribute__((always_inline)) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
                                                  0x00020000);
@@ -177,7 +189,7 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
         Src s;
         s.sc = rsrc(sc_base + ka * sc_kstride, ka < nk);
         s.a = rsrc(A + (long long)ka * BKB, ka < nk);
-        s.b = rsrc(B + (long long)kb * N * BKB, kb < nk);
+        s.b = rsrc(B + (FRAG ? (long long)kb * 2048 : (long long)kb * N * BKB), kb < nk);
         return s;
     };
     auto dma = [&](auto HPC, const Src& s, int d) __attribute__((always_inline)) {
@@ -211,10 +223,18 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     i32x8 af[4], bf[2];
     f32x4 part[2];
     float fs[4] = {0.f, 0.f, 0.f, 0.f};
+    // fragment of a 16-row block: chunks q and q+4 of row l16, swizzled rows
+    // (A, B'); B'' blocks hold the operand order itself (lane L at 16 L)
     const int rd8 = l16 * BKB + ((q ^ (l16 & 7)) << 4);
+    const int rdb0 = FRAG ? L * 16 : rd8, rdb1 = FRAG ? 1024 + L * 16 : rd8 ^ 64;
     auto ld_frag = [&](const QG_LDS uint8_t* blk) __attribute__((always_inline)) -> i32x8 {
         const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd8);
         const i32x4 hi = *(const QG_LDS i32x4*)(blk + (rd8 ^ 64));
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    auto ld_bfrag = [&](const QG_LDS uint8_t* blk) __attribute__((always_inline)) -> i32x8 {
+        const i32x4 lo = *(const QG_LDS i32x4*)(blk + rdb0);
+        const i32x4 hi = *(const QG_LDS i32x4*)(blk + rdb1);
         return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
     // acc[i][jj] += part[x] * fs[i]
@@ -251,7 +271,7 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
                 __builtin_amdgcn_sched_barrier(0);
                 rescale((d + 3) & 3, JP + (d == 0 ? 2 : 3), (d + 1) & 1);
             }
-            if (d == 0) bf[0] = ld_frag(sB);
+            if (d == 0) bf[0] = ld_bfrag(sB);
             if constexpr (JH == 0) {
                 af[d] = ld_frag(sA + 16 * d * BKB);
                 if (d == 3) {
@@ -268,7 +288,7 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
 #pragma unroll
         for (int k = 0; k < 12; ++k) {
             const int j = k >> 2, i = k & 3;
-            if (i == 0) bf[(j + 1) & 1] = ld_frag(sB + (j + 1) * 16 * BKB);
+            if (i == 0) bf[(j + 1) & 1] = ld_bfrag(sB + (j + 1) * 16 * BKB);
             part[k & 1] = bsf::mfma_part(bf[j & 1], af[i]);
             __builtin_amdgcn_sched_barrier(0);
             if (k == 0) {

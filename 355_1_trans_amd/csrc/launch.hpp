@@ -7,8 +7,9 @@
 namespace qg {
 
 
-// kernels_bsf32.hip: eight-wave 256 x 256 tiles, fp32 block scales (B in K-panel layout)
-hipError_t launch_bsf32_kpanel(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+// kernels_bsf32.hip: eight-wave 256 x 256 tiles, fp32 block scales; B' (K-panel) or,
+// with frag, B'' (the LDS-bypass entry's fragment order)
+hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
 hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);

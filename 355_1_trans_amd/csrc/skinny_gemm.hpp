@@ -53,7 +53,7 @@
 
 namespace qg {
 
-constexpr BLay kBFrag = static_cast<BLay>(3);
+constexpr BLay kBFrag = BLay::FRAG;
 constexpr int kSkinnyWaves = 8;
 
 struct SkinnyArgs {

@@ -16,14 +16,16 @@
 //         and the VALU adds partial * (sfa*sfb) into the accumulator, the
 //         reference's order of operations (scale each K-group, then sum).
 // B layouts: RAW [N][Kbytes]; KPANEL [Kbytes/128][N][128] (BPS host.cc:92-111);
-//            W16 shuffle_weight(16,16) [N/16][Kbytes/16][16][16] (SNAP host.cc:161-179).
+//            W16 shuffle_weight(16,16) [N/16][Kbytes/16][16][16] (SNAP host.cc:161-179);
+//            FRAG this library's B'' for the LDS-bypass entry: per 16-row block and
+//            128-byte K-tile, 2048 contiguous bytes in 16x16x128 operand order.
 #pragma once
 #include "common.hpp"
 
 namespace qg {
 
 enum class ScaleKind : int { MX = 0, BS8 = 1, BSF32 = 2 };
-enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2 };
+enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2, FRAG = 3 };
 
 struct TileArgs {
     const uint8_t* a;

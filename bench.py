@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--m", type=int, default=None, help="override M (decode sweeps)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--sweep", action="store_true",
+                   help="BASELINE configs[2]: time the block-scale shape sweep (bpreshuffle and ldsbypass), "
+                        "one JSON line per shape")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run only a plain 256 MiB device copy 5 times (PMC byte-counter calibration)")
     return p.parse_args()
@@ -68,6 +71,125 @@ def traffic_from_profiles(kernel_tag):
         return None
     m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
     return float(m.group(1)) if m else None
+
+
+SWEEP_M = (1, 16, 64, 256, 1024, 4096, 16384)
+SWEEP_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168))
+
+
+def _gpu_quant_bs(rows, k, block_rows, gen, dev):
+    """N(0,1) data quantized to e4m3 with one fp32 scale (amax / 448) per
+    block_rows x 128 block, on the GPU (the sweep's operands are too large for
+    the host quantizer to be quick); returns (uint8 [rows, k], fp32 scales
+    [ceil(rows / block_rows), k / 128])."""
+    import torch
+    rp = -(-rows // block_rows) * block_rows
+    x = torch.randn((rp, k), generator=gen, device=dev)
+    blk = x.view(rp // block_rows, block_rows, k // 128, 128)
+    sc = blk.abs().amax(dim=(1, 3)).clamp_min(1e-12) / 448.0
+    qx = (blk / sc[:, None, :, None]).to(torch.float8_e4m3fn).view(rp, k)[:rows]
+    return qx.contiguous().view(torch.uint8), sc.contiguous()
+
+
+def _time_calls(calls, ws, stream, graph_mode, steps, warmup):
+    """Average launch time (ms) of `steps` launches cycling through `calls`:
+    back-to-back launches, or (graph_mode) one HIP graph replay of them."""
+    import torch
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    def launch(i):
+        fn, ka = calls[i % len(calls)]
+        st = fn(ctypes.byref(ka), 1, ws.data_ptr(), ws.numel(), sptr)
+        if st:
+            raise RuntimeError(f"{fn.__name__} failed: HIP error {st}")
+
+    with torch.cuda.stream(stream):
+        launch(0)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    if graph_mode:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                launch(i)
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                launch(i)
+            graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        e1.record(stream)
+    else:
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                launch(i)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            for i in range(steps):
+                launch(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def sweep(args):
+    """M x (N, K) for both block-scale entry points.
+    HBM-bound shapes (M <= 256) replay a graph over rotating weight copies
+    (> 512 MB, beyond the last-level cache); the others launch back to back."""
+    import torch
+    q = importlib.import_module("355_1_trans_amd")
+    L = q.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    stream = torch.cuda.Stream(dev)
+    for n, k in SWEEP_NK:
+        qb, sb = _gpu_quant_bs(n, k, 128, gen, dev)
+        bk = q.shuffle_b_kpanel(qb)
+        bpp = q.ldsbypass_repack(bk)
+        kg = k // 128
+        for m in SWEEP_M:
+            qa, sa = _gpu_quant_bs(m, k, 1, gen, dev)
+            C = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            hbm = m <= 256
+            for variant, B0 in (("bpreshuffle", bk), ("ldsbypass", bpp)):
+                b_bytes = B0.numel() + sb.numel() * 4
+                copies = max(2, ROTATE_BYTES // b_bytes + 1) if hbm else 1
+                Bs = [B0] + [B0.clone() for _ in range(copies - 1)]
+                SBs = [sb] + [sb.clone() for _ in range(copies - 1)]
+                calls = []
+                for B, SB in zip(Bs, SBs):
+                    if variant == "bpreshuffle":
+                        ka = q.Kargs(qa.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, 1, k, 128, n, m * k, n * k,
+                                     m * n, sa.data_ptr(), SB.data_ptr(), 1 if m > 1 else m, kg, m * kg, SB.numel())
+                        fn, wq = L.gemm_a8w8_blockscale_bpreshuffle, L.gemm_a8w8_blockscale_bpreshuffle_workspace_bytes
+                    else:
+                        ka = q.LdsBypassKargs(qa.data_ptr(), None, B.data_ptr(), C.data_ptr(), m, n, k, 1, k, 128, n,
+                                              m * k, n * k, m * n, sa.data_ptr(), SB.data_ptr(), 1 if m > 1 else m, kg,
+                                              m * kg, SB.numel(), B.numel())
+                        fn, wq = L.gemm_a8w8_blockscale_ldsbypass, L.gemm_a8w8_blockscale_ldsbypass_workspace_bytes
+                    calls.append((fn, ka))
+                wsb = max(1, wq(ctypes.byref(calls[0][1])))
+                ws = torch.zeros((wsb + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+                flops = 2.0 * m * n * k
+                steps = max(8, min(50, int(2e13 / flops)))
+                ms = _time_calls(calls, ws, stream, hbm, steps, max(4, steps // 2))
+                alg = m * k + sa.numel() * 4 + b_bytes + m * n * 2
+                tf = flops / (ms * 1e-3) / 1e12
+                gbps = alg / (ms * 1e-3) / 1e9
+                print(json.dumps({"sweep": "configs[2]", "variant": variant, "M": m, "N": n, "K": k,
+                                  "us": round(ms * 1e3, 2), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / 5000.0, 4),
+                                  "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_GBPS, 4),
+                                  "bound": "hbm" if hbm else "mfma"}), flush=True)
+                del Bs, SBs, calls, ws
+            del qa, sa, C
+        del qb, sb, bk, bpp
+        torch.cuda.empty_cache()
 
 
 def main():
@@ -90,6 +212,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration": {"bytes_read": 256 << 20, "bytes_written": 256 << 20,
                                                "launches": 5}}), flush=True)
+        return
+
+    if args.sweep:
+        sweep(args)
         return
 
     import oracle as O

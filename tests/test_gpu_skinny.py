@@ -128,6 +128,18 @@ def test_ldsbypass(qgemm, gpu, m, n, k, sfa_layout):
     assert_close(ref, out_to_f32(y), f"ldsbypass {m}x{n}x{k} {sfa_layout}")
 
 
+# tile-kernel cases of the LDS-bypass entry (M > 256: B'' blocks staged
+# through LDS): one K-tile, odd K-tile counts, ragged tiles, fp32 output
+@pytest.mark.parametrize("m,n,k", [(520, 300, 128), (264, 1000, 640), (512, 512, 1408), (768, 256, 256)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_ldsbypass_tile(qgemm, gpu, m, n, k, dtype):
+    qa, qb, sa, sb = make_bs(m, n, k, seed=5 * m + n + k)
+    ref = O.gemm_bs_fp32(qa, qb, sa, sb)
+    Bpp = qgemm.ldsbypass_repack(qgemm.shuffle_b_kpanel(to_dev(qb, None, gpu)))
+    y = qgemm.gemm_a8w8_ldsbypass(_fp8(qa, gpu), Bpp, to_dev(sa, None, gpu), to_dev(sb, None, gpu), n, dtype=dtype)
+    assert_close(ref, out_to_f32(y), f"ldsbypass tile {m}x{n}x{k} {dtype}")
+
+
 # ----------------------------------------------- batched calls (C ABI)
 def _call(qgemm, name, args, out_code, ws):
     L = qgemm.lib()
