@@ -14,6 +14,7 @@
 #include "launch.hpp"
 #include "qgemm.h"
 #include "decode_gemm.hpp"
+#include "mid_gemm.hpp"
 
 static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "reference kargs ABI");
@@ -138,6 +139,7 @@ static_assert(kSplitBelow <= 2 * kCUs, "counter block too small");
 struct Plan {
     bool skinny = false;
     bool decode = false;     // skinny shape with M <= 64 on an LDS-staged B layout
+    bool mid = false;        // fp32 block scales on 128 x 128 tiles (mid_gemm.hpp)
     int mb = 1, nb = 1, nw = 8, m_tiles = 1, n_tiles = 1, splitk = 1, kt_per_split = 1;
     size_t ctr_bytes = 0, ws_bytes = 0;
 };
@@ -217,6 +219,59 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
         p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
     }
     return p;
+}
+
+// fp32 block scales: M <= kMidMinM keeps the decode / skinny plan; larger M
+// runs the 256 x 256 kernel once it has at least kMidBelow tiles, else the
+// 128 x 128 kernel, with K split until about kMidTarget workgroups (two per
+// CU) are in flight, >= kMidMinKt K-tiles per slice.
+constexpr int kMidMinM = 64;
+constexpr int kMidBelow = 128;
+constexpr int kMidTarget = 2 * kCUs;
+constexpr int kMidMinKt = 8;
+
+Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
+    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, false, decode_ok);
+    if (m <= kMidMinM) return p;
+    const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    if (tiles256 >= kMidBelow) return p;
+    p = Plan{};
+    p.mid = true;
+    p.kt_per_split = k_tiles;
+    const long long tiles = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
+    if (tiles >= kMidTarget / 2 || tiles > kCounterBytes / (long long)sizeof(unsigned) ||
+        (long long)m * n >= (1LL << 29))    // partial offsets are 32-bit bytes
+        return p;
+    const long long split = std::min<long long>(kMidTarget / tiles, k_tiles / kMidMinKt);
+    if (split <= 1) return p;
+    p.kt_per_split = ceil_div(k_tiles, (int)split);
+    p.splitk = ceil_div(k_tiles, p.kt_per_split);
+    if (p.splitk > 1) {
+        p.ctr_bytes = kCounterBytes;
+        p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
+    }
+    return p;
+}
+
+// Launches the 128 x 128 fp32-block-scale kernel; a NULL workspace runs it
+// without a K split.
+hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, bool frag, void* ws, size_t ws_bytes, int k_tiles,
+                   hipStream_t stream) {
+    qg::MidArgs a{};
+    t.tiles_m = ceil_div(t.m, 128);
+    t.tiles_n = ceil_div(t.n, 128);
+    a.t = t;
+    if (pl.splitk > 1 && ws) {
+        if (ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return hipErrorInvalidValue;
+        a.counters = static_cast<unsigned*>(ws);
+        a.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl.ctr_bytes);
+        a.splitk = pl.splitk;
+        a.kt_per_split = pl.kt_per_split;
+    } else {
+        a.splitk = 1;
+        a.kt_per_split = k_tiles;
+    }
+    return qg::launch_mid(a, batch, bf16, frag, stream);
 }
 
 // Launches the skinny or decode kernel.  A NULL workspace runs one K slice
@@ -465,7 +520,8 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bk, false);
+    const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bk, true);
+    if (pl.mid) return run_mid(t, a.batch, pl, bf16, false, workspace, workspace_bytes, a.k / 128, stream);
     if (pl.skinny)
         return run_skinny(SkinnyKind::BSF32_KPANEL, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128,
                           stream);
@@ -476,7 +532,7 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
 
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false).ws_bytes;
+    return plan_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, true).ws_bytes;
 }
 
 // ------------------------------------------------ LDS-bypass block-scale FP8
@@ -502,7 +558,9 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
     t.sfb_sn = a.stride_sfb;
     // small M: the skinny kernel streams B'' straight into registers; large
     // M: the eight-wave tile kernel stages B'' blocks through LDS like B'
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, bpp, false, false);
+    const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bpp, false);
+    if (pl.mid)
+        return run_mid(t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, true, workspace, workspace_bytes, a.k / 128, stream);
     if (!pl.skinny) return qg::launch_bsf32(t, a.batch, out_dtype == QGEMM_OUT_BF16, true, stream);
     return run_skinny(SkinnyKind::BSF32_FRAG, t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, workspace,
                       workspace_bytes, a.k / 128, stream);
@@ -510,7 +568,7 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
 
 size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), false, false)
+    return plan_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), false)
         .ws_bytes;
 }
 

@@ -1,0 +1,19 @@
+// Instantiations and launcher of the four-wave 128 x 128 fp32-block-scale kernel.
+#include "launch.hpp"
+#include "mid_gemm.hpp"
+
+namespace qg {
+
+hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, bool frag, hipStream_t s) {
+    const dim3 grid(a.t.tiles_m * a.t.tiles_n, a.splitk, batch);
+    if (frag) {
+        if (bf16) mid_gemm_kernel<true, BLay::FRAG><<<grid, 256, 0, s>>>(a);
+        else mid_gemm_kernel<false, BLay::FRAG><<<grid, 256, 0, s>>>(a);
+    } else {
+        if (bf16) mid_gemm_kernel<true, BLay::KPANEL><<<grid, 256, 0, s>>>(a);
+        else mid_gemm_kernel<false, BLay::KPANEL><<<grid, 256, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace qg

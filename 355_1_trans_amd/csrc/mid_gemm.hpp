@@ -1,0 +1,318 @@
+// Four-wave 128 x 128 tile GEMM for fp8 with fp32 block scales (BSF32), with
+// split-K, for the middle of the M range on gfx950.
+//
+// At M ~ 256-4096 with narrow N the 256 x 256 tiles of bsf32_gemm.hpp leave
+// most of the 256 CUs idle (M = 1024, N = 2112: 36 tiles).  This kernel cuts
+// the tile to 128 x 128 (4 x the tiles) and can split K over workgroups; a
+// workgroup is 4 waves (one per SIMD) and two workgroups share a CU (66 KB of
+// LDS each), so one workgroup's barrier and DMA waits are covered by the
+// other's MFMAs.
+//
+//  * wave (wm, wn) = (w / 2, w % 2) owns 64 x 64 outputs: 4 x 4 blocks of
+//    v_mfma_f32_16x16x128_f8f6f4 (unscaled fp8; one instruction = one
+//    128-deep K-tile = one scale block), 64 VGPR accumulators, each
+//    partial rescaled acc += part * (sa * sb) after the next MFMA issued;
+//  * two LDS stages of one K-tile (A 128 rows, B 128 rows, the K-tile's
+//    scales), one barrier per K-tile; the 9 DMAs per wave of K-tile t+1
+//    (buffer_load ... lds, 4 A, 4 B, 1 scale) go into the other stage,
+//    spread over K-tile t's MFMAs; DMAs past the slice use an empty-range
+//    descriptor (no branches, so the compiler's DMA waits stay exact; the
+//    loop is unrolled by two so every stage is its own LDS object);
+//  * B' (K-panel): the tile's 128 rows of a K-tile are 16 contiguous KB;
+//    B'' (the LDS-bypass entry's fragment order): 8 blocks of 2 KB, copied
+//    as is and read back linearly (the block is the MFMA operand order);
+//  * split-K: each workgroup stores its fp32 partial tile device-coherently,
+//    then one relaxed counter atomic per workgroup (common.hpp); the last
+//    workgroup of a tile adds the slices in slice order (deterministic),
+//    rounds, stores and re-arms the counter.
+//
+// LDS rows are 128 bytes, 16-byte chunks XOR-swizzled by row & 7.
+#pragma once
+#include "tile_args.hpp"
+
+namespace qg {
+
+struct MidArgs {
+    TileArgs t;            // tiles_m / tiles_n count 128 x 128 tiles
+    float* ws;             // fp32 partials [splitk][batch][M][N] (splitk > 1)
+    unsigned* counters;    // [batch][tiles], zero between launches
+    int splitk, kt_per_split;
+};
+
+namespace mid {
+template <int V>
+struct I {
+    static constexpr int value = V;
+};
+}  // namespace mid
+
+template <bool BF16, BLay BL>
+__global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
+    static_assert(BL == BLay::KPANEL || BL == BLay::FRAG, "K-panel B' or fragment-order B''");
+    constexpr bool FRAG = (BL == BLay::FRAG);
+    constexpr int BKB = 128, BT = 128;
+    constexpr int OPB = BT * BKB;              // 16 KB per operand and K-tile
+    constexpr int SA_OFF = 2 * OPB;            // 128 fp32 row scales
+    constexpr int SB_OFF = SA_OFF + 512;       // 2 slots of 256 B (waves 2, 3)
+    constexpr int STAGE = SB_OFF + 512;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
+    __shared__ int last_flag;
+
+    const TileArgs& p = mp.t;
+    // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
+    const int T = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+    const int gfull = p.group_m * p.tiles_n;
+    const int gi = bid / gfull;
+    const int first_m = gi * p.group_m;
+    const int gm = min(p.tiles_m - first_m, p.group_m);
+    const int within = bid - gi * gfull;
+    const int tm = first_m + within % gm;
+    const int tn = within / gm;
+    const int tile = tm * p.tiles_n + tn;
+    const int sk = blockIdx.y, bz = blockIdx.z;
+    const int m0 = tm * BT, n0 = tn * BT;
+
+    const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDC = p.ldc;
+    const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
+    const int NKT = KB / BKB;
+    const int kt0 = sk * mp.kt_per_split;
+    const int nk = min(NKT, kt0 + mp.kt_per_split) - kt0;    // K-tiles of this slice
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
+    const int wm = w >> 1, wn = w & 1;
+    const int q = L >> 4, l16 = L & 15;
+
+    const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA + (long long)kt0 * BKB;
+    const uint8_t* B = p.b + bz * p.b_batch +
+                       (FRAG ? (long long)(n0 >> 4) * NKT * 2048 + (long long)kt0 * 2048
+                             : (long long)kt0 * N * BKB + (long long)n0 * BKB);
+    const long long b_kstep = FRAG ? 2048 : (long long)N * BKB;
+    const uint8_t* SFA = p.sfa + 4ll * bz * p.sfa_batch;
+    const uint8_t* SFB = p.sfb + 4ll * bz * p.sfb_batch;
+
+    // ---- DMA offsets: wave w moves 8-row groups 4w .. 4w+3 of A and of B'
+    // (lane L: row +L/8, physical chunk L%8 = logical (L%8) ^ (row & 7)),
+    // or blocks 2w, 2w+1 of B'' (two 1 KB halves each) ----
+    int aoff[4], boff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int r = (4 * w + u) * 8 + (L >> 3);
+        const int c = (L & 7) ^ (r & 7);
+        aoff[u] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
+        if constexpr (FRAG) {
+            const int blk = 2 * w + (u >> 1);
+            const int nb = min((n0 >> 4) + blk, ((N + 15) >> 4) - 1) - (n0 >> 4);
+            boff[u] = nb * NKT * 2048 + (u & 1) * 1024 + L * 16;
+        } else {
+            boff[u] = (min(n0 + r, N - 1) - n0) * BKB + c * 16;
+        }
+    }
+    // scales: waves 0, 1 move the fp32 row scales of rows [64w, 64w + 64);
+    // waves 2, 3 the tile's weight scale (its 128 columns are one scale block)
+    const bool sc_is_a = w < 2;
+    const uint8_t* sc_base = sc_is_a ? SFA + 4ll * m0 * SFA_SM + 4ll * kt0 * SFA_SK
+                                     : SFB + 4ll * min(n0 >> 7, (N - 1) >> 7) * SFB_SN + 4ll * kt0;
+    const int sc_voff = sc_is_a ? 4 * (min(m0 + 64 * w + L, M - 1) - m0) * SFA_SM : 0;
+    const long long sc_kstep = sc_is_a ? 4ll * SFA_SK : 4ll;
+    const int sc_dst = sc_is_a ? SA_OFF + 256 * w : SB_OFF + 256 * (w - 2);
+
+    QG_LDS uint8_t* const pS0 = (QG_LDS uint8_t*)st0;
+    QG_LDS uint8_t* const pS1 = (QG_LDS uint8_t*)st1;
+
+    auto rsrc = [&](const uint8_t* base, bool valid) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
+                                                 0x00020000);
+    };
+    struct Src {
+        __amdgpu_buffer_rsrc_t a, b, sc;
+    };
+    auto sources = [&](int kt) __attribute__((always_inline)) {
+        const bool v = kt < nk;
+        Src s;
+        s.a = rsrc(A + (long long)kt * BKB, v);
+        s.b = rsrc(B + (long long)kt * b_kstep, v);
+        s.sc = rsrc(sc_base + kt * sc_kstep, v);
+        return s;
+    };
+    // DMA d (0..8) of a K-tile into stage st: 0-3 A, 4-7 B, 8 scales
+    auto dma = [&](QG_LDS uint8_t* st, const Src& s, int d) __attribute__((always_inline)) {
+        if (d < 4) dma16_buf(s.a, st + (4 * w + d) * 1024, aoff[d], 0);
+        else if (d < 8) dma16_buf(s.b, st + OPB + (4 * w + d - 4) * 1024, boff[d - 4], 0);
+        else dma4_buf(s.sc, st + sc_dst, sc_voff, 0);
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    i32x8 af[4], bf[2];
+    f32x4 part[2];
+    float fs[4];
+    const int rd8 = l16 * BKB + ((q ^ (l16 & 7)) << 4);
+    const int rdb0 = FRAG ? L * 16 : rd8, rdb1 = FRAG ? 1024 + L * 16 : rd8 ^ 64;
+    auto frag = [&](const QG_LDS uint8_t* blk, int o0, int o1) __attribute__((always_inline)) -> i32x8 {
+        const i32x4 lo = *(const QG_LDS i32x4*)(blk + o0);
+        const i32x4 hi = *(const QG_LDS i32x4*)(blk + o1);
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    auto mfma_part = [&](const i32x8& b, const i32x8& a) __attribute__((always_inline)) {
+        // zero scale operands select the unscaled fp8 MFMA (a plain product)
+        return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b, a, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+    };
+    auto rescale = [&](int i, int j, int x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_fmaf(part[x][e], fs[i], acc[i][j][e]);
+    };
+
+    // K-tile t (local index) from stage ST; the 9 DMAs of K-tile t + 1 go
+    // into the other stage, one after each of the first 9 MFMAs
+    auto ktile = [&](auto STC, int t) __attribute__((always_inline)) {
+        constexpr int ST = decltype(STC)::value;
+        QG_LDS uint8_t* cur = ST ? pS1 : pS0;
+        QG_LDS uint8_t* nxt = ST ? pS0 : pS1;
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        const QG_LDS uint8_t* sA = cur + wm * 64 * BKB;
+        const QG_LDS uint8_t* sB = cur + OPB + wn * 64 * BKB;
+        bf[0] = frag(sB, rdb0, rdb1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = frag(sA + 16 * i * BKB, rd8, rd8 ^ 64);
+        const float sb = *(const QG_LDS float*)(cur + SB_OFF);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fs[i] = *(const QG_LDS float*)(cur + SA_OFF + 4 * (wm * 64 + 16 * i + l16)) * sb;
+        const Src src = sources(t + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int j = k >> 2, i = k & 3;
+            if (i == 0 && j < 3) bf[(j + 1) & 1] = frag(sB + (j + 1) * 16 * BKB, rdb0, rdb1);
+            part[k & 1] = mfma_part(bf[j & 1], af[i]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k > 0) rescale((k - 1) & 3, (k - 1) >> 2, (k - 1) & 1);
+            if (k < 9) dma(nxt, src, k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        rescale(3, 3, 1);
+    };
+
+    // ---- prologue: K-tile 0 into stage 0 ----
+    {
+        const Src s0 = sources(0);
+#pragma unroll
+        for (int d = 0; d < 9; ++d) dma(pS0, s0, d);
+    }
+    int t = 0;
+    for (; t + 2 <= nk; t += 2) {
+        ktile(mid::I<0>{}, t);
+        ktile(mid::I<1>{}, t + 1);
+    }
+    if (t < nk) ktile(mid::I<0>{}, t);
+    wait_vmcnt<0>();    // the DMAs past the slice still write zeros
+
+    // ---- output: lane holds C[16i + l16][16j + 4q + 0..3] of the wave's block ----
+    const int mw = m0 + wm * 64 + l16, nw0 = n0 + wn * 64 + 4 * q;
+    const bool vec_ok = (LDC & 3) == 0;
+    auto store_c = [&](int m, int n, f32x4 v) __attribute__((always_inline)) {
+        if (m >= M) return;
+        if constexpr (BF16) {
+            uint16_t* c = (uint16_t*)p.c + (long long)bz * p.c_batch + (long long)m * LDC + n;
+            if (vec_ok && n + 3 < N) {
+                *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            } else {
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < N) c[r] = bf16_bits(v[r]);
+            }
+        } else {
+            float* c = (float*)p.c + (long long)bz * p.c_batch + (long long)m * LDC + n;
+            if (vec_ok && n + 3 < N) {
+                *(f32x4*)c = v;
+            } else {
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < N) c[r] = v[r];
+            }
+        }
+    };
+    if (mp.splitk == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) store_c(mw + 16 * i, nw0 + 16 * j, acc[i][j]);
+        return;
+    }
+
+    // split-K: this slice's partial tile, device-coherent; then the counter
+    const long long plane = (long long)M * N;
+    const int batch = gridDim.z;
+    const long long split_stride = (long long)batch * plane;
+    const float* ws0 = mp.ws + (long long)bz * plane;
+    const bool nvec = (N & 3) == 0;
+    {
+        const auto part_out = partial_rsrc(ws0 + sk * split_stride);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = mw + 16 * i, n = nw0 + 16 * j;
+                if (m >= M) continue;
+                const int x = m * N + n;
+                if (nvec && n + 3 < N) {
+                    store_partial4(part_out, x, acc[i][j]);
+                } else {
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < N) store_partial1(part_out, x + r, acc[i][j][r]);
+                }
+            }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    unsigned* ctr = mp.counters + (long long)bz * T + tile;
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (unsigned)(mp.splitk - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    // slices in order 0 .. splitk-1 (this workgroup's own from registers);
+    // each slice's 16 loads are issued together
+    f32x4 v[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < mp.splitk; ++s) {
+        f32x4 u[4][4];
+        const auto src = partial_rsrc(ws0 + s * split_stride);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = min(mw + 16 * i, M - 1), n = nw0 + 16 * j;
+                const int x = m * N + n;
+                if (s == sk) {
+                    u[i][j] = acc[i][j];
+                } else if (nvec && n + 3 < N) {
+                    u[i][j] = load_partial4(src, x);
+                } else {
+                    for (int r = 0; r < 4; ++r) u[i][j][r] = n + r < N ? load_partial1(src, x + r) : 0.f;
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[i][j][r] += u[i][j][r];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) store_c(mw + 16 * i, nw0 + 16 * j, v[i][j]);
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace qg

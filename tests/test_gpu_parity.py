@@ -147,9 +147,12 @@ def test_blockscale_fp32(qgemm, gpu, m, n, k, sfa_layout):
     assert_close(ref, out_to_f32(y), f"bs-fp32 {m}x{n}x{k} {sfa_layout}")
 
 
-# tile-kernel cases: one K-tile, an odd K-tile count (the loop runs two
-# K-tiles per iteration), whole and ragged tiles, fp32 output
-@pytest.mark.parametrize("m,n,k", [(520, 300, 128), (264, 1000, 640), (512, 512, 1408), (768, 256, 256)])
+# tile-kernel cases: one K-tile, odd K-tile counts (the loops run two and
+# four half-steps per iteration), whole and ragged tiles, fp32 output; the
+# 128 x 128 kernel with K split 2, 3 and 7 ways (ragged last slice) and
+# without a split; the 256 x 256 kernel at 4096 x 4096
+@pytest.mark.parametrize("m,n,k", [(520, 300, 128), (264, 1000, 640), (512, 512, 1408), (768, 256, 256),
+                                   (300, 520, 2048), (130, 1000, 7168), (1024, 2112, 7168), (4096, 4096, 384)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_blockscale_fp32_tile(qgemm, gpu, m, n, k, dtype):
     qa, qb, sa, sb = make_bs(m, n, k, seed=3 * m + n + k)

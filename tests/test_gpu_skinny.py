@@ -130,7 +130,8 @@ def test_ldsbypass(qgemm, gpu, m, n, k, sfa_layout):
 
 # tile-kernel cases of the LDS-bypass entry (M > 256: B'' blocks staged
 # through LDS): one K-tile, odd K-tile counts, ragged tiles, fp32 output
-@pytest.mark.parametrize("m,n,k", [(520, 300, 128), (264, 1000, 640), (512, 512, 1408), (768, 256, 256)])
+@pytest.mark.parametrize("m,n,k", [(520, 300, 128), (264, 1000, 640), (512, 512, 1408), (768, 256, 256),
+                                   (130, 1000, 7168), (4096, 4096, 384)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_ldsbypass_tile(qgemm, gpu, m, n, k, dtype):
     qa, qb, sa, sb = make_bs(m, n, k, seed=5 * m + n + k)
@@ -169,7 +170,7 @@ def test_mxfp8_batched(qgemm, gpu, m, n, k):
         assert_close(O.gemm_mx8(*d), C[i].cpu().numpy(), f"batch {i}")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 2112, 2048), (24, 640, 1024), (300, 520, 384)])
+@pytest.mark.parametrize("m,n,k", [(1, 2112, 2048), (24, 640, 1024), (300, 520, 384), (300, 520, 2048)])
 def test_blockscale_fp32_batched(qgemm, gpu, m, n, k):
     batch = 2
     data = [make_bs(m, n, k, seed=70 + i) for i in range(batch)]
