@@ -374,7 +374,8 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
             for (int u = 0; u < 16; ++u) {
                 const int r = u * 4 + rr;
                 const i32x4 v = *(const QG_LDS i32x4*)(img + r * 256 + ((cc ^ (r & 15)) << 4));
-                *(i32x4*)(cbase + (long long)u * 4 * LDC) = v;
+                // non-temporal: the output is not re-read, keep L2 and MALL for A and B
+                __builtin_nontemporal_store(v, (i32x4*)(cbase + (long long)u * 4 * LDC));
             }
         } else {
             float* cw = (float*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 64 + l16) * LDC + n0 +

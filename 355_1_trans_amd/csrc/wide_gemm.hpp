@@ -148,7 +148,12 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
 
     // ---- per-lane DMA offsets: wave w fills rows [64w, 64w + 64) of A and
     // B, eight 8-row DMAs each; lane L writes row +L/8, physical chunk L%8 =
-    // logical chunk (L%8) ^ swizzle(row) ----
+    // logical chunk (L%8) ^ swizzle(row).  B in shuffle_weight(16,16) order
+    // (W16) instead moves whole 16-row blocks as is: a block's K-tile is 2 KB
+    // contiguous ([8 chunks][16 rows][16 B], already the 16x16x128 operand
+    // order), two linear 1 KB DMAs, read back linearly.  (Gathering W16 into
+    // 128-byte rows made every lane of a DMA hit a different cache line:
+    // 18% more cycles per K-tile.) ----
     int aoff[8], boff[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -158,7 +163,10 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         const int gn = min(n0 + r, N - 1) - n0;
         if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
         else if constexpr (BL == BLay::KPANEL) boff[t] = gn * BKB + c * 16;
-        else boff[t] = (gn >> 4) * 16 * KB + (gn & 15) * 16 + c * 256;
+        else {
+            const int blk = min((n0 >> 4) + w * 4 + (t >> 1), ((N + 15) >> 4) - 1) - (n0 >> 4);
+            boff[t] = blk * 16 * KB + (t & 1) * 1024 + L * 16;
+        }
     }
 
     // ---- scale sources (buffer DMAs; empty range = no-op) ----
@@ -308,8 +316,9 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             dst[h][4 * (x >> 1) + s0 + 1] = *(const QG_LDS i32x4*)(blk + rd4(s0 + 1));
         } else {
             const QG_LDS uint8_t* blk = base + (4 * h + x) * 16 * BKB;
-            const i32x4 lo = *(const QG_LDS i32x4*)(blk + rd8);
-            const i32x4 hi = *(const QG_LDS i32x4*)(blk + (rd8 ^ 64));
+            const bool lin = BL == BLay::W16 && !is_a;    // W16 blocks: operand order
+            const i32x4 lo = *(const QG_LDS i32x4*)(blk + (lin ? L * 16 : rd8));
+            const i32x4 hi = *(const QG_LDS i32x4*)(blk + (lin ? 1024 + L * 16 : rd8 ^ 64));
             dst[h][x] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
     };
@@ -468,7 +477,8 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             for (int u = 0; u < 32; ++u) {
                 const int r = u * 4 + rr;
                 const i32x4 v = *(const QG_LDS i32x4*)(img + r * 256 + ((cc ^ (r & 15)) << 4));
-                *(i32x4*)(cbase + (long long)u * 4 * LDC) = v;
+                // non-temporal: the output is not re-read, keep L2 and MALL for A and B
+                __builtin_nontemporal_store(v, (i32x4*)(cbase + (long long)u * 4 * LDC));
             }
         } else {
             float* cw = (float*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128) * LDC + n0 + wn * 128;

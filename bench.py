@@ -28,6 +28,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -44,6 +46,9 @@ WORKLOADS = {
     "bs_c0": ("bs", 32, 1536, 7168, 0),
     "ldsbypass_c0": ("lbp", 32, 1536, 7168, 0),
     "mxfp4_c4": ("mx4", 32, 7168, 16384, 4),
+    # the reference's headline block-scale kernel (E8M0 1x128 / 128x128 scales,
+    # shuffle_weight(16,16) B: 3.31 PFLOPS at 8192^3)
+    "bs_e8m0_8192": ("bs8", 8192, 8192, 8192, None),
 }
 
 
@@ -89,6 +94,19 @@ def _gpu_quant_bs(rows, k, block_rows, gen, dev):
     sc = blk.abs().amax(dim=(1, 3)).clamp_min(1e-12) / 448.0
     qx = (blk / sc[:, None, :, None]).to(torch.float8_e4m3fn).view(rp, k)[:rows]
     return qx.contiguous().view(torch.uint8), sc.contiguous()
+
+
+def _gpu_quant_e8m0(rows, k, block_rows, gen, dev):
+    """N(0,1) data quantized to e4m3 with one E8M0 scale 2^ceil(log2(amax /
+    448)) per block_rows x 128 block, on the GPU; returns (uint8 [rows, k],
+    uint8 exponent codes [ceil(rows / block_rows), k / 128])."""
+    import torch
+    rp = -(-rows // block_rows) * block_rows
+    x = torch.randn((rp, k), generator=gen, device=dev)
+    blk = x.view(rp // block_rows, block_rows, k // 128, 128)
+    e = torch.ceil(torch.log2(blk.abs().amax(dim=(1, 3)).clamp_min(1e-30) / 448.0)).clamp(-127, 127)
+    qx = (blk / torch.exp2(e)[:, None, :, None]).to(torch.float8_e4m3fn).view(rp, k)[:rows]
+    return qx.contiguous().view(torch.uint8), (e + 127).to(torch.uint8).contiguous()
 
 
 def _time_calls(calls, ws, stream, graph_mode, steps, warmup):
@@ -229,12 +247,26 @@ def main():
     if args.m:
         M = args.m
     hbm_bound = M <= 256
-    a = O.randn((M, K), 0, 0)
-    b = O.randn((N, K), 0, 1)
     kg32, kg128 = K // 32, K // 128
+    if fam == "bs8":
+        # N(0,1) quantized on the GPU with E8M0 block scales 2^ceil(log2(amax / 448))
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0)
+        qa, sa = _gpu_quant_e8m0(M, K, 1, gen, dev)
+        qb, sb = _gpu_quant_e8m0(N, K, 128, gen, dev)
+        A = qa
+        SA = sa.t().contiguous()                        # physical [K/128][M], stride_sfa = M
+        B0 = q.shuffle_weight_16x16(qb)
+        SB0 = sb
+        a = b = None
+    else:
+        a = O.randn((M, K), 0, 0)
+        b = O.randn((N, K), 0, 1)
 
     # quantize once on the host (BASELINE recipe); device copies of the operands
-    if fam == "mx8":
+    if fam == "bs8":
+        pass
+    elif fam == "mx8":
         qa, sa = O.quant_mx8(a)
         qb, sb = O.quant_mx8(b)
     elif fam == "mx4":
@@ -243,10 +275,11 @@ def main():
     else:
         qa, sa = O.quant_bs_act(a)
         qb, sb = O.quant_bs_wgt(b)
-    A = torch.from_numpy(qa).to(dev)
-    SA = torch.from_numpy(sa).to(dev)
-    B0 = torch.from_numpy(qb).to(dev)
-    SB0 = torch.from_numpy(sb).to(dev)
+    if fam != "bs8":
+        A = torch.from_numpy(qa).to(dev)
+        SA = torch.from_numpy(sa).to(dev)
+        B0 = torch.from_numpy(qb).to(dev)
+        SB0 = torch.from_numpy(sb).to(dev)
     if fam == "bs":
         B0 = q.shuffle_b_kpanel(B0)
     elif fam == "lbp":
@@ -265,6 +298,16 @@ def main():
                             SA.data_ptr(), SB.data_ptr(), kg32, kg32, M * kg32, N * kg32)
             fn = L.gemm_a8w8_mxfp8 if fam == "mx8" else L.gemm_a4w4_mxfp4
             wq = L.gemm_a8w8_mxfp8_workspace_bytes if fam == "mx8" else L.gemm_a4w4_mxfp4_workspace_bytes
+        elif fam == "bs8":
+            args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, K, N, M * K, N * K, M * N,
+                            SA.data_ptr(), SB.data_ptr(), M, kg128, M * kg128, SB.numel())
+
+            def fn(ka, out_bf16, ws_ptr, ws_bytes, stream):
+                return L.launch_blockscale_bpreshuffle(ka, out_bf16, 0, stream)
+            fn.__name__ = "launch_blockscale_bpreshuffle"
+
+            def wq(ka):
+                return 0
         elif fam == "bs":
             args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K, N * K, M * N,
                             SA.data_ptr(), SB.data_ptr(), 1 if M > 1 else M, kg128, M * kg128, SB.numel())
@@ -348,6 +391,10 @@ def main():
             cpu_fn = lambda rows: O.gemm_mx8(qa[rows], qb, sa[rows], sb)
         elif fam == "mx4":
             cpu_fn = lambda rows: O.gemm_mx4(qa[rows], qb, sa[rows], sb)
+        elif fam == "bs8":
+            qa_h, qb_h = qa.cpu().numpy(), qb.cpu().numpy()
+            sa_h, sb_h = SA.cpu().numpy(), sb.cpu().numpy()
+            cpu_fn = lambda rows: O.gemm_bs_e8m0(qa_h[rows], qb_h, np.ascontiguousarray(sa_h[:, rows]), sb_h)
         else:
             cpu_fn = lambda rows: O.gemm_bs_fp32(qa[rows], qb, sa[rows], sb)
         # bounded row band of the same GEMM on this host's cores, extrapolated per FLOP
@@ -367,12 +414,15 @@ def main():
     names = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
              "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
              "bs": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, K-panel B (bpreshuffle)",
-             "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)"}
+             "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)",
+             "bs8": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, shuffle_weight(16,16) B"}
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": launches,
         "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": kind, "data": "synthetic N(0,1) seed 0, BASELINE quantization recipe",
-        "config": {"workload": f"{names[fam]} M={M} N={N} K={K}, bf16 out (BASELINE configs[{cfg}])",
+        "config": {"workload": f"{names[fam]} M={M} N={N} K={K}, bf16 out " +
+                               (f"(BASELINE configs[{cfg}])" if cfg is not None
+                                else "(the reference's headline block-scale kernel, BASELINE.md)"),
                    "M": M, "N": N, "K": K, "out": "bf16",
                    "timing": ("one HIP graph of the timed launches over %d rotating weight copies" % len(calls))
                    if hbm_bound else "back-to-back launches"},
