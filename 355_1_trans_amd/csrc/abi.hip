@@ -456,7 +456,10 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false);
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);
-    return qg::launch_wide_mx4_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
+    // 32-byte panels (4 K-tiles, two DMA lanes per scale row) need whole
+    // panels: K % 1024 == 0
+    const int pb = mx_wide_panels(a) ? (a.k % 1024 == 0 ? 32 : 16) : 8;
+    return qg::launch_wide_mx4_raw(t, a.batch, bf16, pb, stream);
 }
 
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {

@@ -97,10 +97,14 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     constexpr int RB = FP4 ? 32 : 16;          // rows per MFMA block
     constexpr int NBLK = 128 / RB;             // blocks per wave and operand
     constexpr int KT_BYTES = FP4 ? 8 : 4;      // MX scale bytes per row per K-tile
-    static_assert(PB == 16 || PB == KT_BYTES, "panel width");
+    static_assert(PB == 16 || (PB == 32 && FP4) || PB == KT_BYTES, "panel width");
+    constexpr bool WIDE = PB >= 16;               // [row][PB] panels of whole 16-byte pieces
     constexpr int SPAN = MX ? PB / KT_BYTES : 1;  // K-tiles per scale DMA
-    constexpr int PANEL = 256 * 16;
-    constexpr int SA_BYTES = MX ? 2 * PANEL : 2 * 256;  // BS8: a 256-byte slot per stage
+    constexpr int PANEL = 256 * (PB > 16 ? PB : 16);
+    // BS8: a 256-byte SFA slot per stage, then the landing slots of the no-op
+    // SFA DMAs of waves 1-3 (an empty-range buffer DMA still writes zeros to
+    // its LDS destination)
+    constexpr int SA_BYTES = MX ? 2 * PANEL : 2 * 256 + 4 * 256;
     constexpr int SB_BYTES = MX ? 2 * PANEL : 2 * 4 * 256;
     // a register half: fp8 4 fragments of 8 VGPRs (one per 16-row block);
     // fp4 8 of 4 VGPRs (2 32-row blocks x 4 sub-tiles)
@@ -114,9 +118,6 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lB1[BM * BKB];
     __shared__ __attribute__((aligned(256))) uint8_t lSA[SA_BYTES];
     __shared__ __attribute__((aligned(256))) uint8_t lSB[SB_BYTES];
-    // BS8: landing slots of the no-op SFA DMAs of waves 1-3 (an empty-range
-    // buffer DMA still writes zeros to its LDS destination)
-    __shared__ __attribute__((aligned(256))) uint8_t lJunk[MX ? 4 : 1024];
 
     // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
     const int T = p.tiles_m * p.tiles_n;
@@ -170,12 +171,20 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     }
 
     // ---- scale sources (buffer DMAs; empty range = no-op) ----
-    // MX panels: wave w moves the panel rows of A quarter w and B quarter w
-    // (lane L = row 64w + L)
+    // MX panels: wave w moves the panel rows of A quarter w and B quarter w:
+    // lane L = row 64w + L (PB <= 16), or with 32-byte panels two lanes per
+    // row (row 64w + 32u + L/2, 16-byte half L%2, DMA u = 0, 1), so that a
+    // DMA touches 32 cache lines instead of 64
     const uint8_t* SFA_t = SFA + (long long)m0 * (MX ? SFA_SM : 1);
     const uint8_t* SFB_t = SFB + (MX ? (long long)n0 * SFB_SN : 0ll);
-    const int mx_voff_a = (min(m0 + w * 64 + L, M - 1) - m0) * SFA_SM;
-    const int mx_voff_b = (min(n0 + w * 64 + L, N - 1) - n0) * SFB_SN;
+    int mx_voff_a[2], mx_voff_b[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int r = PB == 32 ? w * 64 + 32 * u + (L >> 1) : w * 64 + L;
+        const int h = PB == 32 ? (L & 1) * 16 : 0;
+        mx_voff_a[u] = (min(m0 + r, M - 1) - m0) * SFA_SM + h;
+        mx_voff_b[u] = (min(n0 + r, N - 1) - n0) * SFB_SN + h;
+    }
     // BS8: SFA's 256 row bytes of a K-tile by wave 0; SFB's byte of the
     // wave's 128-column block as the aligned dword holding it
     const long long bs_b_idx = (long long)min((n0 >> 7) + wn, (N - 1) >> 7) * SFB_SN;
@@ -186,7 +195,6 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     QG_LDS uint8_t* pB1 = (QG_LDS uint8_t*)lB1;
     QG_LDS uint8_t* pSA = (QG_LDS uint8_t*)lSA;
     QG_LDS uint8_t* pSB = (QG_LDS uint8_t*)lSB;
-    QG_LDS uint8_t* pJunk = (QG_LDS uint8_t*)lJunk;
 
     const int nk = KB / BKB;
 
@@ -211,29 +219,35 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     };
     // scale DMAs that go with K-tile kt (MX: only when kt starts a panel,
     // which the callers know at compile time); `valid` false = no-op DMAs.
-    // MX panel images: PB = 16: [row][16 B]; PB = 4 (fp8): [row][4 B];
+    // MX panel images: PB = 16, 32: [row][PB]; PB = 4 (fp8): [row][4 B];
     // PB = 8 (fp4): [2 halves][row][4 B]
     auto dma_scales = [&](int kt, bool valid) __attribute__((always_inline)) {
         if constexpr (MX) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
             const auto ra = rsrc(SFA_t + kt * KT_BYTES, valid);
             const auto rb = rsrc(SFB_t + kt * KT_BYTES, valid);
-            if constexpr (PB == 16) {
-                dma16_buf(ra, pSA + buf + w * 1024, mx_voff_a, 0);
-                dma16_buf(rb, pSB + buf + w * 1024, mx_voff_b, 0);
+            if constexpr (PB == 32) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    dma16_buf(ra, pSA + buf + w * 2048 + u * 1024, mx_voff_a[u], 0);
+                    dma16_buf(rb, pSB + buf + w * 2048 + u * 1024, mx_voff_b[u], 0);
+                }
+            } else if constexpr (PB == 16) {
+                dma16_buf(ra, pSA + buf + w * 1024, mx_voff_a[0], 0);
+                dma16_buf(rb, pSB + buf + w * 1024, mx_voff_b[0], 0);
             } else {
-                dma4_buf(ra, pSA + buf + w * 256, mx_voff_a, 0);
-                dma4_buf(rb, pSB + buf + w * 256, mx_voff_b, 0);
+                dma4_buf(ra, pSA + buf + w * 256, mx_voff_a[0], 0);
+                dma4_buf(rb, pSB + buf + w * 256, mx_voff_b[0], 0);
                 if constexpr (PB == 8) {
-                    dma4_buf(ra, pSA + buf + 1024 + w * 256, mx_voff_a + 4, 0);
-                    dma4_buf(rb, pSB + buf + 1024 + w * 256, mx_voff_b + 4, 0);
+                    dma4_buf(ra, pSA + buf + 1024 + w * 256, mx_voff_a[0] + 4, 0);
+                    dma4_buf(rb, pSB + buf + 1024 + w * 256, mx_voff_b[0] + 4, 0);
                 }
             }
         } else {
             const int st = kt & 1;
             const auto ra = rsrc(SFA_t + (long long)kt * SFA_SK, valid && w == 0);
             const auto rb = rsrc(SFB + ((bs_b_idx + kt) & ~3ll), valid);
-            dma4_buf(ra, w == 0 ? pSA + st * 256 : pJunk + w * 256, 4 * L, 0);
+            dma4_buf(ra, w == 0 ? pSA + st * 256 : pSA + 256 + w * 256, 4 * L, 0);
             dma4_buf(rb, pSB + st * 1024 + w * 256, 0, 0);
         }
     };
@@ -249,17 +263,17 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     auto read_scale = [&](int kt, int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
         if constexpr (MX && !FP4) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
-            const int col = PB == 16 ? (kt % SPAN) * KT_BYTES + q : q;
+            const int col = WIDE ? (kt % SPAN) * KT_BYTES + q : q;
             sa[x] = pSA[buf + (wm * 128 + x * 16 + l16) * PB + col];
             sb[x] = pSB[buf + (wn * 128 + x * 16 + l16) * PB + col];
         } else if constexpr (MX) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
             const int ra = wm * 128 + (x >> 1) * 32 + l32, rb = wn * 128 + (x >> 1) * 32 + l32;
-            if constexpr (PB == 16) {
+            if constexpr (WIDE) {
                 // both words of the block in one read (x even; x odd is a no-op)
                 if ((x & 1) == 0) {
-                    const i32x2 va = *(const QG_LDS i32x2*)(pSA + buf + ra * 16 + (kt % SPAN) * KT_BYTES);
-                    const i32x2 vb = *(const QG_LDS i32x2*)(pSB + buf + rb * 16 + (kt % SPAN) * KT_BYTES);
+                    const i32x2 va = *(const QG_LDS i32x2*)(pSA + buf + ra * PB + (kt % SPAN) * KT_BYTES);
+                    const i32x2 vb = *(const QG_LDS i32x2*)(pSB + buf + rb * PB + (kt % SPAN) * KT_BYTES);
                     sa[x] = va[0];
                     sa[x + 1] = va[1];
                     sb[x] = vb[0];

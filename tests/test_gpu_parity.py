@@ -91,7 +91,7 @@ def test_mxfp8_k_pattern_scales(qgemm, gpu):
 
 # ----------------------------------------------------------------- MXFP4
 MX4_SHAPES = [(256, 256, 256), (256, 512, 1024), (100, 300, 512), (1, 512, 2048), (257, 256, 768),
-              (512, 512, 2048), (384, 1024, 512)]
+              (512, 512, 2048), (384, 1024, 512), (300, 520, 3072), (512, 768, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", MX4_SHAPES)
@@ -101,6 +101,20 @@ def test_mxfp4(qgemm, gpu, m, n, k):
     y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
                               to_dev(eb, None, gpu), dtype=torch.bfloat16)
     assert_close(ref, out_to_f32(y), f"mxfp4 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 256, 4096), (300, 520, 3072), (512, 512, 1536)])
+def test_mxfp4_k_pattern_scales(qgemm, gpu, m, n, k):
+    """Distinct per-K-group scales on both operands catch K-group and scale
+    panel misrouting (32-, 16- and 8-byte panels)."""
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=11)
+    g = np.arange(k // 32)
+    ea = np.broadcast_to((122 + (g % 11)).astype(np.uint8), ea.shape).copy()
+    eb = np.broadcast_to((121 + ((3 * g) % 13)).astype(np.uint8), eb.shape).copy()
+    ref = O.gemm_mx4(qa, qb, ea, eb)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.float32)
+    assert_close(ref, out_to_f32(y), f"mxfp4 K-pattern {m}x{n}x{k}")
 
 
 # ----------------------------------------------- block-scale, E8M0 (SNAP ABI)
