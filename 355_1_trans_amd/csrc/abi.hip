@@ -432,7 +432,9 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
-    return qg::launch_wide_mx8_raw(t, a.batch, bf16, mx_wide_panels(a), stream);
+    // (32-byte panels would cover 8 K-tiles; the loop then unrolls by 8, and
+    // measured 1% slower than 16-byte panels for fp8)
+    return qg::launch_wide_mx8_raw(t, a.batch, bf16, mx_wide_panels(a) ? 16 : 4, stream);
 }
 
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {

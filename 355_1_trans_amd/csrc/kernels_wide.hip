@@ -15,9 +15,9 @@ hipError_t launch_wide(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
 }
 }  // namespace
 
-hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s) {
-    return wide_panels ? launch_wide<kFmtFp8, ScaleKind::MX, BLay::RAW, 16>(a, batch, bf16, s)
-                       : launch_wide<kFmtFp8, ScaleKind::MX, BLay::RAW, 4>(a, batch, bf16, s);
+hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s) {
+    if (panel_bytes == 16) return launch_wide<kFmtFp8, ScaleKind::MX, BLay::RAW, 16>(a, batch, bf16, s);
+    return launch_wide<kFmtFp8, ScaleKind::MX, BLay::RAW, 4>(a, batch, bf16, s);
 }
 hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s) {
     if (panel_bytes == 32) return launch_wide<kFmtFp4, ScaleKind::MX, BLay::RAW, 32>(a, batch, bf16, s);

@@ -11,7 +11,8 @@ namespace qg {
 // with frag, B'' (the LDS-bypass entry's fragment order)
 hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
-hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, bool wide_panels, hipStream_t s);
+// panel_bytes: MX8 scale panel width, 16 or 4 bytes per row
+hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s);
 // panel_bytes: MX4 scale panel width, 32, 16 or 8 bytes per row
 hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s);
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);

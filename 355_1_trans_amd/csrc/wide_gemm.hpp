@@ -41,6 +41,7 @@
 // tile_args.hpp.
 #pragma once
 #include <type_traits>
+#include <utility>
 
 #include "tile_args.hpp"
 
@@ -62,6 +63,15 @@ template <int V>
 struct I {
     static constexpr int value = V;
 };
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(I<Is>{}), ...);
+}
+// f(I<0>{}), ..., f(I<N-1>{})
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 // acc += scaled MFMA with the accumulator pinned to AGPRs (the "a"
 // constraint): left to the register allocator, 256 accumulators plus 128
 // operand registers get shuffled between AGPRs, VGPRs and scratch.  The
@@ -97,7 +107,7 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     constexpr int RB = FP4 ? 32 : 16;          // rows per MFMA block
     constexpr int NBLK = 128 / RB;             // blocks per wave and operand
     constexpr int KT_BYTES = FP4 ? 8 : 4;      // MX scale bytes per row per K-tile
-    static_assert(PB == 16 || (PB == 32 && FP4) || PB == KT_BYTES, "panel width");
+    static_assert(PB == 16 || PB == 32 || PB == KT_BYTES, "panel width");
     constexpr bool WIDE = PB >= 16;               // [row][PB] panels of whole 16-byte pieces
     constexpr int SPAN = MX ? PB / KT_BYTES : 1;  // K-tiles per scale DMA
     constexpr int PANEL = 256 * (PB > 16 ? PB : 16);
@@ -437,16 +447,18 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
 #pragma unroll
     for (int x = 0; x < 8; ++x) finish_scale(x, s0a, s0b);
 
+    // the loop runs U K-tiles per iteration: the quadrant rotation repeats
+    // every 4 and the scale-panel DMA every SPAN, both at compile time
+    constexpr int U = SPAN > 4 ? SPAN : 4;
+    auto step = [&](auto PC, int tt) __attribute__((always_inline)) {
+        if constexpr (decltype(PC)::value & 1) ktile(PC, tt, s1a, s1b, s0a, s0b);
+        else ktile(PC, tt, s0a, s0b, s1a, s1b);
+    };
     int t = 0;
-    for (; t + 4 <= nk; t += 4) {
-        ktile(wide::I<0>{}, t, s0a, s0b, s1a, s1b);
-        ktile(wide::I<1>{}, t + 1, s1a, s1b, s0a, s0b);
-        ktile(wide::I<2>{}, t + 2, s0a, s0b, s1a, s1b);
-        ktile(wide::I<3>{}, t + 3, s1a, s1b, s0a, s0b);
-    }
-    if (t < nk) ktile(wide::I<0>{}, t, s0a, s0b, s1a, s1b);
-    if (t + 1 < nk) ktile(wide::I<1>{}, t + 1, s1a, s1b, s0a, s0b);
-    if (t + 2 < nk) ktile(wide::I<2>{}, t + 2, s0a, s0b, s1a, s1b);
+    for (; t + U <= nk; t += U) wide::static_for<U>([&](auto pc) __attribute__((always_inline)) { step(pc, t + pc.value); });
+    wide::static_for<U - 1>([&](auto pc) __attribute__((always_inline)) {
+        if (t + pc.value < nk) step(pc, t + pc.value);
+    });
     wait_vmcnt<0>();
     // the accumulators come from inline-asm MFMAs, which the compiler's hazard
     // tracking does not see: cover the MFMA-result-to-VALU-read latency

@@ -77,9 +77,10 @@ def test_mxfp8(qgemm, gpu, m, n, k, dtype):
     assert_close(ref, out_to_f32(y), f"mxfp8 {m}x{n}x{k}")
 
 
-def test_mxfp8_k_pattern_scales(qgemm, gpu):
-    """Distinct per-K-group scales catch K-group misrouting (MX4 host.cc:185-187)."""
-    m, n, k = 512, 256, 1024
+@pytest.mark.parametrize("m,n,k", [(512, 256, 1024), (512, 512, 4096), (300, 520, 1536)])
+def test_mxfp8_k_pattern_scales(qgemm, gpu, m, n, k):
+    """Distinct per-K-group scales catch K-group and scale panel misrouting
+    (MX4 host.cc:185-187; 32- and 16-byte panels)."""
     qa, qb, ea, eb = make_mx8(m, n, k, seed=7)
     ea = np.broadcast_to((120 + (np.arange(k // 32) % 13)).astype(np.uint8), ea.shape).copy()
     ref = O.gemm_mx8(qa, qb, ea, eb)
