@@ -20,7 +20,9 @@
 //    barrier per K-tile: every wave waits for its own DMAs of K-tile k, the
 //    barrier makes the other waves' rows of A visible and frees the stage of
 //    K-tile k-1, into which the DMAs of K-tile k+D-1 go;
-//  * scales go straight into registers with the same look-ahead;
+//  * MX scale bytes go straight into registers with the same look-ahead;
+//    fp32 row scales by one DMA per K-tile into the stage (one cache-line
+//    request per row; per-wave register loads made one per row and wave);
 //  * K is split over workgroups when the N tiles alone leave CUs idle; the
 //    last workgroup of a tile sums the fp32 partial slices in slice order
 //    (deterministic), one launch.
@@ -41,10 +43,13 @@ struct DecodeArgs {
     int splitk, kt_per_split, n_tiles;
 };
 
-// LDS bytes of one K-tile stage and the ring depth for MB row blocks, NW waves
-__host__ __device__ constexpr int decode_stage_bytes(int mb, int nw) { return (mb + nw) * 2048; }
-__host__ __device__ constexpr int decode_depth(int mb, int nw) {
-    const int d = 150 * 1024 / decode_stage_bytes(mb, nw);
+// LDS bytes of one K-tile stage and the ring depth for MB row blocks, NW
+// waves; fp32 block scales add a 256-byte row-scale slot per wave
+__host__ __device__ constexpr int decode_stage_bytes(int mb, int nw, bool lds_sa) {
+    return (mb + nw) * 2048 + (lds_sa ? 256 * nw : 0);
+}
+__host__ __device__ constexpr int decode_depth(int mb, int nw, bool lds_sa) {
+    const int d = 150 * 1024 / decode_stage_bytes(mb, nw, lds_sa);
     return d > 8 ? 8 : d;
 }
 
@@ -57,15 +62,20 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
     static_assert(BL == BLay::RAW || BL == BLay::KPANEL, "row-major or K-panel B");
     constexpr bool FP4 = (FMT == kFmtFp4);
     constexpr bool MX = (SK == ScaleKind::MX);
-    constexpr int D = decode_depth(MB, NW);
+    // fp32 row scales of a K-tile go into the stage by one DMA (wave 0; the
+    // other waves' no-op DMAs land in their own slots): one cache-line
+    // request per row, instead of one per row and wave from register loads
+    constexpr bool LDS_SA = !MX;
+    constexpr int D = decode_depth(MB, NW, LDS_SA);
     static_assert(D >= 3, "ring depth");
     constexpr int ROWS = MB * 16, COLS = NW * 16, NT = NW * 64;
-    constexpr int STAGE = decode_stage_bytes(MB, NW);
+    constexpr int STAGE = decode_stage_bytes(MB, NW, LDS_SA);
+    constexpr int SA_OFF = (MB + NW) * 2048;
     constexpr int A_BYTES = MB * 2048;               // A rows of one K-tile
     constexpr int A_SHARE = A_BYTES / NW;            // bytes of A each wave moves
     constexpr int A_DMAS = A_SHARE >= 1024 ? A_SHARE / 1024 : A_SHARE / 256;   // x4 or x1 DMAs
     constexpr bool A_X4 = A_SHARE >= 1024;
-    constexpr int P = A_DMAS + 2 + MB + 1;           // vector-memory instructions per wave and K-tile
+    constexpr int P = A_DMAS + 2 + (MX ? MB : 1) + 1;   // vector-memory instructions per wave and K-tile
 
     __shared__ __attribute__((aligned(16))) uint8_t ring0[STAGE];
     __shared__ __attribute__((aligned(16))) uint8_t ring1[STAGE];
@@ -150,6 +160,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
     const int nb = min(nw0 + l16, N - 1);
     const int sb_voff = MX ? nb * SFB_SN + (FP4 ? 2 * q : q) : ((min(nw0, N - 1) >> 7) * SFB_SN) * 4;
     const int sa_kstep = MX ? (FP4 ? 8 : 4) : SFA_SK * 4;
+    const int sa_dma_voff = min(L, M - 1) * SFA_SM * 4;      // fp32: lane L moves row L's scale
     const int sb_kstep = MX ? (FP4 ? 8 : 4) : 4;
     // fragment reads inside a 16-row block: row l16, chunks c0 / c1
     const int c0 = FP4 ? 2 * q : q, c1 = FP4 ? 2 * q + 1 : q + 4;
@@ -186,9 +197,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
             if constexpr (FP4) sc.sb = __builtin_amdgcn_raw_buffer_load_b16(rSB, sb_voff, kt * sb_kstep, 0);
             else sc.sb = __builtin_amdgcn_raw_buffer_load_b8(rSB, sb_voff, kt * sb_kstep, 0);
         } else {
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-                sc.fa[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSA, sa_voff[i], kt * sa_kstep, 0));
+            dma4_buf(rsrc(SFA, valid && w == 0), st + SA_OFF + w * 256, sa_dma_voff, kt * sa_kstep);
             sc.fb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSB, sb_voff, kt * sb_kstep, 0));
         }
     };
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
             } else {
                 const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                     bf, af, f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, unit, 0, unit);
-                const float s = sc.fa[i] * sc.fb;
+                const float s = *(const QG_LDS float*)(st + SA_OFF + 4 * (i * 16 + l16)) * sc.fb;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[i][r] = __builtin_fmaf(part[r], s, acc[i][r]);
             }
