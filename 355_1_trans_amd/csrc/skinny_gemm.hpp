@@ -61,7 +61,22 @@ struct SkinnyArgs {
     float* ws;               // fp32 partials [splitk][batch][M][N] (splitk > 1)
     unsigned* counters;      // [batch][m_tiles][n_tiles], zero between launches
     int splitk, kt_per_split, n_tiles, m_tiles;
+    int scale_panel;         // MX: per-wave scale panels (skinny_scale_panel_ok)
 };
+
+// MX scale panels: a wave takes a contiguous run of at most 64 / kt_bytes
+// K-tiles (kt_bytes = scale bytes per row and K-tile; runs start on a
+// 16-byte boundary of the scale row) and DMAs its rows' scale bytes for the
+// whole run once, 64 bytes per row, into its own LDS panel; needs 16-byte
+// aligned scale rows and K slices starting on a 16-byte boundary.
+__host__ __device__ constexpr int skinny_panel_run(int slice_kt, int waves, int kt_bytes) {
+    const int g = 16 / kt_bytes;
+    return ((slice_kt + waves - 1) / waves + g - 1) / g * g;
+}
+// the panels fit next to at least two LDS ring stages of B
+__host__ __device__ constexpr bool skinny_scp_fits(int mb, int nb) {
+    return 2 * 8 * nb * 2048 + 8 * (mb + nb) * 1024 <= 152 * 1024;
+}
 
 // blockIdx.x -> (n-tile, m-tile): the m-tiles that share one B slice get
 // workgroup ids 8 apart, i.e. the same XCD (ids are dealt round-robin over
@@ -72,10 +87,11 @@ __host__ __device__ inline int skinny_grid_x(int n_tiles, int m_tiles) { return 
 // K-tiles in flight per wave.  Register budget: D stages of A fragments
 // (8*MB dwords + scales) next to 4*MB*NB accumulators (and, without the LDS
 // ring, 8*NB dwords of B per stage).  LDS budget (LDS ring): 8 waves x D
-// stages x NB*2 KB <= 152 KB.
-__host__ __device__ constexpr int skinny_depth(int mb, int nb, bool lds_b) {
+// stages x NB*2 KB <= 152 KB, less the scale panels ((MB + NB) KB per wave).
+__host__ __device__ constexpr int skinny_depth(int mb, int nb, bool lds_b, bool scp = false) {
+    const int lds = 152 * 1024 - (scp ? kSkinnyWaves * (mb + nb) * 1024 : 0);
     int d = lds_b ? (150 - 8 * mb * nb) / (8 * mb + 6) : (150 - 4 * mb * nb) / (8 * (mb + nb) + 6);
-    if (lds_b && d > 152 * 1024 / (kSkinnyWaves * nb * 2048)) d = 152 * 1024 / (kSkinnyWaves * nb * 2048);
+    if (lds_b && d > lds / (kSkinnyWaves * nb * 2048)) d = lds / (kSkinnyWaves * nb * 2048);
     return d > 8 ? 8 : (d < 2 ? 2 : d);
 }
 
@@ -89,7 +105,7 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int FMT, ScaleKind SK, BLay BL, int MB, int NB, bool BF16>
+template <int FMT, ScaleKind SK, BLay BL, int MB, int NB, bool BF16, bool SCP = false>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const SkinnyArgs sp) {
     constexpr int BKB = 128, W = kSkinnyWaves;
     static_assert(MB == 1 || MB == 2 || MB == 4, "16, 32 or 64 rows per M-tile");
@@ -100,7 +116,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     constexpr bool MX = (SK == ScaleKind::MX);
     constexpr bool VALU_SCALE = (SK == ScaleKind::BSF32);
     constexpr bool LDS_B = (BL != kBFrag);
-    constexpr int D = skinny_depth(MB, NB, LDS_B);
+    static_assert(!SCP || SK == ScaleKind::MX, "scale panels hold E8M0 bytes");
+    constexpr int D = skinny_depth(MB, NB, LDS_B, SCP);
+    constexpr int KT_BYTES = FP4 ? 8 : 4;          // MX scale bytes per row and K-tile
+    constexpr int PANEL_W = (MB + NB) * 1024;      // a wave's panel: 16-row blocks x 64-byte rows
     constexpr int ROWS = MB * 16, COLS = NB * 16;
     constexpr int RP = COLS + 4;           // reduction row pitch in floats (breaks the bank period)
     constexpr int REGION = ROWS * RP;
@@ -117,6 +136,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     __shared__ __attribute__((aligned(16))) uint8_t ring5[D > 5 ? RING : 16];
     __shared__ __attribute__((aligned(16))) uint8_t ring6[D > 6 ? RING : 16];
     __shared__ __attribute__((aligned(16))) uint8_t ring7[D > 7 ? RING : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t spanel[SCP ? W * PANEL_W : 16];
     // two reduction regions; with the LDS ring they reuse ring0 once every
     // wave has left the K loop
     constexpr int RED_BYTES = 2 * REGION * 4;
@@ -241,7 +261,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
         }
 #pragma unroll
         for (int i = 0; i < MB; ++i) s.a[i] = cat8(ld16(rA, aoff[i][0], kt * BKB), ld16(rA, aoff[i][1], kt * BKB));
-        if constexpr (MX) {
+        if constexpr (SCP) {
+            // scale bytes come from the wave's panel (compute)
+        } else if constexpr (MX) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 if constexpr (FP4) s.sa[i] = __builtin_amdgcn_raw_buffer_load_b16(rSA, sa_voff[i], kt * sa_kstep, 0);
@@ -289,7 +311,18 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
                                                                          s.sb[j], 0, s.sa[i]);
         }
     };
-    auto compute = [&](auto dc, const Stage& s) {
+    auto compute = [&](auto dc, const Stage& s0, int kl) {
+        // kl: the K-tile's index in the wave's run (scale panel column)
+        Stage s = s0;
+        if constexpr (SCP) {
+            const QG_LDS uint8_t* pw = (const QG_LDS uint8_t*)spanel + w * PANEL_W + l16 * 64 + kl * KT_BYTES;
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                s.sa[i] = FP4 ? *(const QG_LDS uint16_t*)(pw + i * 1024 + 2 * q) : pw[i * 1024 + q];
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                s.sb[j] = FP4 ? *(const QG_LDS uint16_t*)(pw + (MB + j) * 1024 + 2 * q) : pw[(MB + j) * 1024 + q];
+        }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             i32x8 bf;
@@ -305,26 +338,48 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     };
 
     // ---- K loop: wave w takes K-tiles kt_begin + w, + W, ...; D in flight ----
-    const int kfirst = kt_begin + w;
-    const int ntw = (kt_end - kfirst + W - 1) / W;     // K-tiles of this wave
+    // interleaved K-tiles (wave w: kt_begin + w, + W, ...) or, with scale
+    // panels, a contiguous run per wave
+    const int run = SCP ? skinny_panel_run(kt_end - kt_begin, W, KT_BYTES) : 1;
+    const int kfirst = kt_begin + (SCP ? w * run : w);
+    const int kstep = SCP ? 1 : W;
+    const int ntw = SCP ? max(0, min(kt_end, kfirst + run) - kfirst)
+                        : (kt_end - kfirst + W - 1) / W;     // K-tiles of this wave
     if (ntw > 0) {
+        if constexpr (SCP) {
+            // the run's scale bytes, 64 per row: 4 lanes per row, 16 rows per
+            // DMA (one cache line per row for the whole run); the byte range
+            // of the scale array bounds the buffer (the run's end may pass K)
+            QG_LDS uint8_t* pw = (QG_LDS uint8_t*)spanel + w * PANEL_W;
+            const int kb = kfirst * KT_BYTES + (L & 3) * 16;
+            const auto rSAp = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SFA), 0,
+                                                                (unsigned)((M - 1) * SFA_SM + nk * KT_BYTES), 0x00020000);
+            const auto rSBp = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SFB), 0,
+                                                                (unsigned)((N - 1) * SFB_SN + nk * KT_BYTES), 0x00020000);
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                dma16_buf(rSAp, pw + i * 1024, min(m0 + i * 16 + (L >> 2), M - 1) * SFA_SM + kb, 0);
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                dma16_buf(rSBp, pw + (MB + j) * 1024, min(n0 + j * 16 + (L >> 2), N - 1) * SFB_SN + kb, 0);
+        }
         Stage st[D];
         static_for<D>([&](auto dc) {
             constexpr int d = decltype(dc)::value;
-            load(dc, st[d], kfirst + W * d, d < ntw);
+            load(dc, st[d], kfirst + kstep * d, d < ntw);
         });
         int i = 0;
         for (; i + D <= ntw; i += D) {
             static_for<D>([&](auto dc) {
                 constexpr int d = decltype(dc)::value;
-                compute(dc, st[d]);
-                load(dc, st[d], kfirst + W * (i + d + D), i + d + D < ntw);
+                compute(dc, st[d], i + d);
+                load(dc, st[d], kfirst + kstep * (i + d + D), i + d + D < ntw);
                 __builtin_amdgcn_sched_barrier(0);   // keep the ring order
             });
         }
         static_for<D - 1>([&](auto dc) {
             constexpr int d = decltype(dc)::value;
-            if (d < ntw - i) compute(dc, st[d]);
+            if (d < ntw - i) compute(dc, st[d], i + d);
         });
     }
 
@@ -458,6 +513,13 @@ hipError_t launch_skinny_family(const SkinnyArgs& a, int mb, int nb, int batch, 
     const dim3 block(kSkinnyWaves * 64);
 #define QG_SKINNY_CASE(MBV, NBV)                                                                  \
     if (mb == MBV && nb == NBV) {                                                                 \
+        if constexpr (SK == ScaleKind::MX && skinny_scp_fits(MBV, NBV)) {                         \
+            if (a.scale_panel) {                                                                  \
+                if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true, true><<<grid, block, 0, s>>>(a); \
+                else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false, true><<<grid, block, 0, s>>>(a);     \
+                return hipGetLastError();                                                         \
+            }                                                                                     \
+        }                                                                                         \
         if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true><<<grid, block, 0, s>>>(a);      \
         else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false><<<grid, block, 0, s>>>(a);          \
         return hipGetLastError();                                                                 \

@@ -72,7 +72,7 @@ def test_splitk_rearms_workspace(qgemm, gpu):
 
 # ----------------------------------------------------------------- MXFP4
 MX4_DECODE = [(1, 2112, 7168), (4, 1000, 2048), (16, 4096, 512), (31, 512, 4096), (64, 7168, 1024),
-              (200, 768, 1536)]
+              (200, 768, 1536), (8, 7168, 16384), (32, 2048, 16384)]
 
 
 @pytest.mark.parametrize("m,n,k", MX4_DECODE)
@@ -83,6 +83,20 @@ def test_mxfp4_skinny(qgemm, gpu, m, n, k, split):
     y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
                               to_dev(eb, None, gpu), dtype=torch.bfloat16, workspace=None if split else False)
     assert_close(ref, out_to_f32(y), f"mxfp4 skinny {m}x{n}x{k} split={split}")
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 2112, 7168), (5, 4096, 16384), (32, 1000, 4096)])
+def test_mxfp4_skinny_k_pattern(qgemm, gpu, m, n, k):
+    """Distinct per-K-group scales on both operands through the skinny
+    kernel (per-wave scale panels and the interleaved path)."""
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=13)
+    g = np.arange(k // 32)
+    ea = np.broadcast_to((119 + g % 15).astype(np.uint8), ea.shape).copy()
+    eb = np.broadcast_to((122 + (7 * g) % 9).astype(np.uint8), eb.shape).copy()
+    ref = O.gemm_mx4(qa, qb, ea, eb)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.float32)
+    assert_close(ref, out_to_f32(y), f"mxfp4 skinny K-pattern {m}x{n}x{k}")
 
 
 # ----------------------------------------------- block-scale, fp32 scales
