@@ -307,14 +307,19 @@ hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bo
     s.kt_per_split = pl.kt_per_split;
     s.n_tiles = pl.n_tiles;
     s.m_tiles = pl.m_tiles;
-    // MX: per-wave scale panels when a wave's run fits one 64-byte panel row
-    // and the 16-byte DMAs stay aligned (skinny_gemm.hpp)
-    if (kind == SkinnyKind::MX8_RAW || kind == SkinnyKind::MX4_RAW) {
+    // per-wave scale panels when a wave's run fits one 64-byte panel row and
+    // the 16-byte DMAs stay aligned (skinny_gemm.hpp); fp32 scales need
+    // row-major row scales (K-tiles contiguous)
+    {
+        const bool mx = kind == SkinnyKind::MX8_RAW || kind == SkinnyKind::MX4_RAW;
         const int kt_bytes = kind == SkinnyKind::MX4_RAW ? 8 : 4;
-        const bool aligned16 = aligned(t.sfa, 16) && aligned(t.sfb, 16) && t.sfa_sm % 16 == 0 &&
-                               t.sfb_sn % 16 == 0 && (batch == 1 || (t.sfa_batch % 16 == 0 && t.sfb_batch % 16 == 0));
+        const int unit = mx ? 1 : 4;    // bytes per stride / batch-stride count
+        const bool layout = mx || t.sfa_sk == 1;
+        const bool aligned16 = aligned(t.sfa, 16) && aligned(t.sfb, 16) && (t.sfa_sm * unit) % 16 == 0 &&
+                               (t.sfb_sn * unit) % 16 == 0 &&
+                               (batch == 1 || ((t.sfa_batch * unit) % 16 == 0 && (t.sfb_batch * unit) % 16 == 0));
         const int run = qg::skinny_panel_run(pl.kt_per_split, qg::kSkinnyWaves, kt_bytes);
-        s.scale_panel = aligned16 && qg::skinny_scp_fits(pl.mb, pl.nb) && run * kt_bytes <= 64 &&
+        s.scale_panel = layout && aligned16 && qg::skinny_scp_fits(pl.mb, pl.nb, mx) && run * kt_bytes <= 64 &&
                         ceil_div(pl.kt_per_split, run) >= 6 &&    // keep most waves busy
                         (pl.splitk == 1 || pl.kt_per_split % (16 / kt_bytes) == 0);
     }

@@ -73,9 +73,10 @@ __host__ __device__ constexpr int skinny_panel_run(int slice_kt, int waves, int 
     const int g = 16 / kt_bytes;
     return ((slice_kt + waves - 1) / waves + g - 1) / g * g;
 }
-// the panels fit next to at least two LDS ring stages of B
-__host__ __device__ constexpr bool skinny_scp_fits(int mb, int nb) {
-    return 2 * 8 * nb * 2048 + 8 * (mb + nb) * 1024 <= 152 * 1024;
+// the panels fit next to at least two LDS ring stages of B (mx: B rows
+// have panel blocks too)
+__host__ __device__ constexpr bool skinny_scp_fits(int mb, int nb, bool mx = true) {
+    return 2 * 8 * nb * 2048 + 8 * (mb + (mx ? nb : 1)) * 1024 <= 152 * 1024;
 }
 
 // blockIdx.x -> (n-tile, m-tile): the m-tiles that share one B slice get
@@ -88,8 +89,8 @@ __host__ __device__ inline int skinny_grid_x(int n_tiles, int m_tiles) { return 
 // (8*MB dwords + scales) next to 4*MB*NB accumulators (and, without the LDS
 // ring, 8*NB dwords of B per stage).  LDS budget (LDS ring): 8 waves x D
 // stages x NB*2 KB <= 152 KB, less the scale panels ((MB + NB) KB per wave).
-__host__ __device__ constexpr int skinny_depth(int mb, int nb, bool lds_b, bool scp = false) {
-    const int lds = 152 * 1024 - (scp ? kSkinnyWaves * (mb + nb) * 1024 : 0);
+__host__ __device__ constexpr int skinny_depth(int mb, int nb, bool lds_b, bool scp = false, bool mx = true) {
+    const int lds = 152 * 1024 - (scp ? kSkinnyWaves * (mb + (mx ? nb : 1)) * 1024 : 0);
     int d = lds_b ? (150 - 8 * mb * nb) / (8 * mb + 6) : (150 - 4 * mb * nb) / (8 * (mb + nb) + 6);
     if (lds_b && d > lds / (kSkinnyWaves * nb * 2048)) d = lds / (kSkinnyWaves * nb * 2048);
     return d > 8 ? 8 : (d < 2 ? 2 : d);
@@ -116,10 +117,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     constexpr bool MX = (SK == ScaleKind::MX);
     constexpr bool VALU_SCALE = (SK == ScaleKind::BSF32);
     constexpr bool LDS_B = (BL != kBFrag);
-    static_assert(!SCP || SK == ScaleKind::MX, "scale panels hold E8M0 bytes");
-    constexpr int D = skinny_depth(MB, NB, LDS_B, SCP);
-    constexpr int KT_BYTES = FP4 ? 8 : 4;          // MX scale bytes per row and K-tile
-    constexpr int PANEL_W = (MB + NB) * 1024;      // a wave's panel: 16-row blocks x 64-byte rows
+    constexpr int D = skinny_depth(MB, NB, LDS_B, SCP, SK == ScaleKind::MX);
+    // scale bytes per row and K-tile: E8M0 bytes (MX) or one fp32 word
+    constexpr int KT_BYTES = FP4 ? 8 : 4;
+    // a wave's panel: 16-row blocks x 64-byte rows -- MX: A and B rows;
+    // fp32 scales: A rows and one block whose rows all hold the tile's
+    // 128-column weight-scale row (row-major row scales only)
+    constexpr int PB_BLOCKS = MB + (MX ? NB : 1);
+    constexpr int PANEL_W = PB_BLOCKS * 1024;
     constexpr int ROWS = MB * 16, COLS = NB * 16;
     constexpr int RP = COLS + 4;           // reduction row pitch in floats (breaks the bank period)
     constexpr int REGION = ROWS * RP;
@@ -262,7 +267,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
 #pragma unroll
         for (int i = 0; i < MB; ++i) s.a[i] = cat8(ld16(rA, aoff[i][0], kt * BKB), ld16(rA, aoff[i][1], kt * BKB));
         if constexpr (SCP) {
-            // scale bytes come from the wave's panel (compute)
+            // scales come from the wave's panel (compute)
         } else if constexpr (MX) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
@@ -314,7 +319,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     auto compute = [&](auto dc, const Stage& s0, int kl) {
         // kl: the K-tile's index in the wave's run (scale panel column)
         Stage s = s0;
-        if constexpr (SCP) {
+        if constexpr (SCP && MX) {
             const QG_LDS uint8_t* pw = (const QG_LDS uint8_t*)spanel + w * PANEL_W + l16 * 64 + kl * KT_BYTES;
 #pragma unroll
             for (int i = 0; i < MB; ++i)
@@ -322,6 +327,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
 #pragma unroll
             for (int j = 0; j < NB; ++j)
                 s.sb[j] = FP4 ? *(const QG_LDS uint16_t*)(pw + (MB + j) * 1024 + 2 * q) : pw[(MB + j) * 1024 + q];
+        } else if constexpr (SCP) {
+            const QG_LDS uint8_t* pw = (const QG_LDS uint8_t*)spanel + w * PANEL_W + kl * 4;
+#pragma unroll
+            for (int i = 0; i < MB; ++i) s.fa[i] = *(const QG_LDS float*)(pw + i * 1024 + l16 * 64);
+            s.fb = *(const QG_LDS float*)(pw + MB * 1024);
         }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
@@ -352,16 +362,25 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
             // of the scale array bounds the buffer (the run's end may pass K)
             QG_LDS uint8_t* pw = (QG_LDS uint8_t*)spanel + w * PANEL_W;
             const int kb = kfirst * KT_BYTES + (L & 3) * 16;
+            // row strides in bytes (the fp32 strides count words)
+            const int a_rs = MX ? SFA_SM : 4 * SFA_SM, b_rs = MX ? SFB_SN : 4 * SFB_SN;
             const auto rSAp = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SFA), 0,
-                                                                (unsigned)((M - 1) * SFA_SM + nk * KT_BYTES), 0x00020000);
-            const auto rSBp = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SFB), 0,
-                                                                (unsigned)((N - 1) * SFB_SN + nk * KT_BYTES), 0x00020000);
+                                                                (unsigned)((M - 1) * a_rs + nk * KT_BYTES), 0x00020000);
 #pragma unroll
             for (int i = 0; i < MB; ++i)
-                dma16_buf(rSAp, pw + i * 1024, min(m0 + i * 16 + (L >> 2), M - 1) * SFA_SM + kb, 0);
+                dma16_buf(rSAp, pw + i * 1024, min(m0 + i * 16 + (L >> 2), M - 1) * a_rs + kb, 0);
+            if constexpr (MX) {
+                const auto rSBp = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SFB), 0,
+                                                                    (unsigned)((N - 1) * b_rs + nk * KT_BYTES), 0x00020000);
 #pragma unroll
-            for (int j = 0; j < NB; ++j)
-                dma16_buf(rSBp, pw + (MB + j) * 1024, min(n0 + j * 16 + (L >> 2), N - 1) * SFB_SN + kb, 0);
+                for (int j = 0; j < NB; ++j)
+                    dma16_buf(rSBp, pw + (MB + j) * 1024, min(n0 + j * 16 + (L >> 2), N - 1) * b_rs + kb, 0);
+            } else {
+                const int nbr = (N - 1) >> 7;    // last 128-column scale row
+                const auto rSBp = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SFB), 0,
+                                                                    (unsigned)(nbr * b_rs + nk * KT_BYTES), 0x00020000);
+                dma16_buf(rSBp, pw + MB * 1024, min(n0 >> 7, nbr) * b_rs + kb, 0);
+            }
         }
         Stage st[D];
         static_for<D>([&](auto dc) {
@@ -513,7 +532,7 @@ hipError_t launch_skinny_family(const SkinnyArgs& a, int mb, int nb, int batch, 
     const dim3 block(kSkinnyWaves * 64);
 #define QG_SKINNY_CASE(MBV, NBV)                                                                  \
     if (mb == MBV && nb == NBV) {                                                                 \
-        if constexpr (SK == ScaleKind::MX && skinny_scp_fits(MBV, NBV)) {                         \
+        if constexpr (skinny_scp_fits(MBV, NBV, SK == ScaleKind::MX)) {                           \
             if (a.scale_panel) {                                                                  \
                 if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true, true><<<grid, block, 0, s>>>(a); \
                 else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false, true><<<grid, block, 0, s>>>(a);     \

@@ -59,7 +59,12 @@ def parse():
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--workload", default="mxfp8_8192", choices=sorted(WORKLOADS))
     p.add_argument("--m", type=int, default=None, help="override M (decode sweeps)")
+    p.add_argument("--n", type=int, default=None, help="override N")
+    p.add_argument("--k", type=int, default=None, help="override K")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--sfa-km", action="store_true",
+                   help="block-scale fp32 workloads: pass A's scales column-major [K/128][M] (the reference's "
+                        "layout) instead of BASELINE's row-major [M][K/128]")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--sweep", action="store_true",
                    help="BASELINE configs[2]: time the block-scale shape sweep (bpreshuffle and ldsbypass), "
@@ -246,6 +251,10 @@ def main():
     fam, M, N, K, cfg = WORKLOADS[args.workload]
     if args.m:
         M = args.m
+    if args.n:
+        N = args.n
+    if args.k:
+        K = args.k
     hbm_bound = M <= 256
     kg32, kg128 = K // 32, K // 128
     if fam == "bs8":
@@ -277,7 +286,7 @@ def main():
         qb, sb = O.quant_bs_wgt(b)
     if fam != "bs8":
         A = torch.from_numpy(qa).to(dev)
-        SA = torch.from_numpy(sa).to(dev)
+        SA = torch.from_numpy(np.ascontiguousarray(sa.T) if args.sfa_km else sa).to(dev)
         B0 = torch.from_numpy(qb).to(dev)
         SB0 = torch.from_numpy(sb).to(dev)
     if fam == "bs":
@@ -310,12 +319,14 @@ def main():
                 return 0
         elif fam == "bs":
             args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K, N * K, M * N,
-                            SA.data_ptr(), SB.data_ptr(), 1 if M > 1 else M, kg128, M * kg128, SB.numel())
+                            SA.data_ptr(), SB.data_ptr(), M if args.sfa_km else (1 if M > 1 else M), kg128,
+                            M * kg128, SB.numel())
             fn, wq = L.gemm_a8w8_blockscale_bpreshuffle, L.gemm_a8w8_blockscale_bpreshuffle_workspace_bytes
         else:
             args_ = q.LdsBypassKargs(A.data_ptr(), None, B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K,
-                                     N * K, M * N, SA.data_ptr(), SB.data_ptr(), 1 if M > 1 else M, kg128,
-                                     M * kg128, SB.numel(), B.numel())
+                                     N * K, M * N, SA.data_ptr(), SB.data_ptr(),
+                                     M if args.sfa_km else (1 if M > 1 else M), kg128, M * kg128, SB.numel(),
+                                     B.numel())
             fn, wq = L.gemm_a8w8_blockscale_ldsbypass, L.gemm_a8w8_blockscale_ldsbypass_workspace_bytes
         calls.append((fn, args_))
     ws_bytes = max(1, wq(ctypes.byref(calls[0][1])))
@@ -372,7 +383,7 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
 
     kind = "fp4" if fam == "mx4" else "fp8"
-    tag = args.workload if args.m is None else f"{args.workload}_m{M}"
+    tag = args.workload + (f"_m{M}" if args.m else "") + (f"_n{N}" if args.n else "") + (f"_k{K}" if args.k else "")
     if hbm_bound:
         # algorithmic bytes: A, B and both scale arrays read once, C written once
         alg = (A.numel() * A.element_size() + SA.numel() * SA.element_size() + b_bytes + C.numel() * 2)

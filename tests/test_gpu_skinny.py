@@ -102,7 +102,7 @@ def test_mxfp4_skinny_k_pattern(qgemm, gpu, m, n, k):
 # ----------------------------------------------- block-scale, fp32 scales
 BS_DECODE = [(1, 2112, 7168), (1, 7168, 2048), (4, 24576, 1536), (32, 2112, 7168), (48, 300, 1024),
              (32, 1536, 7168), (64, 1536, 7168), (17, 1000, 4096), (2, 200, 26624),
-             (64, 7168, 512), (128, 4096, 1024)]
+             (64, 7168, 512), (128, 4096, 1024), (48, 7168, 8192)]
 
 
 @pytest.mark.parametrize("m,n,k", BS_DECODE)
