@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
         if constexpr (BF16) {
             uint16_t* c = (uint16_t*)p.c + (long long)bz * p.c_batch + (long long)m * LDC + n;
             if (vec_ok && n + 3 < N) {
-                __builtin_nontemporal_store(u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, (u32x2*)c);
+                *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             } else {
                 for (int r = 0; r < 4; ++r)
                     if (n + r < N) c[r] = bf16_bits(v[r]);
@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
         } else {
             float* c = (float*)p.c + (long long)bz * p.c_batch + (long long)m * LDC + n;
             if (vec_ok && n + 3 < N) {
-                __builtin_nontemporal_store(v, (f32x4*)c);
+                *(f32x4*)c = v;
             } else {
                 for (int r = 0; r < 4; ++r)
                     if (n + r < N) c[r] = v[r];
