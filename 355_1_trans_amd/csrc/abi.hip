@@ -15,6 +15,7 @@
 #include "qgemm.h"
 #include "decode_gemm.hpp"
 #include "mid_gemm.hpp"
+#include "stream_gemm.hpp"
 
 static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "reference kargs ABI");
@@ -253,6 +254,37 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
     return p;
 }
 
+// Row-streaming decode kernel (stream_gemm.hpp): M <= kStreamMaxM with
+// row-major MX B.  It needs no workspace; A (every row and piece) and its
+// scales sit in LDS, which bounds K; A's scales move as dwords.  Its matrix
+// work grows with M (one MFMA per row of A and 2048 K elements of B): at
+// N = 7168, K = 16384 it beats the skinny kernel up to M = 4 and loses at
+// M = 8 (MXFP4 20.6 vs 17.0 us).
+constexpr int kStreamMaxM = 4;
+constexpr int kStreamMinN = 256;
+
+bool stream_ok(const opus_gemm_scale_kargs& a, bool fp4) {
+    (void)fp4;
+    if (a.m > kStreamMaxM || a.n < kStreamMinN) return false;
+    if (a.k > qg::kStreamMaxK) return false;
+    if (!dma_aligned(a, false) || a.stride_b % 16 || !aligned(a.ptr_sfa, 4) || a.stride_sfa % 4) return false;
+    return a.batch == 1 || a.stride_sfa_batch % 4 == 0;
+}
+
+// About one workgroup per CU: R rows of B each, at most kStreamMaxRows and
+// as many as the LDS image of their scales holds (256 bytes per 4 pieces).
+hipError_t run_stream(const TileArgs& t, int batch, bool fp4, bool bf16, hipStream_t stream) {
+    qg::StreamArgs s{};
+    s.t = t;
+    const long long rows = (long long)t.n * batch;
+    const int np = ceil_div(t.kbytes, fp4 ? 1024 : 2048);
+    const int r_lds = qg::kStreamWsBytes / (256 * ceil_div(np, 4));
+    s.rows_per_wg = (int)std::min<long long>(std::min(qg::kStreamMaxRows, r_lds),
+                                             std::max<long long>(1, (rows + kCUs - 1) / kCUs));
+    const int mb = t.m <= 1 ? 1 : (t.m <= 2 ? 2 : 4);
+    return qg::launch_stream(s, fp4, mb, batch, bf16, stream);
+}
+
 // Launches the 128 x 128 fp32-block-scale kernel; a NULL workspace runs it
 // without a K split.
 hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, bool frag, void* ws, size_t ws_bytes, int k_tiles,
@@ -445,6 +477,7 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    if (stream_ok(a, false)) return run_stream(t, a.batch, false, bf16, stream);
     const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
@@ -471,6 +504,7 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    if (stream_ok(a, true)) return run_stream(t, a.batch, true, bf16, stream);
     const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false);
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);

@@ -1,0 +1,134 @@
+"""GPU parity of the row-streaming decode kernel (MXFP8 / MXFP4 with M <= 4,
+row-major B) against the CPU oracle: partial last pieces (K not a multiple
+of 2048), the largest K the kernel holds in LDS, N tails, every M from 1 to
+8 (M > 4: the routing boundary to the skinny kernel), per-K-group scale
+patterns on both operands (which pin the lane -> E8M0 group routing of both
+formats), padded strides with batching through the C ABI, fp32 and bf16
+outputs, and bit-identical repeated calls."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import assert_close, make_mx4, make_mx8, out_to_f32, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _fp8(x, dev):
+    return to_dev(x, None, dev).view(torch.float8_e4m3fn)
+
+
+# (m, n, k): K = 16384 is configs[4] and the largest K the kernel holds in LDS
+# (K = 32768 goes to the skinny kernel); 7168 and 2304 end in a partial
+# piece, 256 / 128 are a single partial piece
+MX4_STREAM = [(1, 7168, 16384), (8, 7168, 16384), (3, 1000, 7168), (5, 4100, 256), (2, 512, 32768),
+              (7, 257, 2304), (4, 2048, 4096), (6, 300, 1024)]
+MX8_STREAM = [(1, 7168, 16384), (8, 2112, 7168), (6, 300, 128), (1, 4096, 2048), (2, 1536, 7168),
+              (3, 777, 640), (5, 7168, 2048), (4, 2560, 16384)]
+
+
+@pytest.mark.parametrize("m,n,k", MX4_STREAM)
+def test_mxfp4_stream(qgemm, gpu, m, n, k):
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=7 * m + n + k)
+    ref = O.gemm_mx4(qa, qb, ea, eb)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.bfloat16)
+    assert_close(ref, out_to_f32(y), f"mxfp4 stream {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", MX8_STREAM)
+def test_mxfp8_stream(qgemm, gpu, m, n, k):
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=5 * m + n + k)
+    ref = O.gemm_mx8(qa, qb, ea, eb)
+    y = qgemm.gemm_a8w8_mxfp8(_fp8(qa, gpu), _fp8(qb, gpu), to_dev(ea, None, gpu), to_dev(eb, None, gpu),
+                              dtype=torch.bfloat16)
+    assert_close(ref, out_to_f32(y), f"mxfp8 stream {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", range(1, 9))
+def test_stream_every_m(qgemm, gpu, m):
+    n, k = 640, 6144
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=90 + m)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.float32)
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"mxfp4 stream m={m}")
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=190 + m)
+    y = qgemm.gemm_a8w8_mxfp8(_fp8(qa, gpu), _fp8(qb, gpu), to_dev(ea, None, gpu), to_dev(eb, None, gpu),
+                              dtype=torch.float32)
+    assert_close(O.gemm_mx8(qa, qb, ea, eb), out_to_f32(y), f"mxfp8 stream m={m}")
+
+
+def _k_pattern(ea, eb):
+    g = np.arange(ea.shape[1])
+    ea = np.broadcast_to((116 + g % 19).astype(np.uint8), ea.shape).copy()
+    eb = np.broadcast_to((120 + (7 * g) % 13).astype(np.uint8), eb.shape).copy()
+    return ea, eb
+
+
+@pytest.mark.parametrize("k", [4096, 7168])
+def test_stream_k_pattern_scales(qgemm, gpu, k):
+    """Distinct E8M0 per K group on both operands: a lane whose data and
+    scale byte come from different groups scales products by the wrong
+    power of two, far outside the tolerance."""
+    m, n = 3, 768
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=k + 1)
+    ea, eb = _k_pattern(ea, eb)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.float32)
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), "mxfp4 stream K-pattern")
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=k + 2)
+    ea, eb = _k_pattern(ea, eb)
+    y = qgemm.gemm_a8w8_mxfp8(_fp8(qa, gpu), _fp8(qb, gpu), to_dev(ea, None, gpu), to_dev(eb, None, gpu),
+                              dtype=torch.float32)
+    assert_close(O.gemm_mx8(qa, qb, ea, eb), out_to_f32(y), "mxfp8 stream K-pattern")
+
+
+def _padded(rows, cols, pitch, batch, fill, arrays):
+    out = np.full((batch, rows, pitch), fill, dtype=np.uint8)
+    for i, a in enumerate(arrays):
+        out[i, :, :cols] = a
+    return out
+
+
+@pytest.mark.parametrize("fp4", [True, False])
+def test_stream_batched_strided(qgemm, gpu, fp4):
+    """Batch of 2 through the C ABI with padded row pitches on A, B, both
+    scale arrays and C (padding bytes are NaN codes / 0xFF scales that must
+    never be read)."""
+    m, n, k, batch = 3, 1100, 5120, 2
+    make = make_mx4 if fp4 else make_mx8
+    data = [make(m, n, k, seed=300 + i + 10 * fp4) for i in range(batch)]
+    kb = k // 2 if fp4 else k
+    kg = k // 32
+    lda, ldb, lsa, lsb, ldc = kb + 48, kb + 128, kg + 12, kg + 8, n + 24    # scale pitches: multiples of 4
+    A = torch.from_numpy(_padded(m, kb, lda, batch, 0xFF, [d[0] for d in data])).to(gpu)
+    B = torch.from_numpy(_padded(n, kb, ldb, batch, 0xFF, [d[1] for d in data])).to(gpu)
+    SA = torch.from_numpy(_padded(m, kg, lsa, batch, 0xFF, [d[2] for d in data])).to(gpu)
+    SB = torch.from_numpy(_padded(n, kg, lsb, batch, 0xFF, [d[3] for d in data])).to(gpu)
+    C = torch.zeros(batch, m, ldc, dtype=torch.float32, device=gpu)
+    args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, lda, ldb, ldc, m * lda, n * ldb,
+                       m * ldc, SA.data_ptr(), SB.data_ptr(), lsa, lsb, m * lsa, n * lsb)
+    name = "gemm_a4w4_mxfp4" if fp4 else "gemm_a8w8_mxfp8"
+    L = qgemm.lib()
+    st = getattr(L, name)(ctypes.byref(args), qgemm.OUT_FP32, None, 0,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, f"{name} returned {st}"
+    torch.cuda.synchronize()
+    gemm = O.gemm_mx4 if fp4 else O.gemm_mx8
+    Cc = C.cpu().numpy()
+    for i, d in enumerate(data):
+        assert_close(gemm(*d), Cc[i, :, :n], f"batch {i}")
+        assert not Cc[i, :, n:].any(), "wrote past N"
+
+
+def test_stream_deterministic(qgemm, gpu):
+    m, n, k = 3, 7168, 16384
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=5)
+    args = [to_dev(x, None, gpu) for x in (qa, qb, ea, eb)]
+    y0 = qgemm.gemm_a4w4_mxfp4(*args, dtype=torch.float32)
+    y1 = qgemm.gemm_a4w4_mxfp4(*args, dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
