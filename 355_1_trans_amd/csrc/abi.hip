@@ -256,11 +256,10 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
 
 // Row-streaming decode kernel (stream_gemm.hpp): M <= kStreamMaxM with
 // row-major MX B.  It needs no workspace; A (every row and piece) and its
-// scales sit in LDS, which bounds K; A's scales move as dwords.  Its matrix
-// work grows with M (one MFMA per row of A and 2048 K elements of B): at
-// N = 7168, K = 16384 it beats the skinny kernel up to M = 4 and loses at
-// M = 8 (MXFP4 20.6 vs 17.0 us).
-constexpr int kStreamMaxM = 4;
+// scales sit in LDS, which bounds K; A's scales move as dwords.  One MFMA
+// covers wr rows of B and wr rows of A (a quarter of its products are used
+// at wr = 4, a sixteenth at wr = 1), so wr grows with M.
+constexpr int kStreamMaxM = 8;
 constexpr int kStreamMinN = 256;
 
 bool stream_ok(const opus_gemm_scale_kargs& a, bool fp4) {
@@ -272,17 +271,24 @@ bool stream_ok(const opus_gemm_scale_kargs& a, bool fp4) {
 }
 
 // About one workgroup per CU: R rows of B each, at most kStreamMaxRows and
-// as many as the LDS image of their scales holds (256 bytes per 4 pieces).
+// as many as the LDS image of their scales holds (256 bytes per 8192 K).
 hipError_t run_stream(const TileArgs& t, int batch, bool fp4, bool bf16, hipStream_t stream) {
     qg::StreamArgs s{};
     s.t = t;
     const long long rows = (long long)t.n * batch;
-    const int np = ceil_div(t.kbytes, fp4 ? 1024 : 2048);
-    const int r_lds = qg::kStreamWsBytes / (256 * ceil_div(np, 4));
+    const int ngroups = t.kbytes / (fp4 ? 16 : 32);
+    const int r_lds = qg::kStreamWsBytes / (256 * ceil_div(ngroups, 256));
     s.rows_per_wg = (int)std::min<long long>(std::min(qg::kStreamMaxRows, r_lds),
                                              std::max<long long>(1, (rows + kCUs - 1) / kCUs));
-    const int mb = t.m <= 1 ? 1 : (t.m <= 2 ? 2 : 4);
-    return qg::launch_stream(s, fp4, mb, batch, bf16, stream);
+    // measured at N = 7168, K = 16384 (MXFP4 / MXFP8 us): M = 4 wr 1, 2, 4:
+    // 15.8, 14.5, 14.0 / 23.6, 22.0, 22.2; M = 8 wr 2, 4: 18.0, 15.6 / 24.4,
+    // 22.5 (skinny kernel: 16.7 / 24.9); M = 2 wr 1 and 2 alike
+    int wr, mb;
+    if (t.m == 1) { wr = 1; mb = 1; }
+    else if (t.m == 2) { wr = 2; mb = 2; }
+    else if (t.m <= 4) { wr = 4; mb = 4; }
+    else { wr = 4; mb = 8; }
+    return qg::launch_stream(s, fp4, wr, mb, batch, bf16, stream);
 }
 
 // Launches the 128 x 128 fp32-block-scale kernel; a NULL workspace runs it

@@ -1,21 +1,23 @@
-// Instantiations and launcher of the row-streaming decode kernel (M <= 4,
-// row-major MX B).
+// Instantiations and launcher of the row-streaming decode kernel (M <= 8,
+// row-major MX B; wr rows of B per MFMA, mb rows of A).
 #include "stream_gemm.hpp"
 #include "launch.hpp"
 
 namespace qg {
 
-hipError_t launch_stream(const StreamArgs& a, bool fp4, int mb, int batch, bool bf16, hipStream_t s) {
+hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batch, bool bf16, hipStream_t s) {
     if (a.rows_per_wg < 1 || a.rows_per_wg > kStreamMaxRows) return hipErrorInvalidValue;
     const dim3 grid((a.t.n + a.rows_per_wg - 1) / a.rows_per_wg, batch);
-#define QG_STREAM_CASE(F, MBV)                                                                     \
-    if (fp4 == F && mb == MBV) {                                                                   \
-        if (bf16) stream_gemm_kernel<F, MBV, true><<<grid, kStreamWaves * 64, 0, s>>>(a);          \
-        else stream_gemm_kernel<F, MBV, false><<<grid, kStreamWaves * 64, 0, s>>>(a);              \
+#define QG_STREAM_CASE(F, WRV, MBV)                                                                \
+    if (fp4 == F && wr == WRV && mb == MBV) {                                                      \
+        if (bf16) stream_gemm_kernel<F, WRV, MBV, true><<<grid, kStreamWaves * 64, 0, s>>>(a);     \
+        else stream_gemm_kernel<F, WRV, MBV, false><<<grid, kStreamWaves * 64, 0, s>>>(a);         \
         return hipGetLastError();                                                                  \
     }
-    QG_STREAM_CASE(true, 1) QG_STREAM_CASE(true, 2) QG_STREAM_CASE(true, 4)
-    QG_STREAM_CASE(false, 1) QG_STREAM_CASE(false, 2) QG_STREAM_CASE(false, 4)
+#define QG_STREAM_FMT(F) QG_STREAM_CASE(F, 1, 1) QG_STREAM_CASE(F, 2, 2) QG_STREAM_CASE(F, 4, 4) QG_STREAM_CASE(F, 4, 8)
+    QG_STREAM_FMT(true)
+    QG_STREAM_FMT(false)
+#undef QG_STREAM_FMT
 #undef QG_STREAM_CASE
     return hipErrorInvalidValue;
 }

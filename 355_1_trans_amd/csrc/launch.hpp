@@ -29,9 +29,10 @@ hipError_t launch_skinny_mx4(const SkinnyArgs& a, int mb, int nb, int batch, boo
 // kernels_decode.hip: decode kernel (M <= 64, mb row blocks, nw waves of 16 columns)
 struct DecodeArgs;
 hipError_t launch_decode(SkinnyKind kind, const DecodeArgs& a, int mb, int nw, int batch, bool bf16, hipStream_t s);
-// kernels_stream.hip: row-streaming decode kernel (M <= mb, mb in {1, 2, 4}; row-major MX B)
+// kernels_stream.hip: row-streaming decode kernel (row-major MX B, M <= mb <= 8; wr rows
+// of B per MFMA; (wr, mb) in {(1,1), (2,2), (4,4), (4,8)})
 struct StreamArgs;
-hipError_t launch_stream(const StreamArgs& a, bool fp4, int mb, int batch, bool bf16, hipStream_t s);
+hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batch, bool bf16, hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);

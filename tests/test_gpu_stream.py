@@ -1,10 +1,11 @@
-"""GPU parity of the row-streaming decode kernel (MXFP8 / MXFP4 with M <= 4,
+"""GPU parity of the row-streaming decode kernel (MXFP8 / MXFP4 with M <= 8,
 row-major B) against the CPU oracle: partial last pieces (K not a multiple
-of 2048), the largest K the kernel holds in LDS, N tails, every M from 1 to
-8 (M > 4: the routing boundary to the skinny kernel), per-K-group scale
-patterns on both operands (which pin the lane -> E8M0 group routing of both
-formats), padded strides with batching through the C ABI, fp32 and bf16
-outputs, and bit-identical repeated calls."""
+of the segment), the largest K the kernel holds in LDS, N tails that cut a
+workgroup's last group of 2 or 4 rows, every M from 1 to 8 (1, 2 or 4 rows
+of B per MFMA), per-K-group scale patterns on both operands (which pin the
+lane -> E8M0 group routing of both formats), padded strides with batching
+through the C ABI, fp32 and bf16 outputs, and bit-identical repeated
+calls."""
 import ctypes
 
 import numpy as np
@@ -69,11 +70,12 @@ def _k_pattern(ea, eb):
 
 
 @pytest.mark.parametrize("k", [4096, 7168])
-def test_stream_k_pattern_scales(qgemm, gpu, k):
-    """Distinct E8M0 per K group on both operands: a lane whose data and
-    scale byte come from different groups scales products by the wrong
-    power of two, far outside the tolerance."""
-    m, n = 3, 768
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_stream_k_pattern_scales(qgemm, gpu, m, k):
+    """Distinct E8M0 per K group on both operands, for 1, 2 and 4 rows of B
+    per MFMA: a lane whose data and scale byte come from different groups
+    scales products by the wrong power of two, far outside the tolerance."""
+    n = 768
     qa, qb, ea, eb = make_mx4(m, n, k, seed=k + 1)
     ea, eb = _k_pattern(ea, eb)
     y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
@@ -98,7 +100,7 @@ def test_stream_batched_strided(qgemm, gpu, fp4):
     """Batch of 2 through the C ABI with padded row pitches on A, B, both
     scale arrays and C (padding bytes are NaN codes / 0xFF scales that must
     never be read)."""
-    m, n, k, batch = 3, 1100, 5120, 2
+    m, n, k, batch = 5, 1100, 5120, 2
     make = make_mx4 if fp4 else make_mx8
     data = [make(m, n, k, seed=300 + i + 10 * fp4) for i in range(batch)]
     kb = k // 2 if fp4 else k
@@ -125,7 +127,7 @@ def test_stream_batched_strided(qgemm, gpu, fp4):
 
 
 def test_stream_deterministic(qgemm, gpu):
-    m, n, k = 3, 7168, 16384
+    m, n, k = 8, 7168, 16384
     qa, qb, ea, eb = make_mx4(m, n, k, seed=5)
     args = [to_dev(x, None, gpu) for x in (qa, qb, ea, eb)]
     y0 = qgemm.gemm_a4w4_mxfp4(*args, dtype=torch.float32)
