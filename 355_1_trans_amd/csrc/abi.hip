@@ -255,40 +255,76 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
 }
 
 // Row-streaming decode kernel (stream_gemm.hpp): M <= kStreamMaxM with
-// row-major MX B.  It needs no workspace; A (every row and piece) and its
-// scales sit in LDS, which bounds K; A's scales move as dwords.  One MFMA
-// covers wr rows of B and wr rows of A (a quarter of its products are used
-// at wr = 4, a sixteenth at wr = 1), so wr grows with M.
+// row-major MX B.  One MFMA covers wr rows of B and wr rows of A (a quarter
+// of its products are used at wr = 4, a sixteenth at wr = 1), so wr grows
+// with M; past M = 8 the 16-row fragments of the skinny kernel waste less
+// matrix work.  A's K slice sits in LDS; when all of K does not fit, K is
+// split over workgroups (fp32 partials in the workspace, like the skinny
+// kernel's split).  The plan depends on the shape only, so the workspace
+// query and the launch agree.
 constexpr int kStreamMaxM = 8;
 constexpr int kStreamMinN = 256;
 
+struct StreamPlan {
+    bool ok = false;
+    int wr = 1, mb = 1, splitk = 1, seg_per_split = 1, rows = 1;
+    size_t ws_bytes = 0;
+};
+
+StreamPlan plan_stream(int m, int n, int k, int batch, bool fp4) {
+    StreamPlan p;
+    if (m > kStreamMaxM || n < kStreamMinN) return p;
+    // measured at N = 7168, K = 16384 (MXFP4 / MXFP8 us): M = 4 wr 1, 2, 4:
+    // 15.8, 14.5, 14.0 / 23.6, 22.0, 22.2; M = 8 wr 2, 4: 18.0, 15.6 / 24.4,
+    // 22.5 (skinny kernel: 16.7 / 24.9); M = 2 wr 1 and 2 alike
+    if (m == 1) { p.wr = 1; p.mb = 1; }
+    else if (m == 2) { p.wr = 2; p.mb = 2; }
+    else { p.wr = 4; p.mb = m <= 4 ? 4 : 8; }
+    const int seg = (fp4 ? 1024 : 2048) / p.wr;
+    const int nseg = ceil_div(fp4 ? k / 2 : k, seg);
+    const int cap = qg::stream_seg_cap(fp4, p.wr, p.mb);
+    p.splitk = ceil_div(nseg, cap);
+    p.seg_per_split = ceil_div(nseg, p.splitk);
+    p.splitk = ceil_div(nseg, p.seg_per_split);
+    // about one workgroup per CU; rows bounded by the waves' row groups and
+    // by the LDS image of their B scales
+    const long long nblk_target = std::max<long long>(1, kCUs / ((long long)p.splitk * batch));
+    long long rows = (n + nblk_target - 1) / nblk_target;
+    const int wsp = 1 << qg::stream_ws_log2(p.seg_per_split * 64 / p.wr);
+    rows = std::min<long long>(rows, std::min(qg::stream_max_rows(p.wr), qg::kStreamWsBytes / wsp));
+    p.rows = (int)std::max<long long>(rows, 1);
+    if (p.splitk > 1) {
+        const long long blocks = (long long)ceil_div(n, p.rows) * batch;
+        if (blocks > (long long)(kCounterBytes / sizeof(unsigned)) || (long long)m * n >= (1LL << 29)) return p;
+        p.ws_bytes = kCounterBytes + (size_t)p.splitk * batch * m * n * 4;
+    }
+    p.ok = true;
+    return p;
+}
+
 bool stream_ok(const opus_gemm_scale_kargs& a, bool fp4) {
-    (void)fp4;
-    if (a.m > kStreamMaxM || a.n < kStreamMinN) return false;
-    if (a.k > qg::kStreamMaxK) return false;
+    if (!plan_stream(a.m, a.n, a.k, a.batch, fp4).ok) return false;
     if (!dma_aligned(a, false) || a.stride_b % 16 || !aligned(a.ptr_sfa, 4) || a.stride_sfa % 4) return false;
     return a.batch == 1 || a.stride_sfa_batch % 4 == 0;
 }
 
-// About one workgroup per CU: R rows of B each, at most kStreamMaxRows and
-// as many as the LDS image of their scales holds (256 bytes per 8192 K).
-hipError_t run_stream(const TileArgs& t, int batch, bool fp4, bool bf16, hipStream_t stream) {
+// Launches the stream kernel; false when its K split needs a workspace the
+// call did not bring (the caller then runs the skinny kernel).
+bool run_stream(const TileArgs& t, int k, int batch, bool fp4, bool bf16, void* ws, size_t ws_bytes,
+                hipStream_t stream, hipError_t* st) {
+    const StreamPlan pl = plan_stream(t.m, t.n, k, batch, fp4);
     qg::StreamArgs s{};
     s.t = t;
-    const long long rows = (long long)t.n * batch;
-    const int ngroups = t.kbytes / (fp4 ? 16 : 32);
-    const int r_lds = qg::kStreamWsBytes / (256 * ceil_div(ngroups, 256));
-    s.rows_per_wg = (int)std::min<long long>(std::min(qg::kStreamMaxRows, r_lds),
-                                             std::max<long long>(1, (rows + kCUs - 1) / kCUs));
-    // measured at N = 7168, K = 16384 (MXFP4 / MXFP8 us): M = 4 wr 1, 2, 4:
-    // 15.8, 14.5, 14.0 / 23.6, 22.0, 22.2; M = 8 wr 2, 4: 18.0, 15.6 / 24.4,
-    // 22.5 (skinny kernel: 16.7 / 24.9); M = 2 wr 1 and 2 alike
-    int wr, mb;
-    if (t.m == 1) { wr = 1; mb = 1; }
-    else if (t.m == 2) { wr = 2; mb = 2; }
-    else if (t.m <= 4) { wr = 4; mb = 4; }
-    else { wr = 4; mb = 8; }
-    return qg::launch_stream(s, fp4, wr, mb, batch, bf16, stream);
+    s.rows_per_wg = pl.rows;
+    s.splitk = pl.splitk;
+    s.seg_per_split = pl.seg_per_split;
+    if (pl.splitk > 1) {
+        if (!ws || ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return false;
+        s.counters = static_cast<unsigned*>(ws);
+        s.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+    }
+    *st = qg::launch_stream(s, fp4, pl.wr, pl.mb, batch, bf16, stream);
+    return true;
 }
 
 // Launches the 128 x 128 fp32-block-scale kernel; a NULL workspace runs it
@@ -483,8 +519,12 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    if (stream_ok(a, false)) return run_stream(t, a.batch, false, bf16, stream);
     const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
+    if (stream_ok(a, false)) {
+        if (run_stream(t, a.k, a.batch, false, bf16, workspace, workspace_bytes, stream, &st)) return st;
+        // the K split's workspace is missing: the skinny kernel, without a split
+        return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, nullptr, 0, a.k / 128, stream);
+    }
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
     // (32-byte panels would cover 8 K-tiles; the loop then unrolls by 8, and
@@ -494,7 +534,9 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
 
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false).ws_bytes;
+    const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, false);
+    return std::max(sp.ok ? sp.ws_bytes : 0,
+                    plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false).ws_bytes);
 }
 
 // ---------------------------------------------------------------- MXFP4
@@ -510,8 +552,12 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    if (stream_ok(a, true)) return run_stream(t, a.batch, true, bf16, stream);
     const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false);
+    if (stream_ok(a, true)) {
+        if (run_stream(t, a.k, a.batch, true, bf16, workspace, workspace_bytes, stream, &st)) return st;
+        // the K split's workspace is missing: the skinny kernel, without a split
+        return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, nullptr, 0, a.k / 256, stream);
+    }
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);
     // 32-byte panels (4 K-tiles, two DMA lanes per scale row) need whole
@@ -522,7 +568,9 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
 
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
-    return plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false, false).ws_bytes;
+    const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, true);
+    return std::max(sp.ok ? sp.ws_bytes : 0, plan_gemm(args->m, args->n, args->k / 256, args->batch,
+                                                        (long long)args->n * args->k / 2, false, false).ws_bytes);
 }
 
 // ------------------------------------------------ block-scale FP8, E8M0 scales

@@ -6,8 +6,10 @@
 namespace qg {
 
 hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batch, bool bf16, hipStream_t s) {
-    if (a.rows_per_wg < 1 || a.rows_per_wg > kStreamMaxRows) return hipErrorInvalidValue;
-    const dim3 grid((a.t.n + a.rows_per_wg - 1) / a.rows_per_wg, batch);
+    if (a.rows_per_wg < 1 || a.rows_per_wg > stream_max_rows(wr) || a.splitk < 1 || a.seg_per_split < 1 ||
+        a.seg_per_split > stream_seg_cap(fp4, wr, mb))
+        return hipErrorInvalidValue;
+    const dim3 grid((a.t.n + a.rows_per_wg - 1) / a.rows_per_wg, batch, a.splitk);
 #define QG_STREAM_CASE(F, WRV, MBV)                                                                \
     if (fp4 == F && wr == WRV && mb == MBV) {                                                      \
         if (bf16) stream_gemm_kernel<F, WRV, MBV, true><<<grid, kStreamWaves * 64, 0, s>>>(a);     \

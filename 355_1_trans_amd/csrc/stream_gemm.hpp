@@ -45,7 +45,17 @@
 //     out-of-range offset (zeros, no traffic), so K needs no multiple of the
 //     segment (K a multiple of 128 (fp8) or 256 (fp4), the MX entries'
 //     contract); pieces past a wave's range load through an empty buffer
-//     descriptor.
+//     descriptor;
+//   * K split: A's LDS image holds 16384 K elements per row, so longer K
+//     splits over workgroups (grid.z); each writes fp32 partials
+//     device-coherently, and the last workgroup of each row block (relaxed
+//     counter, see store_partial4 in common.hpp) adds the slices in slice
+//     order and re-arms the counter;
+//   * why M <= 8: a 16x16x128 MFMA with fp4 operands runs at the fp8 rate,
+//     and only 1 / CH of its products are used, so the matrix work is
+//     (16 / WR) x the GEMM's; at WR = 4 and M = 32 (N = 7168, K = 16384,
+//     K split 4 ways) the kernel took 33 us against the skinny kernel's
+//     19.7 us (full 16-row fragments).
 //
 // Follows the MX GEMM semantics of MX8 host.cc:96-122 / MX4 host.cc:66-115:
 // y[m][n] = sum_k a[m][k] * 2^(sfa-127) * b[n][k] * 2^(sfb-127).
@@ -57,15 +67,33 @@ namespace qg {
 
 struct StreamArgs {
     TileArgs t;
-    int rows_per_wg;    // R: rows of B (output columns) per workgroup, 1 .. kStreamMaxRows
+    int rows_per_wg;      // R: rows of B (output columns) per workgroup, 1 .. stream_max_rows(wr)
+    int splitk;           // K slices (grid.z)
+    int seg_per_split;    // segments per slice (stream_seg_cap at most)
+    float* ws;            // splitk > 1: fp32 partials [splitk][batch][M][N]
+    unsigned* counters;   // splitk > 1: one per (batch, row block), zero on entry and exit
 };
 
 constexpr int kStreamWaves = 8;
-constexpr int kStreamMaxRows = 56;        // keeps a wave within kStreamGroupsPerWave row groups
-constexpr int kStreamGroupsPerWave = 8;
-constexpr int kStreamMaxK = 16384;        // K held in LDS: A rows (8 or 16 KB) and their scales
-constexpr int kStreamXsBytes = 512;       // A scale bytes per row held in LDS (K / 32)
-constexpr int kStreamWsBytes = 16384;     // the workgroup's B scales: R rows x 256 * ceil(K/8192) bytes
+constexpr int kStreamGroupsPerWave = 8;   // row groups one wave may touch
+constexpr int kStreamWsBytes = 16384;     // the workgroup's B scales: R rows x (slice groups, power of 2)
+
+// A image bytes per row of A held in LDS: 16384 K elements
+__host__ __device__ constexpr int stream_xbytes(bool fp4, int mb) {
+    return (void)mb, 16384 / (fp4 ? 2 : 1);
+}
+// segments of one K slice (a segment: 2048 / wr K elements of a row)
+__host__ __device__ constexpr int stream_seg_cap(bool fp4, int wr, int mb) {
+    return stream_xbytes(fp4, mb) / ((fp4 ? 1024 : 2048) / wr);
+}
+// log2 of the B scale image's row pitch for a slice of `groups` E8M0 groups
+__host__ __device__ constexpr int stream_ws_log2(int groups) {
+    int l = 2;
+    while ((1 << l) < groups) ++l;
+    return l;
+}
+// rows per workgroup: kStreamGroupsPerWave - 1 row groups per wave at most
+__host__ __device__ constexpr int stream_max_rows(int wr) { return wr * kStreamWaves * (kStreamGroupsPerWave - 1); }
 
 namespace strm {
 template <int N, class F, int... I>
@@ -92,27 +120,31 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
     constexpr int D = FP4 ? 8 : 4;               // pieces in flight per wave
     constexpr int FMT = FP4 ? kFmtFp4 : kFmtFp8;
     constexpr int OOB = 0x40000000;              // voffset past every descriptor's range
-    constexpr int XB = kStreamMaxK / (FP4 ? 2 : 1);                   // A image bytes per row
-    constexpr int XS_CH = (MB * kStreamXsBytes / 256) < kStreamWaves ? kStreamWaves : MB * kStreamXsBytes / 256;
+    constexpr int XB = stream_xbytes(FP4, MB);   // A image bytes per row
+    constexpr int XSB = (XB * (FP4 ? 2 : 1) / 32) < 256 ? 256 : XB * (FP4 ? 2 : 1) / 32;   // A scale bytes per row
+    constexpr int XS_CH = (MB * XSB / 256) < kStreamWaves ? kStreamWaves : MB * XSB / 256;
     constexpr int RG = kStreamGroupsPerWave;
 
     __shared__ __attribute__((aligned(1024))) uint8_t xi[MB * XB];
     __shared__ __attribute__((aligned(256))) uint8_t xs[XS_CH * 256];
     __shared__ __attribute__((aligned(256))) uint8_t wsi[kStreamWsBytes];
     __shared__ float part[kStreamWaves][RG][4 * MB];
+    __shared__ int last_flag;
 
     const TileArgs& p = sa.t;
     const int tid = threadIdx.x, L = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = L & 15, lq = L >> 4;
     const int lr = li / CH, lc = li % CH;        // the lane's operand row: (row of its group, chunk)
-    const int bz = blockIdx.y;
+    const int bz = blockIdx.y, z = blockIdx.z;
     const int r0 = blockIdx.x * sa.rows_per_wg;
     const int R = min(sa.rows_per_wg, p.n - r0);
     const int M = p.m, KB = p.kbytes, ldb = p.ldb, lds = p.sfb_sn;
-    const int nseg = (KB + SEG - 1) / SEG;
+    const int nseg_all = (KB + SEG - 1) / SEG;
+    const int s0 = z * sa.seg_per_split;                      // this slice's first segment
+    const int nseg = min(sa.seg_per_split, nseg_all - s0);    // and its segments
     const int nrg = (R + WR - 1) / WR;
     const int ngroups = FP4 ? KB / 16 : KB / 32;     // E8M0 groups (32 elements) per row
-    const int slast = (ngroups % GPS) ? nseg - 1 : nseg;   // index of a partial last segment (nseg: none)
+    const int slast = ((ngroups % GPS) ? nseg_all - 1 : nseg_all) - s0;   // local index of a partial last segment
 
     // per-lane byte offsets inside a segment and the groups they belong to
     int voff[NH], vlast[NH];
@@ -120,10 +152,14 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
     for (int h = 0; h < NH; ++h) {
         voff[h] = lr * ldb + h * H + 64 * lc + 16 * lq;
         const int g = FP4 ? 4 * lc + lq : h * (H / 32) + 2 * lc + (lq >> 1);
-        vlast[h] = GPS * (nseg - 1) + g < ngroups ? voff[h] : OOB;
+        vlast[h] = GPS * (nseg_all - 1) + g < ngroups ? voff[h] : OOB;
     }
     const int gs = FP4 ? 4 * lc + lq : (lq >> 1) * (H / 32) + 2 * lc + (lq & 1);   // the lane's scale group
-    const int wsp = 256 * ((ngroups + 255) / 256);    // B scale image: bytes per row (whole 256-byte DMAs)
+    // B scale image: the slice's groups of each row (zeros past K), row pitch
+    // the power of two >= every group a lane of the slice reads
+    const int sgroups = min(nseg * GPS, ngroups - s0 * GPS);
+    const int wsl = stream_ws_log2(nseg * GPS);
+    const int wsp = 1 << wsl;
 
     // ---- A, its scales and the workgroup's B scales into LDS, issued first --
     {
@@ -139,7 +175,8 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
             const int m = mg * WR + lr;
             const int g = FP4 ? 4 * lc + lq : h * (H / 32) + 2 * lc + (lq >> 1);
             int v = OOB;
-            if (m < M && GPS * s + g < ngroups) v = m * p.lda + s * SEG + h * H + 64 * lc + 16 * lq;
+            if (m < M && s < nseg && GPS * (s0 + s) + g < ngroups)
+                v = m * p.lda + (s0 + s) * SEG + h * H + 64 * lc + 16 * lq;
             dma16_buf(rA, (QG_LDS uint8_t*)xi + c * 1024, v, 0);
         }
         const uint8_t* SA = p.sfa + (long long)bz * p.sfa_batch;
@@ -147,20 +184,19 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
 #pragma unroll
         for (int j = 0; j < XS_CH / kStreamWaves; ++j) {
             const int c = w + kStreamWaves * j;
-            const int m = c / (kStreamXsBytes / 256), off = (c % (kStreamXsBytes / 256)) * 256 + 4 * L;
-            const int v = (m < M && off < ngroups) ? m * p.sfa_sm + off : OOB;
+            const int m = c / (XSB / 256), off = (c % (XSB / 256)) * 256 + 4 * L;
+            const int v = (m < M && off < sgroups) ? m * p.sfa_sm + s0 * GPS + off : OOB;
             dma4_buf(rS, (QG_LDS uint8_t*)xs + c * 256, v, 0);
         }
         // B scales of the workgroup's R rows (a 64-byte scale load per piece
         // would cost as many load instructions as the data)
         const uint8_t* SB = p.sfb + (long long)bz * p.sfb_batch + (long long)r0 * lds;
         const auto rW = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(SB), 0, R * lds, 0x00020000);
-        const int cpr = wsp / 256;
 #pragma unroll
         for (int j = 0; j < kStreamWsBytes / 256 / kStreamWaves; ++j) {
             const int c = w + kStreamWaves * j;
-            const int row = c / cpr, off = (c - row * cpr) * 256 + 4 * L;
-            const int v = (row < R && off < ngroups) ? row * lds + off : OOB;
+            const int b = c * 256 + 4 * L, row = b >> wsl, off = b & (wsp - 1);
+            const int v = (row < R && off < sgroups) ? row * lds + s0 * GPS + off : OOB;
             dma4_buf(rW, (QG_LDS uint8_t*)wsi + c * 256, v, 0);
         }
     }
@@ -183,7 +219,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
         const auto rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(Bw), 0, ok ? R * ldb : 0, 0x00020000);
         const bool last = ls == slast;
         const bool rows_cut = WR > 1 && (lg + 1) * WR > R;    // the workgroup's last, partial row group
-        const int soff = lg * WR * ldb + ls * SEG;
+        const int soff = lg * WR * ldb + (s0 + ls) * SEG;
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
             int v = last ? vlast[h] : voff[h];
@@ -236,7 +272,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
             const QG_LDS uint8_t* x = (const QG_LDS uint8_t*)xi + g * WR * XB + s * NH * 1024 + 16 * L;
 #pragma unroll
             for (int h = 0; h < NH; ++h) xq[g][h] = *(const QG_LDS i32x4*)(x + h * 1024);
-            xsq[g] = ((const QG_LDS uint8_t*)xs)[(g * WR + lr) * kStreamXsBytes + s * GPS + gs];
+            xsq[g] = ((const QG_LDS uint8_t*)xs)[(g * WR + lr) * XSB + s * GPS + gs];
         }
     };
     xload(cg, cs);
@@ -280,23 +316,54 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
     __syncthreads();
 
     // ---- outputs: the partials of the waves that covered each row group ---
-    if (T > 0) {
+    auto row_sum = [&](int m, int rl) __attribute__((always_inline)) {
+        const int rg = rl / WR, wr = rl - rg * WR;
+        const int wlo = (rg * nseg) / T, whi = (rg * nseg + nseg - 1) / T;
+        float s = 0.f;
+        for (int ww = wlo; ww <= whi; ++ww) {
+            const float* pp = &part[ww][rg - (ww * T) / nseg][(wr * MB + m) * NE];
+#pragma unroll
+            for (int k = 0; k < NE; ++k) s += pp[k];
+        }
+        return s;
+    };
+    auto store_c = [&](int m, int rl, float v) __attribute__((always_inline)) {
+        const long long o = (long long)bz * p.c_batch + (long long)m * p.ldc + r0 + rl;
+        if constexpr (BF16) ((uint16_t*)p.c)[o] = bf16_bits(v);
+        else ((float*)p.c)[o] = v;
+    };
+    if (sa.splitk == 1) {
         for (int idx = tid; idx < MB * R; idx += kStreamWaves * 64) {
             const int m = idx / R, rl = idx - m * R;
-            if (m >= M) continue;
-            const int rg = rl / WR, wr = rl - rg * WR;
-            const int wlo = (rg * nseg) / T, whi = (rg * nseg + nseg - 1) / T;
-            float s = 0.f;
-            for (int ww = wlo; ww <= whi; ++ww) {
-                const float* pp = &part[ww][rg - (ww * T) / nseg][(wr * MB + m) * NE];
-#pragma unroll
-                for (int k = 0; k < NE; ++k) s += pp[k];
-            }
-            const long long o = (long long)bz * p.c_batch + (long long)m * p.ldc + r0 + rl;
-            if constexpr (BF16) ((uint16_t*)p.c)[o] = bf16_bits(s);
-            else ((float*)p.c)[o] = s;
+            if (m < M) store_c(m, rl, row_sum(m, rl));
         }
+        return;
     }
+    const int N = p.n;
+    const long long plane = (long long)M * N;
+    const int nbatch = gridDim.y;
+    const auto mine = partial_rsrc(sa.ws + ((long long)z * nbatch + bz) * plane);
+    for (int idx = tid; idx < MB * R; idx += kStreamWaves * 64) {
+        const int m = idx / R, rl = idx - m * R;
+        if (m < M) store_partial1(mine, m * N + r0 + rl, row_sum(m, rl));
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    unsigned* ctr = sa.counters + (long long)bz * gridDim.x + blockIdx.x;
+    if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    (unsigned)(sa.splitk - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    for (int idx = tid; idx < MB * R; idx += kStreamWaves * 64) {
+        const int m = idx / R, rl = idx - m * R;
+        if (m >= M) continue;
+        float v = 0.f;
+        for (int zz = 0; zz < sa.splitk; ++zz)
+            v += load_partial1(partial_rsrc(sa.ws + ((long long)zz * nbatch + bz) * plane), m * N + r0 + rl);
+        store_c(m, rl, v);
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace qg

@@ -23,8 +23,8 @@ def _fp8(x, dev):
 
 
 # (m, n, k): K = 16384 is configs[4] and the largest K the kernel holds in LDS
-# (K = 32768 goes to the skinny kernel); 7168 and 2304 end in a partial
-# piece, 256 / 128 are a single partial piece
+# without a K split; 7168 and 2304 end in a partial segment, 256 / 128 are a
+# single partial segment
 MX4_STREAM = [(1, 7168, 16384), (8, 7168, 16384), (3, 1000, 7168), (5, 4100, 256), (2, 512, 32768),
               (7, 257, 2304), (4, 2048, 4096), (6, 300, 1024)]
 MX8_STREAM = [(1, 7168, 16384), (8, 2112, 7168), (6, 300, 128), (1, 4096, 2048), (2, 1536, 7168),
@@ -134,3 +134,72 @@ def test_stream_deterministic(qgemm, gpu):
     y1 = qgemm.gemm_a4w4_mxfp4(*args, dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(y0, y1)
+
+
+# K split over workgroups: A's LDS image holds 16384 K elements per row;
+# longer K (uneven last slices, partial segments)
+MX4_SPLIT = [(1, 512, 32768), (8, 2048, 32768), (5, 1000, 24576), (2, 3000, 40960), (3, 777, 17152)]
+MX8_SPLIT = [(3, 1024, 24576), (8, 2560, 32768), (1, 1536, 20480), (6, 777, 17408)]
+
+
+@pytest.mark.parametrize("m,n,k", MX4_SPLIT)
+def test_mxfp4_stream_split(qgemm, gpu, m, n, k):
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=3 * m + n + k)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.bfloat16)
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"mxfp4 stream split {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", MX8_SPLIT)
+def test_mxfp8_stream_split(qgemm, gpu, m, n, k):
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=9 * m + n + k)
+    y = qgemm.gemm_a8w8_mxfp8(_fp8(qa, gpu), _fp8(qb, gpu), to_dev(ea, None, gpu), to_dev(eb, None, gpu),
+                              dtype=torch.float32)
+    assert_close(O.gemm_mx8(qa, qb, ea, eb), out_to_f32(y), f"mxfp8 stream split {m}x{n}x{k}")
+
+
+def test_stream_split_without_workspace(qgemm, gpu):
+    """No workspace: the call runs the skinny kernel without a K split."""
+    m, n, k = 4, 2048, 32768
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=77)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.float32, workspace=False)
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), "no workspace")
+
+
+def test_stream_split_rearms_workspace(qgemm, gpu):
+    """Calls sharing one workspace, the second with a smaller problem and a
+    batch of 2: results within tolerance, the repeat bit-identical, the
+    counters back at zero."""
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device=gpu)
+    outs = []
+    for i, (m, n, k) in enumerate([(8, 4096, 32768), (5, 1024, 24576), (8, 4096, 32768)]):
+        qa, qb, ea, eb = make_mx4(m, n, k, seed=400 + m)
+        y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                                  to_dev(eb, None, gpu), dtype=torch.float32, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"call {i}")
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[2])
+    assert int(ws[:2048].to(torch.int32).sum()) == 0, "stream split counters not re-armed"
+
+    m, n, k, batch = 6, 1100, 32768, 2
+    data = [make_mx4(m, n, k, seed=500 + i) for i in range(batch)]
+    A = torch.stack([torch.from_numpy(d[0]) for d in data]).to(gpu)
+    B = torch.stack([torch.from_numpy(d[1]) for d in data]).to(gpu)
+    SA = torch.stack([torch.from_numpy(d[2]) for d in data]).to(gpu)
+    SB = torch.stack([torch.from_numpy(d[3]) for d in data]).to(gpu)
+    C = torch.empty(batch, m, n, dtype=torch.bfloat16, device=gpu)
+    kb, kg = k // 2, k // 32
+    args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, kb, kb, n, m * kb, n * kb, m * n,
+                       SA.data_ptr(), SB.data_ptr(), kg, kg, m * kg, n * kg)
+    L = qgemm.lib()
+    need = L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(args))
+    assert 0 < need <= ws.numel()
+    st = L.gemm_a4w4_mxfp4(ctypes.byref(args), qgemm.OUT_BF16, ws.data_ptr(), ws.numel(),
+                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0
+    torch.cuda.synchronize()
+    for i, d in enumerate(data):
+        assert_close(O.gemm_mx4(*d), out_to_f32(C[i]), f"batched split {i}")
+    assert int(ws[:2048].to(torch.int32).sum()) == 0
