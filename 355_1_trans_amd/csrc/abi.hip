@@ -345,7 +345,11 @@ hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, bool frag, void* w
         a.splitk = 1;
         a.kt_per_split = k_tiles;
     }
-    return qg::launch_mid(a, batch, bf16, frag, stream);
+    // at most one workgroup per CU (the K split's minimum slice bounds it):
+    // four LDS stages, three K-tiles in flight; else two workgroups per CU
+    // with two stages each
+    const long long wgs = (long long)t.tiles_m * t.tiles_n * batch * a.splitk;
+    return qg::launch_mid(a, batch, bf16, frag, wgs <= kCUs ? 4 : 2, stream);
 }
 
 // Launches the skinny or decode kernel.  A NULL workspace runs one K slice

@@ -4,15 +4,20 @@
 
 namespace qg {
 
-hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, bool frag, hipStream_t s) {
+hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, bool frag, int stages, hipStream_t s) {
     const dim3 grid(a.t.tiles_m * a.t.tiles_n, a.splitk, batch);
-    if (frag) {
-        if (bf16) mid_gemm_kernel<true, BLay::FRAG><<<grid, 256, 0, s>>>(a);
-        else mid_gemm_kernel<false, BLay::FRAG><<<grid, 256, 0, s>>>(a);
-    } else {
-        if (bf16) mid_gemm_kernel<true, BLay::KPANEL><<<grid, 256, 0, s>>>(a);
-        else mid_gemm_kernel<false, BLay::KPANEL><<<grid, 256, 0, s>>>(a);
+#define QG_MID(ST)                                                                    \
+    if (frag) {                                                                       \
+        if (bf16) mid_gemm_kernel<true, BLay::FRAG, ST><<<grid, 256, 0, s>>>(a);      \
+        else mid_gemm_kernel<false, BLay::FRAG, ST><<<grid, 256, 0, s>>>(a);          \
+    } else {                                                                          \
+        if (bf16) mid_gemm_kernel<true, BLay::KPANEL, ST><<<grid, 256, 0, s>>>(a);    \
+        else mid_gemm_kernel<false, BLay::KPANEL, ST><<<grid, 256, 0, s>>>(a);        \
     }
+    if (stages == 2) { QG_MID(2) }
+    else if (stages == 4) { QG_MID(4) }
+    else return hipErrorInvalidValue;
+#undef QG_MID
     return hipGetLastError();
 }
 

@@ -19,7 +19,8 @@ hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStrea
 
 // kernels_mid.hip: four-wave 128 x 128 tiles, fp32 block scales, split-K
 struct MidArgs;
-hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, bool frag, hipStream_t s);
+// stages: 2 (two workgroups per CU) or 4 (one, three K-tiles in flight)
+hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, bool frag, int stages, hipStream_t s);
 // skinny_*.hip: skinny-M / split-K kernel (mb = M-tile rows / 16, nb = N-tile columns / 16)
 struct SkinnyArgs;
 enum class SkinnyKind : int { MX8_RAW, MX4_RAW, BSF32_KPANEL, BSF32_FRAG };

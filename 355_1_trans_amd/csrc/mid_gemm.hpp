@@ -28,6 +28,7 @@
 //
 // LDS rows are 128 bytes, 16-byte chunks XOR-swizzled by row & 7.
 #pragma once
+#include <utility>
 #include "tile_args.hpp"
 
 namespace qg {
@@ -44,10 +45,20 @@ template <int V>
 struct I {
     static constexpr int value = V;
 };
+template <int N, class F, int... K>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, K...>) {
+    (f(I<K>{}), ...);
+}
+// f(I<k>) for k = 0 .. N-1, unrolled at compile time
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
 }  // namespace mid
 
-template <bool BF16, BLay BL>
-__global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
+template <bool BF16, BLay BL, int STAGES>
+__global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(const MidArgs mp) {
+    static_assert(STAGES == 2 || STAGES == 4, "two stages (two workgroups per CU) or four (one)");
     static_assert(BL == BLay::KPANEL || BL == BLay::FRAG, "K-panel B' or fragment-order B''");
     constexpr bool FRAG = (BL == BLay::FRAG);
     constexpr int BKB = 128, BT = 128;
@@ -58,6 +69,8 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
 
     __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES > 2 ? STAGE : 1];
+    __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 2 ? STAGE : 1];
     __shared__ int last_flag;
 
     const TileArgs& p = mp.t;
@@ -123,6 +136,12 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
 
     QG_LDS uint8_t* const pS0 = (QG_LDS uint8_t*)st0;
     QG_LDS uint8_t* const pS1 = (QG_LDS uint8_t*)st1;
+    QG_LDS uint8_t* const pS2 = (QG_LDS uint8_t*)st2;
+    QG_LDS uint8_t* const pS3 = (QG_LDS uint8_t*)st3;
+    auto stage = [&](auto SC) __attribute__((always_inline)) {
+        constexpr int S = decltype(SC)::value % STAGES;
+        return S == 0 ? pS0 : (S == 1 ? pS1 : (S == 2 ? pS2 : pS3));
+    };
 
     auto rsrc = [&](const uint8_t* base, bool valid) __attribute__((always_inline)) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
@@ -170,13 +189,15 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
         for (int e = 0; e < 4; ++e) acc[i][j][e] = __builtin_fmaf(part[x][e], fs[i], acc[i][j][e]);
     };
 
-    // K-tile t (local index) from stage ST; the 9 DMAs of K-tile t + 1 go
-    // into the other stage, one after each of the first 9 MFMAs
+    // K-tile t (local index) from stage ST; the 9 DMAs of K-tile
+    // t + STAGES - 1 go into the stage K-tile t - 1 read (freed by this
+    // barrier), one after each of the first 9 MFMAs; the barrier waits for
+    // K-tile t's DMAs only (the later K-tiles' 9 (STAGES - 2) stay in flight)
     auto ktile = [&](auto STC, int t) __attribute__((always_inline)) {
         constexpr int ST = decltype(STC)::value;
-        QG_LDS uint8_t* cur = ST ? pS1 : pS0;
-        QG_LDS uint8_t* nxt = ST ? pS0 : pS1;
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        QG_LDS uint8_t* cur = stage(mid::I<ST>{});
+        QG_LDS uint8_t* nxt = stage(mid::I<ST + STAGES - 1>{});
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(9 * (STAGES - 2)) : "memory");
         __builtin_amdgcn_sched_barrier(0);
         const QG_LDS uint8_t* sA = cur + wm * 64 * BKB;
         const QG_LDS uint8_t* sB = cur + OPB + wn * 64 * BKB;
@@ -186,7 +207,7 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
         const float sb = *(const QG_LDS float*)(cur + SB_OFF);
 #pragma unroll
         for (int i = 0; i < 4; ++i) fs[i] = *(const QG_LDS float*)(cur + SA_OFF + 4 * (wm * 64 + 16 * i + l16)) * sb;
-        const Src src = sources(t + 1);
+        const Src src = sources(t + STAGES - 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -201,18 +222,18 @@ __global__ __launch_bounds__(256, 2) void mid_gemm_kernel(const MidArgs mp) {
         rescale(3, 3, 1);
     };
 
-    // ---- prologue: K-tile 0 into stage 0 ----
-    {
-        const Src s0 = sources(0);
+    // ---- prologue: K-tiles 0 .. STAGES - 2 into their stages ----
+    mid::static_for<STAGES - 1>([&](auto SC) __attribute__((always_inline)) {
+        const Src s0 = sources(decltype(SC)::value);
 #pragma unroll
-        for (int d = 0; d < 9; ++d) dma(pS0, s0, d);
-    }
+        for (int d = 0; d < 9; ++d) dma(stage(SC), s0, d);
+    });
     int t = 0;
-    for (; t + 2 <= nk; t += 2) {
-        ktile(mid::I<0>{}, t);
-        ktile(mid::I<1>{}, t + 1);
-    }
-    if (t < nk) ktile(mid::I<0>{}, t);
+    for (; t + STAGES <= nk; t += STAGES)
+        mid::static_for<STAGES>([&](auto SC) __attribute__((always_inline)) { ktile(SC, t + decltype(SC)::value); });
+    mid::static_for<STAGES - 1>([&](auto SC) __attribute__((always_inline)) {
+        if (t + decltype(SC)::value < nk) ktile(SC, t + decltype(SC)::value);
+    });
     wait_vmcnt<0>();    // the DMAs past the slice still write zeros
 
     // ---- output: lane holds C[16i + l16][16j + 4q + 0..3] of the wave's block ----
