@@ -16,6 +16,16 @@ hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, int pane
 // panel_bytes: MX4 scale panel width, 32, 16 or 8 bytes per row
 hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s);
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+// E8M0 scales of A and B into the wide kernel's panel-major layout
+// [ngroups/pb][rows][pb] (pb = 16 or 32 bytes, ngroups % pb == 0)
+struct ScalePanelArgs {
+    const uint8_t* src[2];
+    uint8_t* dst[2];
+    int rows[2], ld[2];
+    long long src_batch[2], dst_batch[2];
+    int ngroups, pb;
+};
+hipError_t launch_mx_scale_panels(const ScalePanelArgs& a, int batch, hipStream_t s);
 
 // kernels_mid.hip: four-wave 128 x 128 tiles, fp32 block scales, split-K
 struct MidArgs;

@@ -39,10 +39,15 @@ struct TileArgs {
     int ldc;             // row pitch of C in elements
     long long a_batch, b_batch, c_batch, sfa_batch, sfb_batch;  // batch strides (bytes / elements)
     // scale addressing (in scale elements):
-    //   MX    : sfa(m, g) = sfa[m*sfa_sm + g], sfb(n, g) = sfb[n*sfb_sn + g]
+    //   MX    : sfa(m, g) = sfa[m*sfa_sm + g], sfb(n, g) = sfb[n*sfb_sn + g]; the
+    //           wide kernel also reads a panel-major copy (sfa_sk / sfb_sk below)
     //   BS8   : sfa(m, kt) = sfa[kt*sfa_sk + m], sfb(nb, kt) = sfb[nb*sfb_sn + kt]
     //   BSF32 : sfa(m, kt) = sfa[kt*sfa_sk + m*sfa_sm], sfb(nb, kt) = sfb[nb*sfb_sn + kt]
     int sfa_sm, sfa_sk, sfb_sn;
+    // MX, wide kernel: bytes from one K-tile's scales to the next (KT_BYTES =
+    // 4 (fp8) or 8 (fp4) row-major; rows * KT_BYTES in the panel-major copy
+    // [K/32/PB][rows][PB], whose row pitch sfa_sm / sfb_sn is then PB)
+    int sfb_sk;
     int tiles_m, tiles_n;
     int group_m;         // tile-rows per raster group
     int unit_scale;      // E8M0 127, passed at run time

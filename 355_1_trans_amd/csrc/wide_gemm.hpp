@@ -145,6 +145,11 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
 
     const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
     const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
+    // MX: bytes from one K-tile's scales to the next along K -- KT_BYTES in
+    // the callers' row-major [rows][K/32], rows * KT_BYTES in the panel-major
+    // copy [K/32/PB][rows][PB] (row pitch PB), whose panel DMAs read 1 KB
+    // contiguously instead of one cache line per row
+    const int SFA_KT = MX ? SFA_SK : 0, SFB_KT = MX ? p.sfb_sk : 0;
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
@@ -234,8 +239,8 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     auto dma_scales = [&](int kt, bool valid) __attribute__((always_inline)) {
         if constexpr (MX) {
             const int buf = ((kt / SPAN) & 1) * PANEL;
-            const auto ra = rsrc(SFA_t + kt * KT_BYTES, valid);
-            const auto rb = rsrc(SFB_t + kt * KT_BYTES, valid);
+            const auto ra = rsrc(SFA_t + (long long)kt * SFA_KT, valid);
+            const auto rb = rsrc(SFB_t + (long long)kt * SFB_KT, valid);
             if constexpr (PB == 32) {
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {

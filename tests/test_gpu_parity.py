@@ -1,5 +1,7 @@
 """GPU parity of every entry point against the CPU oracle (seeded inputs,
 BASELINE tolerance |y-y_ref| <= 2^-7|y_ref| + 1e-3 rms(y_ref))."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -176,3 +178,45 @@ def test_blockscale_fp32_tile(qgemm, gpu, m, n, k, dtype):
     Bk = qgemm.shuffle_b_kpanel(to_dev(qb, None, gpu)).view(torch.float8_e4m3fn)
     y = qgemm.gemm_a8w8_bpreshuffle(A, Bk, to_dev(sa, None, gpu), to_dev(sb, None, gpu), dtype=dtype)
     assert_close(ref, out_to_f32(y), f"bs-fp32 tile {m}x{n}x{k} {dtype}")
+
+
+# ------------------------------------- wide MX kernels: scale-panel copy
+@pytest.mark.parametrize("fp4", [False, True])
+def test_mx_wide_scale_panels(qgemm, gpu, fp4):
+    """Batched wide-kernel call through the C ABI with the queried workspace
+    (E8M0 scales copied panel-major first) against the oracle, and bit-equal
+    to the same call without a workspace (row-major scales read directly);
+    padded scale row pitches and batch strides."""
+    m, n, k, batch = 520, 300, 2048, 2
+    make = make_mx4 if fp4 else make_mx8
+    data = [make(m, n, k, seed=600 + i + 10 * fp4) for i in range(batch)]
+    kb, kg = (k // 2 if fp4 else k), k // 32
+    lsa, lsb = kg + 16, kg + 32
+    A = torch.stack([torch.from_numpy(d[0]) for d in data]).to(gpu)
+    B = torch.stack([torch.from_numpy(d[1]) for d in data]).to(gpu)
+    SA = torch.full((batch, m, lsa), 0xFF, dtype=torch.uint8)
+    SB = torch.full((batch, n, lsb), 0xFF, dtype=torch.uint8)
+    for i, d in enumerate(data):
+        SA[i, :, :kg] = torch.from_numpy(d[2])
+        SB[i, :, :kg] = torch.from_numpy(d[3])
+    SA, SB = SA.to(gpu), SB.to(gpu)
+    name = "gemm_a4w4_mxfp4" if fp4 else "gemm_a8w8_mxfp8"
+    L = qgemm.lib()
+    outs = []
+    for use_ws in (True, False):
+        C = torch.empty(batch, m, n, dtype=torch.float32, device=gpu)
+        args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, kb, kb, n, m * kb, n * kb,
+                           m * n, SA.data_ptr(), SB.data_ptr(), lsa, lsb, m * lsa, n * lsb)
+        need = getattr(L, name + "_workspace_bytes")(ctypes.byref(args))
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=gpu)
+        if use_ws:
+            assert need >= batch * (m + n) * kg, "query must cover the scale panels"
+        st = getattr(L, name)(ctypes.byref(args), qgemm.OUT_FP32, ws.data_ptr() if use_ws else None,
+                              need if use_ws else 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert st == 0, f"{name} returned {st}"
+        torch.cuda.synchronize()
+        outs.append(C.cpu())
+    gemm = O.gemm_mx4 if fp4 else O.gemm_mx8
+    for i, d in enumerate(data):
+        assert_close(gemm(*d), outs[0][i].numpy(), f"batch {i}")
+    assert torch.equal(outs[0], outs[1]), "panel-major and row-major scale paths differ"
