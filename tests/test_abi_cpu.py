@@ -86,8 +86,14 @@ def test_bpreshuffle_requires_kpanel_stride(qgemm):
 
 def test_workspace_queries(qgemm):
     L = qgemm.lib()
-    # large M runs the 256 x 256 tile kernel: no workspace
-    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=8192, n=8192, k=8192))) == 0
+    # large M runs the 256 x 256 tile kernel: 2 KB of counters, then both
+    # operands' E8M0 scales copied panel-major ((M + N) * K/32 bytes, each
+    # operand's share rounded up to 256) -- only when K % 512 == 0
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=8192, n=8192, k=8192))) == \
+        2048 + 2 * 8192 * 256
+    assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1000, n=8192, k=4096))) == \
+        2048 + 1000 * 128 + 8192 * 128
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=8192, n=8192, k=8320))) == 0
     # decode (M <= 64) with too few N tiles for the skinny kernel: the decode
     # kernel splits K -- 2 KB of counters + splitk * M * N fp32 partials
     for m, n, k in [(1, 1536, 7168), (32, 1536, 7168), (4, 1000, 7168), (64, 1536, 7168)]:
