@@ -29,26 +29,26 @@ hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStrea
 }
 
 // E8M0 scales [rows][ngroups] (row pitch ld) -> panel-major [ngroups/pb][rows][pb]
-// for both operands (grid.z), one 16-byte piece per thread; writes are
-// contiguous, reads one piece of a row each.
+// for both operands (grid.z), one 16-byte piece per thread: consecutive
+// threads take consecutive pieces of a row (a wave reads 1 KB of whole rows
+// contiguously) and write them into their panels (runs of 64 bytes).
 __global__ __launch_bounds__(256) void mx_scale_panels_kernel(const ScalePanelArgs a) {
     const int op = blockIdx.z, bz = blockIdx.y;
-    const int rows = a.rows[op], pieces = a.pb / 16;
-    const long long units = (long long)(a.ngroups / a.pb) * rows * pieces;
+    const int rows = a.rows[op], per_row = a.ngroups / 16, pieces = a.pb / 16;
+    const long long units = (long long)rows * per_row;
     const uint8_t* src = a.src[op] + (long long)bz * a.src_batch[op];
     uint8_t* dst = a.dst[op] + (long long)bz * a.dst_batch[op];
     for (long long u = (long long)blockIdx.x * 256 + threadIdx.x; u < units; u += (long long)gridDim.x * 256) {
-        const int h = (int)(u % pieces);
-        const long long rp = u / pieces;
-        const int r = (int)(rp % rows), pnl = (int)(rp / rows);
-        const i32x4 v = *(const i32x4*)(src + (long long)r * a.ld[op] + pnl * a.pb + 16 * h);
-        *(i32x4*)(dst + u * 16) = v;
+        const int r = (int)(u / per_row), j = (int)(u - (long long)r * per_row);
+        const int pnl = j / pieces, h = j - pnl * pieces;
+        const i32x4 v = *(const i32x4*)(src + (long long)r * a.ld[op] + 16 * j);
+        *(i32x4*)(dst + ((long long)pnl * rows + r) * a.pb + 16 * h) = v;
     }
 }
 
 hipError_t launch_mx_scale_panels(const ScalePanelArgs& a, int batch, hipStream_t s) {
     if ((a.pb != 16 && a.pb != 32) || a.ngroups % a.pb) return hipErrorInvalidValue;
-    const long long units = (long long)(a.ngroups / a.pb) * (a.rows[0] > a.rows[1] ? a.rows[0] : a.rows[1]) * (a.pb / 16);
+    const long long units = (long long)(a.rows[0] > a.rows[1] ? a.rows[0] : a.rows[1]) * (a.ngroups / 16);
     const long long blocks = (units + 255) / 256;
     const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024), batch, 2);
     mx_scale_panels_kernel<<<grid, 256, 0, s>>>(a);
