@@ -117,7 +117,11 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
     constexpr int GPS = 64 / WR;                 // E8M0 groups per row and segment
     constexpr int MG = MB / WR;                  // MFMAs per piece (groups of WR rows of A)
     constexpr int NE = 4 / WR;                   // partial sums per output and wave
-    constexpr int D = FP4 ? 8 : 4;               // pieces in flight per wave
+    // pieces in flight per wave: 4 (1 KB fp4 / 2 KB fp8 each); configs[4]
+    // M = 1 / 8 with fp4: D = 4, 5, 6, 8 -> 12.7, 12.8, 12.9, 13.4 us / 13.9,
+    // 14.3, 14.3, 15.0 us (fewer requests in flight per wave keep each row's
+    // reads closer together); fp8 M = 1: D = 3, 4, 6 -> 21.1, 20.7, 21.1 us
+    constexpr int D = 4;
     constexpr int FMT = FP4 ? kFmtFp4 : kFmtFp8;
     constexpr int OOB = 0x40000000;              // voffset past every descriptor's range
     constexpr int XB = stream_xbytes(FP4, MB);   // A image bytes per row
