@@ -186,7 +186,8 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
             else dma4_buf(rA, st + a_dma_lds[u], a_dma_off[u], kt * BKB);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) dma16_buf(rB, st + A_BYTES + w * 2048 + h * 1024, b_off[h], kt * b_kstep);
+        // (nontemporal: M <= 64 is one M tile, each B byte is read once)
+        for (int h = 0; h < 2; ++h) dma16_buf_nt(rB, st + A_BYTES + w * 2048 + h * 1024, b_off[h], kt * b_kstep);
         const auto rSA = rsrc(SFA, valid), rSB = rsrc(SFB, valid);
         if constexpr (MX) {
 #pragma unroll

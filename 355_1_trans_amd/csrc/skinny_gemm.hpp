@@ -106,7 +106,9 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int FMT, ScaleKind SK, BLay BL, int MB, int NB, bool BF16, bool SCP = false>
+// NTB: B moves with the nontemporal cache policy (one M tile: each B byte
+// is read once; with several M tiles the other tiles re-read it from cache)
+template <int FMT, ScaleKind SK, BLay BL, int MB, int NB, bool BF16, bool SCP, bool NTB>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const SkinnyArgs sp) {
     constexpr int BKB = 128, W = kSkinnyWaves;
     static_assert(MB == 1 || MB == 2 || MB == 4, "16, 32 or 64 rows per M-tile");
@@ -239,6 +241,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     auto ld16 = [](__amdgpu_buffer_rsrc_t r, int voff, int soff) -> i32x4 {
         return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
     };
+    auto ld16b = [](__amdgpu_buffer_rsrc_t r, int voff, int soff) -> i32x4 {
+        return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NTB ? 2 : 0));
+    };
     auto cat8 = [](i32x4 lo, i32x4 hi) { return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}; };
 
     struct Stage {
@@ -258,11 +263,12 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
             for (int j = 0; j < NB; ++j)
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
-                    dma16_buf(rB, dst + j * 2048 + h * 1024, boff[j][h], kt * b_kstep);
+                    if constexpr (NTB) dma16_buf_nt(rB, dst + j * 2048 + h * 1024, boff[j][h], kt * b_kstep);
+                    else dma16_buf(rB, dst + j * 2048 + h * 1024, boff[j][h], kt * b_kstep);
         } else {
 #pragma unroll
             for (int j = 0; j < NB; ++j)
-                s.b[j] = cat8(ld16(rB, boff[j][0], kt * b_kstep), ld16(rB, boff[j][1], kt * b_kstep));
+                s.b[j] = cat8(ld16b(rB, boff[j][0], kt * b_kstep), ld16b(rB, boff[j][1], kt * b_kstep));
         }
 #pragma unroll
         for (int i = 0; i < MB; ++i) s.a[i] = cat8(ld16(rA, aoff[i][0], kt * BKB), ld16(rA, aoff[i][1], kt * BKB));
@@ -530,23 +536,27 @@ template <int FMT, ScaleKind SK, BLay BL>
 hipError_t launch_skinny_family(const SkinnyArgs& a, int mb, int nb, int batch, bool bf16, hipStream_t s) {
     const dim3 grid(skinny_grid_x(a.n_tiles, a.m_tiles), a.splitk, batch);
     const dim3 block(kSkinnyWaves * 64);
-#define QG_SKINNY_CASE(MBV, NBV)                                                                  \
-    if (mb == MBV && nb == NBV) {                                                                 \
-        if constexpr (skinny_scp_fits(MBV, NBV, SK == ScaleKind::MX)) {                           \
-            if (a.scale_panel) {                                                                  \
-                if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true, true><<<grid, block, 0, s>>>(a); \
-                else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false, true><<<grid, block, 0, s>>>(a);     \
-                return hipGetLastError();                                                         \
-            }                                                                                     \
-        }                                                                                         \
-        if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true><<<grid, block, 0, s>>>(a);      \
-        else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false><<<grid, block, 0, s>>>(a);          \
-        return hipGetLastError();                                                                 \
+#define QG_SKINNY_LAUNCH(MBV, NBV, SCPV, NTV)                                                        \
+    if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true, SCPV, NTV><<<grid, block, 0, s>>>(a);  \
+    else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false, SCPV, NTV><<<grid, block, 0, s>>>(a);      \
+    return hipGetLastError();
+// mb < 4 always means one M tile (the plan takes mb = 4 beyond 32 rows)
+#define QG_SKINNY_NT(MBV, NBV, SCPV)                                                                 \
+    if (MBV < 4 || a.m_tiles == 1) { QG_SKINNY_LAUNCH(MBV, NBV, SCPV, true) }                        \
+    else { QG_SKINNY_LAUNCH(MBV, NBV, SCPV, (MBV < 4)) }
+#define QG_SKINNY_CASE(MBV, NBV)                                                                     \
+    if (mb == MBV && nb == NBV) {                                                                    \
+        if constexpr (skinny_scp_fits(MBV, NBV, SK == ScaleKind::MX)) {                              \
+            if (a.scale_panel) { QG_SKINNY_NT(MBV, NBV, true) }                                      \
+        }                                                                                            \
+        QG_SKINNY_NT(MBV, NBV, false)                                                                \
     }
     QG_SKINNY_CASE(1, 1) QG_SKINNY_CASE(1, 2) QG_SKINNY_CASE(1, 4)
     QG_SKINNY_CASE(2, 1) QG_SKINNY_CASE(2, 2) QG_SKINNY_CASE(2, 4)
     QG_SKINNY_CASE(4, 1) QG_SKINNY_CASE(4, 2) QG_SKINNY_CASE(4, 4)
 #undef QG_SKINNY_CASE
+#undef QG_SKINNY_NT
+#undef QG_SKINNY_LAUNCH
     return hipErrorInvalidValue;
 }
 
