@@ -181,13 +181,14 @@ def test_blockscale_fp32_tile(qgemm, gpu, m, n, k, dtype):
 
 
 # ------------------------------------- wide MX kernels: scale-panel copy
-@pytest.mark.parametrize("fp4", [False, True])
-def test_mx_wide_scale_panels(qgemm, gpu, fp4):
+@pytest.mark.parametrize("fp4,k", [(False, 2048), (True, 2048), (True, 1536), (False, 1536)])
+def test_mx_wide_scale_panels(qgemm, gpu, fp4, k):
     """Batched wide-kernel call through the C ABI with the queried workspace
-    (E8M0 scales copied panel-major first) against the oracle, and bit-equal
-    to the same call without a workspace (row-major scales read directly);
-    padded scale row pitches and batch strides."""
-    m, n, k, batch = 520, 300, 2048, 2
+    (E8M0 scales copied panel-major first: 32-byte panels for fp4 with
+    K % 1024 == 0, else 16-byte) against the oracle, and bit-equal to the
+    same call without a workspace (row-major scales read directly); padded
+    scale row pitches and batch strides, M and N tails."""
+    m, n, batch = 520, 300, 2
     make = make_mx4 if fp4 else make_mx8
     data = [make(m, n, k, seed=600 + i + 10 * fp4) for i in range(batch)]
     kb, kg = (k // 2 if fp4 else k), k // 32

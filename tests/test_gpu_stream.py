@@ -203,3 +203,18 @@ def test_stream_split_rearms_workspace(qgemm, gpu):
     for i, d in enumerate(data):
         assert_close(O.gemm_mx4(*d), out_to_f32(C[i]), f"batched split {i}")
     assert int(ws[:2048].to(torch.int32).sum()) == 0
+
+
+@pytest.mark.parametrize("m,n", [(8, 256), (8, 255), (9, 256), (1, 255)])
+def test_stream_routing_boundaries(qgemm, gpu, m, n):
+    """Both sides of the stream kernel's limits (M <= 8, N >= 256) give the
+    oracle's result."""
+    k = 4096
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=m * 1000 + n)
+    y = qgemm.gemm_a4w4_mxfp4(to_dev(qa, None, gpu), to_dev(qb, None, gpu), to_dev(ea, None, gpu),
+                              to_dev(eb, None, gpu), dtype=torch.float32)
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"mxfp4 {m}x{n}x{k}")
+    qa, qb, ea, eb = make_mx8(m, n, k, seed=m * 1000 + n + 1)
+    y = qgemm.gemm_a8w8_mxfp8(_fp8(qa, gpu), _fp8(qb, gpu), to_dev(ea, None, gpu), to_dev(eb, None, gpu),
+                              dtype=torch.float32)
+    assert_close(O.gemm_mx8(qa, qb, ea, eb), out_to_f32(y), f"mxfp8 {m}x{n}x{k}")
