@@ -189,7 +189,15 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
 // decode shapes whose N is too narrow for the skinny kernel without a K
 // split; with enough N tiles the skinny kernel (waves split K) streams
 // row-major B with better DRAM page locality and needs no split.
-Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny, bool decode_ok = true) {
+// decode_wide: the B layout streams well through the decode kernel's LDS
+// stages (the K-panel B', 16-row K-tiles of 2 KB), which then also takes
+// M >= 16 with up to 2 * kSplitBelow skinny tiles and >= 32 K-tiles: A is
+// shared by the workgroup's waves instead of re-read by every 16-column
+// skinny tile (BS fp32 M = 64: N = 2112, K = 7168 17.8 -> 14.8 us; N = 7168,
+// K = 16384 39.7 -> 33.0 us; M = 1 or short K stay faster on the skinny
+// kernel, and row-major B (MXFP8) on the skinny kernel at any M)
+Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny, bool decode_ok = true,
+               bool decode_wide = false) {
     Plan p;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
     p.skinny = force_skinny || (m <= 256 && tiles256 < 128);
@@ -203,7 +211,8 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
         if ((long long)p.n_tiles * p.m_tiles * batch >= kMinTiles) break;
     }
     const long long base = (long long)p.n_tiles * p.m_tiles * batch;
-    if (decode_ok && m <= 64 && base < kSplitBelow) {
+    if (decode_ok && m <= 64 &&
+        (base < kSplitBelow || (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32))) {
         plan_decode(p, m, n, k_tiles, batch, b_bytes);
         return p;
     }
@@ -232,7 +241,7 @@ constexpr int kMidTarget = 2 * kCUs;
 constexpr int kMidMinKt = 16;    // 8 measured slower where the split tail dominates (M = 256, N = 4096, K = 7168: 34.4 vs 27.0 us)
 
 Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
-    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, false, decode_ok);
+    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, false, decode_ok, decode_ok);
     if (m <= kMidMinM) return p;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
     if (tiles256 >= kMidBelow) return p;
