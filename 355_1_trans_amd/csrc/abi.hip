@@ -195,7 +195,10 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
 // shared by the workgroup's waves instead of re-read by every 16-column
 // skinny tile (BS fp32 M = 64: N = 2112, K = 7168 17.8 -> 14.8 us; N = 7168,
 // K = 16384 39.7 -> 33.0 us; M = 1 or short K stay faster on the skinny
-// kernel, and row-major B (MXFP8) on the skinny kernel at any M)
+// kernel, and row-major B (MXFP8) on the skinny kernel at any M); and short
+// K (<= 16 K-tiles) with many skinny tiles, whose 8 waves would share too
+// few K-tiles (N = 24576, K = 1536: M = 1, 16, 64 11.9, 13.0, 22.6 -> 10.7,
+// 11.2, 17.3 us; with 224 tiles, N = 7168, K = 2048, the skinny kernel wins)
 Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny, bool decode_ok = true,
                bool decode_wide = false) {
     Plan p;
@@ -212,7 +215,8 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
     }
     const long long base = (long long)p.n_tiles * p.m_tiles * batch;
     if (decode_ok && m <= 64 &&
-        (base < kSplitBelow || (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32))) {
+        (base < kSplitBelow || (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32) ||
+         (decode_wide && k_tiles <= 16 && base >= 2 * kSplitBelow))) {
         plan_decode(p, m, n, k_tiles, batch, b_bytes);
         return p;
     }
