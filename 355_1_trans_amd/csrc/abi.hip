@@ -195,12 +195,17 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
 // shared by the workgroup's waves instead of re-read by every 16-column
 // skinny tile (BS fp32 M = 64: N = 2112, K = 7168 17.8 -> 14.8 us; N = 7168,
 // K = 16384 39.7 -> 33.0 us; M = 1 or short K stay faster on the skinny
-// kernel, and row-major B (MXFP8) on the skinny kernel at any M); and short
-// K (<= 16 K-tiles) with many skinny tiles, whose 8 waves would share too
-// few K-tiles (N = 24576, K = 1536: M = 1, 16, 64 11.9, 13.0, 22.6 -> 10.7,
-// 11.2, 17.3 us; with 224 tiles, N = 7168, K = 2048, the skinny kernel wins)
+// kernel, and row-major B (MXFP8) on the skinny kernel at any M).  Short K
+// (<= 16 K-tiles) with many skinny tiles goes to the decode kernel for
+// either layout: the skinny kernel's 8 waves would share too few K-tiles
+// (N = 24576, K = 1536, BS fp32 M = 1, 16, 64: 11.9, 13.0, 22.6 -> 10.7,
+// 11.2, 17.3 us; MXFP8 M = 16, 64: 15.0, 23.9 -> 11.9, 19.6 us; with 224
+// tiles, N = 7168, K = 2048, the skinny kernel wins)
+// decode_short: the short-K rule alone (MXFP4, which the decode kernel
+// otherwise streams slower than the skinny kernel; M = 16, 32 with 12-16
+// K-tiles: 16.7, 13.6 -> 14.0, 12.6 us, M = 64 alike)
 Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny, bool decode_ok = true,
-               bool decode_wide = false) {
+               bool decode_wide = false, bool decode_short = false) {
     Plan p;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
     p.skinny = force_skinny || (m <= 256 && tiles256 < 128);
@@ -214,9 +219,10 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
         if ((long long)p.n_tiles * p.m_tiles * batch >= kMinTiles) break;
     }
     const long long base = (long long)p.n_tiles * p.m_tiles * batch;
-    if (decode_ok && m <= 64 &&
-        (base < kSplitBelow || (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32) ||
-         (decode_wide && k_tiles <= 16 && base >= 2 * kSplitBelow))) {
+    const bool short_k = k_tiles <= 16 && base >= 2 * kSplitBelow;
+    if (m <= 64 && ((decode_ok && (base < kSplitBelow || short_k ||
+                                   (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32))) ||
+                    (decode_short && short_k))) {
         plan_decode(p, m, n, k_tiles, batch, b_bytes);
         return p;
     }
@@ -623,7 +629,7 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false);
+    const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false, false, true);
     if (stream_ok(a, true)) {
         if (run_stream(t, a.k, a.batch, true, bf16, workspace, workspace_bytes, stream, &st)) return st;
         // the K split's workspace is missing: the skinny kernel, without a split
@@ -640,8 +646,8 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
     const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, true);
-    const Plan pl =
-        plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false, false);
+    const Plan pl = plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false,
+                              false, false, true);
     return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny ? 0 : scale_panel_bytes(*args)});
 }
 

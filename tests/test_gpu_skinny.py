@@ -24,7 +24,8 @@ def _fp8(x, dev):
 # the rest the skinny kernel
 MX8_DECODE = [(1, 2112, 7168), (8, 1024, 2048), (16, 7168, 512), (17, 1000, 1024), (33, 4096, 1024),
               (64, 2112, 7168), (128, 1536, 2048), (256, 512, 1024),
-              (1, 1536, 7168), (40, 1200, 4096), (64, 1536, 7168), (5, 300, 26624)]
+              (1, 1536, 7168), (40, 1200, 4096), (64, 1536, 7168), (5, 300, 26624),
+              (16, 24576, 1536), (40, 32768, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", MX8_DECODE)
@@ -71,8 +72,9 @@ def test_splitk_rearms_workspace(qgemm, gpu):
 
 
 # ----------------------------------------------------------------- MXFP4
+# (16, 24576, 3072), (40, 16384, 2048): short K with >= 256 skinny tiles -> decode kernel
 MX4_DECODE = [(1, 2112, 7168), (4, 1000, 2048), (16, 4096, 512), (31, 512, 4096), (64, 7168, 1024),
-              (200, 768, 1536), (8, 7168, 16384), (32, 2048, 16384)]
+              (200, 768, 1536), (8, 7168, 16384), (32, 2048, 16384), (16, 24576, 3072), (40, 16384, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", MX4_DECODE)
