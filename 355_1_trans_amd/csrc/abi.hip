@@ -250,26 +250,40 @@ constexpr int kMidBelow = 128;
 constexpr int kMidTarget = 2 * kCUs;
 constexpr int kMidMinKt = 16;    // 8 measured slower where the split tail dominates (M = 256, N = 4096, K = 7168: 34.4 vs 27.0 us)
 
-Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
-    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, false, decode_ok, decode_ok);
-    if (m <= kMidMinM) return p;
+// Replaces p with a 128 x 128 plan when M > kMidMinM and the 256 x 256
+// kernel would have fewer than kMidBelow tiles.
+void plan_mid(Plan& p, int m, int n, int k_tiles, int batch) {
+    if (m <= kMidMinM) return;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
-    if (tiles256 >= kMidBelow) return p;
+    if (tiles256 >= kMidBelow) return;
     p = Plan{};
     p.mid = true;
     p.kt_per_split = k_tiles;
     const long long tiles = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
     if (tiles >= kMidTarget / 2 || tiles > kCounterBytes / (long long)sizeof(unsigned) ||
         (long long)m * n >= (1LL << 29))    // partial offsets are 32-bit bytes
-        return p;
+        return;
     const long long split = std::min<long long>(kMidTarget / tiles, k_tiles / kMidMinKt);
-    if (split <= 1) return p;
+    if (split <= 1) return;
     p.kt_per_split = ceil_div(k_tiles, (int)split);
     p.splitk = ceil_div(k_tiles, p.kt_per_split);
     if (p.splitk > 1) {
         p.ctr_bytes = kCounterBytes;
         p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
     }
+}
+
+Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
+    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, false, decode_ok, decode_ok);
+    plan_mid(p, m, n, k_tiles, batch);
+    return p;
+}
+
+// MX: the same 128 x 128 rule (row-major B, E8M0 scales applied by the MFMA)
+Plan plan_mx(int m, int n, int k_tiles, int batch, long long b_bytes, bool fp4) {
+    Plan p = fp4 ? plan_gemm(m, n, k_tiles, batch, b_bytes, false, false, false, true)
+                 : plan_gemm(m, n, k_tiles, batch, b_bytes, false);
+    plan_mid(p, m, n, k_tiles, batch);
     return p;
 }
 
@@ -400,10 +414,9 @@ hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int
                : qg::launch_wide_mx8_raw(t, a.batch, bf16, pb, stream);
 }
 
-// Launches the 128 x 128 fp32-block-scale kernel; a NULL workspace runs it
-// without a K split.
-hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, bool frag, void* ws, size_t ws_bytes, int k_tiles,
-                   hipStream_t stream) {
+// Launches the 128 x 128 kernel; a NULL workspace runs it without a K split.
+hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, qg::MidKind kind, void* ws, size_t ws_bytes,
+                   int k_tiles, hipStream_t stream) {
     qg::MidArgs a{};
     t.tiles_m = ceil_div(t.m, 128);
     t.tiles_n = ceil_div(t.n, 128);
@@ -422,7 +435,7 @@ hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, bool frag, void* w
     // four LDS stages, three K-tiles in flight; else two workgroups per CU
     // with two stages each
     const long long wgs = (long long)t.tiles_m * t.tiles_n * batch * a.splitk;
-    return qg::launch_mid(a, batch, bf16, frag, wgs <= kCUs ? 4 : 2, stream);
+    return qg::launch_mid(a, batch, bf16, kind, wgs <= kCUs ? 4 : 2, stream);
 }
 
 // Launches the skinny or decode kernel.  A NULL workspace runs one K slice
@@ -596,7 +609,7 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
+    const Plan pl = plan_mx(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
     if (stream_ok(a, false)) {
         if (run_stream(t, a.k, a.batch, false, bf16, workspace, workspace_bytes, stream, &st)) return st;
         // the K split's workspace is missing: the skinny kernel, without a split
@@ -604,6 +617,10 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
     }
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
+    if (pl.mid) {
+        t.sfa_sk = t.sfb_sk = 4;
+        return run_mid(t, a.batch, pl, bf16, qg::MidKind::MX8, workspace, workspace_bytes, a.k / 128, stream);
+    }
     // (32-byte panels would cover 8 K-tiles; the loop then unrolls by 8, and
     // measured 1% slower than 16-byte panels for fp8)
     return run_wide_mx(t, a, false, mx_wide_panels(a) ? 16 : 4, bf16, workspace, workspace_bytes, stream);
@@ -612,8 +629,8 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
     const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, false);
-    const Plan pl = plan_gemm(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false);
-    return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny ? 0 : scale_panel_bytes(*args)});
+    const Plan pl = plan_mx(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false);
+    return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny || pl.mid ? 0 : scale_panel_bytes(*args)});
 }
 
 // ---------------------------------------------------------------- MXFP4
@@ -629,7 +646,7 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_gemm(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, false, false, false, true);
+    const Plan pl = plan_mx(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, true);
     if (stream_ok(a, true)) {
         if (run_stream(t, a.k, a.batch, true, bf16, workspace, workspace_bytes, stream, &st)) return st;
         // the K split's workspace is missing: the skinny kernel, without a split
@@ -637,6 +654,10 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
     }
     if (pl.skinny)
         return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);
+    if (pl.mid) {
+        t.sfa_sk = t.sfb_sk = 8;
+        return run_mid(t, a.batch, pl, bf16, qg::MidKind::MX4, workspace, workspace_bytes, a.k / 256, stream);
+    }
     // 32-byte panels (4 K-tiles, two DMA lanes per scale row) need whole
     // panels: K % 1024 == 0
     const int pb = mx_wide_panels(a) ? (a.k % 1024 == 0 ? 32 : 16) : 8;
@@ -646,9 +667,8 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
     const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, true);
-    const Plan pl = plan_gemm(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, false,
-                              false, false, true);
-    return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny ? 0 : scale_panel_bytes(*args)});
+    const Plan pl = plan_mx(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, true);
+    return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny || pl.mid ? 0 : scale_panel_bytes(*args)});
 }
 
 // ------------------------------------------------ block-scale FP8, E8M0 scales
@@ -708,7 +728,8 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
     const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bk, true);
-    if (pl.mid) return run_mid(t, a.batch, pl, bf16, false, workspace, workspace_bytes, a.k / 128, stream);
+    if (pl.mid)
+        return run_mid(t, a.batch, pl, bf16, qg::MidKind::BS_KPANEL, workspace, workspace_bytes, a.k / 128, stream);
     if (pl.skinny)
         return run_skinny(SkinnyKind::BSF32_KPANEL, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128,
                           stream);
@@ -747,7 +768,8 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
     // M: the eight-wave tile kernel stages B'' blocks through LDS like B'
     const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bpp, false);
     if (pl.mid)
-        return run_mid(t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, true, workspace, workspace_bytes, a.k / 128, stream);
+        return run_mid(t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, qg::MidKind::BS_FRAG, workspace,
+                       workspace_bytes, a.k / 128, stream);
     if (!pl.skinny) return qg::launch_bsf32(t, a.batch, out_dtype == QGEMM_OUT_BF16, true, stream);
     return run_skinny(SkinnyKind::BSF32_FRAG, t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, workspace,
                       workspace_bytes, a.k / 128, stream);

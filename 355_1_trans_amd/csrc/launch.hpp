@@ -27,10 +27,12 @@ struct ScalePanelArgs {
 };
 hipError_t launch_mx_scale_panels(const ScalePanelArgs& a, int batch, hipStream_t s);
 
-// kernels_mid.hip: four-wave 128 x 128 tiles, fp32 block scales, split-K
+// kernels_mid.hip: four-wave 128 x 128 tiles, split-K; fp32 block scales
+// with B' or B'', or MXFP8 / MXFP4 with row-major B
 struct MidArgs;
+enum class MidKind : int { BS_KPANEL, BS_FRAG, MX8, MX4 };
 // stages: 2 (two workgroups per CU) or 4 (one, three K-tiles in flight)
-hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, bool frag, int stages, hipStream_t s);
+hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, MidKind kind, int stages, hipStream_t s);
 // skinny_*.hip: skinny-M / split-K kernel (mb = M-tile rows / 16, nb = N-tile columns / 16)
 struct SkinnyArgs;
 enum class SkinnyKind : int { MX8_RAW, MX4_RAW, BSF32_KPANEL, BSF32_FRAG };

@@ -56,16 +56,25 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 }  // namespace mid
 
-template <bool BF16, BLay BL, int STAGES>
+// SK = BSF32: fp8, fp32 block scales, B' or B''; SK = MX: fp8 or fp4 (FMT),
+// E8M0 scales per 32 K, row-major B, the scales applied by the MFMA
+template <bool BF16, BLay BL, int STAGES, ScaleKind SK = ScaleKind::BSF32, int FMT = kFmtFp8>
 __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(const MidArgs mp) {
     static_assert(STAGES == 2 || STAGES == 4, "two stages (two workgroups per CU) or four (one)");
-    static_assert(BL == BLay::KPANEL || BL == BLay::FRAG, "K-panel B' or fragment-order B''");
+    constexpr bool MX = (SK == ScaleKind::MX);
+    constexpr bool FP4 = (FMT == kFmtFp4);
+    static_assert(MX ? BL == BLay::RAW : (BL == BLay::KPANEL || BL == BLay::FRAG && !FP4),
+                  "MX: row-major B; fp32 block scales: fp8 with K-panel B' or fragment-order B''");
     constexpr bool FRAG = (BL == BLay::FRAG);
+    constexpr bool RAW = (BL == BLay::RAW);
     constexpr int BKB = 128, BT = 128;
     constexpr int OPB = BT * BKB;              // 16 KB per operand and K-tile
-    constexpr int SA_OFF = 2 * OPB;            // 128 fp32 row scales
-    constexpr int SB_OFF = SA_OFF + 512;       // 2 slots of 256 B (waves 2, 3)
-    constexpr int STAGE = SB_OFF + 512;
+    constexpr int KTB = MX ? (FP4 ? 8 : 4) : 4;   // scale bytes per row and K-tile (MX)
+    constexpr int SA_OFF = 2 * OPB;            // BSF32: 128 fp32 row scales; MX: [128][KTB] of A
+    constexpr int SB_OFF = SA_OFF + (MX ? 128 * KTB : 512);   // BSF32: 2 slots of 256 B; MX: [128][KTB] of B
+    constexpr int STAGE = SB_OFF + (MX ? 128 * KTB : 512);
+    constexpr int SCD = MX && FP4 ? 2 : 1;     // scale DMAs per wave and K-tile
+    constexpr int NDMA = 8 + SCD;              // DMAs per wave and K-tile
 
     __shared__ __attribute__((aligned(1024))) uint8_t st0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
@@ -101,12 +110,14 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
     const int q = L >> 4, l16 = L & 15;
 
     const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA + (long long)kt0 * BKB;
+    const int LDB = p.ldb;
     const uint8_t* B = p.b + bz * p.b_batch +
-                       (FRAG ? (long long)(n0 >> 4) * NKT * 2048 + (long long)kt0 * 2048
-                             : (long long)kt0 * N * BKB + (long long)n0 * BKB);
-    const long long b_kstep = FRAG ? 2048 : (long long)N * BKB;
-    const uint8_t* SFA = p.sfa + 4ll * bz * p.sfa_batch;
-    const uint8_t* SFB = p.sfb + 4ll * bz * p.sfb_batch;
+                       (RAW ? (long long)n0 * LDB + (long long)kt0 * BKB
+                            : FRAG ? (long long)(n0 >> 4) * NKT * 2048 + (long long)kt0 * 2048
+                                   : (long long)kt0 * N * BKB + (long long)n0 * BKB);
+    const long long b_kstep = RAW ? BKB : FRAG ? 2048 : (long long)N * BKB;
+    const uint8_t* SFA = p.sfa + (MX ? 1ll : 4ll) * bz * p.sfa_batch;
+    const uint8_t* SFB = p.sfb + (MX ? 1ll : 4ll) * bz * p.sfb_batch;
 
     // ---- DMA offsets: wave w moves 8-row groups 4w .. 4w+3 of A and of B'
     // (lane L: row +L/8, physical chunk L%8 = logical (L%8) ^ (row & 7)),
@@ -117,7 +128,9 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
         const int r = (4 * w + u) * 8 + (L >> 3);
         const int c = (L & 7) ^ (r & 7);
         aoff[u] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
-        if constexpr (FRAG) {
+        if constexpr (RAW) {
+            boff[u] = (min(n0 + r, N - 1) - n0) * LDB + c * 16;
+        } else if constexpr (FRAG) {
             const int blk = 2 * w + (u >> 1);
             const int nb = min((n0 >> 4) + blk, ((N + 15) >> 4) - 1) - (n0 >> 4);
             boff[u] = nb * NKT * 2048 + (u & 1) * 1024 + L * 16;
@@ -125,14 +138,35 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
             boff[u] = (min(n0 + r, N - 1) - n0) * BKB + c * 16;
         }
     }
-    // scales: waves 0, 1 move the fp32 row scales of rows [64w, 64w + 64);
-    // waves 2, 3 the tile's weight scale (its 128 columns are one scale block)
+    // scales: BSF32 -- waves 0, 1 move the fp32 row scales of rows [64w,
+    // 64w + 64); waves 2, 3 the tile's weight scale (its 128 columns are one
+    // scale block).  MX -- waves 0, 1 the K-tile's E8M0 bytes of A rows
+    // [64w, 64w + 64), waves 2, 3 those of B rows [64(w-2), +64): KTB bytes
+    // per row, one dword per lane (fp4: two DMAs of 32 rows)
     const bool sc_is_a = w < 2;
-    const uint8_t* sc_base = sc_is_a ? SFA + 4ll * m0 * SFA_SM + 4ll * kt0 * SFA_SK
-                                     : SFB + 4ll * min(n0 >> 7, (N - 1) >> 7) * SFB_SN + 4ll * kt0;
-    const int sc_voff = sc_is_a ? 4 * (min(m0 + 64 * w + L, M - 1) - m0) * SFA_SM : 0;
-    const long long sc_kstep = sc_is_a ? 4ll * SFA_SK : 4ll;
-    const int sc_dst = sc_is_a ? SA_OFF + 256 * w : SB_OFF + 256 * (w - 2);
+    const uint8_t* sc_base;
+    int sc_voff[SCD], sc_dst[SCD];
+    long long sc_kstep;
+    if constexpr (MX) {
+        const int r64 = 64 * (w & 1);
+        sc_base = sc_is_a ? SFA + (long long)m0 * SFA_SM + (long long)kt0 * SFA_SK
+                          : SFB + (long long)n0 * SFB_SN + (long long)kt0 * p.sfb_sk;
+        sc_kstep = sc_is_a ? SFA_SK : p.sfb_sk;
+#pragma unroll
+        for (int s2 = 0; s2 < SCD; ++s2) {
+            const int row = FP4 ? r64 + 32 * s2 + (L >> 1) : r64 + L;
+            const int sm = sc_is_a ? SFA_SM : SFB_SN;
+            const int lim = sc_is_a ? M - 1 - m0 : N - 1 - n0;
+            sc_voff[s2] = min(row, lim) * sm + (FP4 ? (L & 1) * 4 : 0);
+            sc_dst[s2] = (sc_is_a ? SA_OFF : SB_OFF) + (FP4 ? (r64 + 32 * s2) * 8 : r64 * 4);
+        }
+    } else {
+        sc_base = sc_is_a ? SFA + 4ll * m0 * SFA_SM + 4ll * kt0 * SFA_SK
+                          : SFB + 4ll * min(n0 >> 7, (N - 1) >> 7) * SFB_SN + 4ll * kt0;
+        sc_voff[0] = sc_is_a ? 4 * (min(m0 + 64 * w + L, M - 1) - m0) * SFA_SM : 0;
+        sc_kstep = sc_is_a ? 4ll * SFA_SK : 4ll;
+        sc_dst[0] = sc_is_a ? SA_OFF + 256 * w : SB_OFF + 256 * (w - 2);
+    }
 
     QG_LDS uint8_t* const pS0 = (QG_LDS uint8_t*)st0;
     QG_LDS uint8_t* const pS1 = (QG_LDS uint8_t*)st1;
@@ -158,11 +192,12 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
         s.sc = rsrc(sc_base + kt * sc_kstep, v);
         return s;
     };
-    // DMA d (0..8) of a K-tile into stage st: 0-3 A, 4-7 B, 8 scales
+    // DMA d (0 .. NDMA-1) of a K-tile into stage st: 0-3 A, 4-7 B, then scales
     auto dma = [&](QG_LDS uint8_t* st, const Src& s, int d) __attribute__((always_inline)) {
         if (d < 4) dma16_buf(s.a, st + (4 * w + d) * 1024, aoff[d], 0);
         else if (d < 8) dma16_buf(s.b, st + OPB + (4 * w + d - 4) * 1024, boff[d - 4], 0);
-        else dma4_buf(s.sc, st + sc_dst, sc_voff, 0);
+        else if (d == 8) dma4_buf(s.sc, st + sc_dst[0], sc_voff[0], 0);
+        else dma4_buf(s.sc, st + sc_dst[SCD - 1], sc_voff[SCD - 1], 0);
     };
 
     f32x4 acc[4][4];
@@ -173,8 +208,12 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
     i32x8 af[4], bf[2];
     f32x4 part[2];
     float fs[4];
-    const int rd8 = l16 * BKB + ((q ^ (l16 & 7)) << 4);
-    const int rdb0 = FRAG ? L * 16 : rd8, rdb1 = FRAG ? 1024 + L * 16 : rd8 ^ 64;
+    // fragment chunks of row l16: fp8 q and q + 4; fp4 2q and 2q + 1 (the
+    // two MFMAs of a 256-element K-tile, scale bytes 2q and 2q + 1)
+    const int ca = FP4 ? 2 * q : q, cb = FP4 ? 2 * q + 1 : q + 4;
+    const int rd8 = l16 * BKB + ((ca ^ (l16 & 7)) << 4);
+    const int rd8b = l16 * BKB + ((cb ^ (l16 & 7)) << 4);
+    const int rdb0 = FRAG ? L * 16 : rd8, rdb1 = FRAG ? 1024 + L * 16 : rd8b;
     auto frag = [&](const QG_LDS uint8_t* blk, int o0, int o1) __attribute__((always_inline)) -> i32x8 {
         const i32x4 lo = *(const QG_LDS i32x4*)(blk + o0);
         const i32x4 hi = *(const QG_LDS i32x4*)(blk + o1);
@@ -197,36 +236,73 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
         constexpr int ST = decltype(STC)::value;
         QG_LDS uint8_t* cur = stage(mid::I<ST>{});
         QG_LDS uint8_t* nxt = stage(mid::I<ST + STAGES - 1>{});
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(9 * (STAGES - 2)) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(NDMA * (STAGES - 2)) : "memory");
         __builtin_amdgcn_sched_barrier(0);
         const QG_LDS uint8_t* sA = cur + wm * 64 * BKB;
         const QG_LDS uint8_t* sB = cur + OPB + wn * 64 * BKB;
         bf[0] = frag(sB, rdb0, rdb1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = frag(sA + 16 * i * BKB, rd8, rd8 ^ 64);
-        const float sb = *(const QG_LDS float*)(cur + SB_OFF);
+        for (int i = 0; i < 4; ++i) af[i] = frag(sA + 16 * i * BKB, rd8, rd8b);
+        if constexpr (MX) {
+            // E8M0 bytes of the lane's rows: fp8 byte q, fp4 bytes 2q, 2q + 1
+            int sa[4], sb[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fs[i] = *(const QG_LDS float*)(cur + SA_OFF + 4 * (wm * 64 + 16 * i + l16)) * sb;
-        const Src src = sources(t + STAGES - 1);
-        __builtin_amdgcn_sched_barrier(0);
+            for (int x = 0; x < 4; ++x) {
+                const QG_LDS uint8_t* pa = cur + SA_OFF + (wm * 64 + 16 * x + l16) * KTB;
+                const QG_LDS uint8_t* pb = cur + SB_OFF + (wn * 64 + 16 * x + l16) * KTB;
+                sa[x] = FP4 ? *(const QG_LDS uint16_t*)(pa + 2 * q) : pa[q];
+                sb[x] = FP4 ? *(const QG_LDS uint16_t*)(pb + 2 * q) : pb[q];
+            }
+            const Src src = sources(t + STAGES - 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int j = k >> 2, i = k & 3;
-            if (i == 0 && j < 3) bf[(j + 1) & 1] = frag(sB + (j + 1) * 16 * BKB, rdb0, rdb1);
-            part[k & 1] = mfma_part(bf[j & 1], af[i]);
+            for (int k = 0; k < 16; ++k) {
+                const int j = k >> 2, i = k & 3;
+                if (i == 0 && j < 3) bf[(j + 1) & 1] = frag(sB + (j + 1) * 16 * BKB, rdb0, rdb1);
+                const i32x8& b = bf[j & 1];
+                if constexpr (FP4) {
+                    const i32x8 b0 = i32x8{b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+                    const i32x8 b1 = i32x8{b[4], b[5], b[6], b[7], 0, 0, 0, 0};
+                    const i32x8 a0 = i32x8{af[i][0], af[i][1], af[i][2], af[i][3], 0, 0, 0, 0};
+                    const i32x8 a1 = i32x8{af[i][4], af[i][5], af[i][6], af[i][7], 0, 0, 0, 0};
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b0, a0, acc[i][j], kFmtFp4, kFmtFp4,
+                                                                                 0, sb[j], 0, sa[i]);
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b1, a1, acc[i][j], kFmtFp4, kFmtFp4,
+                                                                                 1, sb[j], 1, sa[i]);
+                } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b, af[i], acc[i][j], kFmtFp8,
+                                                                                 kFmtFp8, 0, sb[j], 0, sa[i]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (k < NDMA) dma(nxt, src, k);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            const float sb = *(const QG_LDS float*)(cur + SB_OFF);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fs[i] = *(const QG_LDS float*)(cur + SA_OFF + 4 * (wm * 64 + 16 * i + l16)) * sb;
+            const Src src = sources(t + STAGES - 1);
             __builtin_amdgcn_sched_barrier(0);
-            if (k > 0) rescale((k - 1) & 3, (k - 1) >> 2, (k - 1) & 1);
-            if (k < 9) dma(nxt, src, k);
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int j = k >> 2, i = k & 3;
+                if (i == 0 && j < 3) bf[(j + 1) & 1] = frag(sB + (j + 1) * 16 * BKB, rdb0, rdb1);
+                part[k & 1] = mfma_part(bf[j & 1], af[i]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (k > 0) rescale((k - 1) & 3, (k - 1) >> 2, (k - 1) & 1);
+                if (k < NDMA) dma(nxt, src, k);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            rescale(3, 3, 1);
         }
-        rescale(3, 3, 1);
     };
 
     // ---- prologue: K-tiles 0 .. STAGES - 2 into their stages ----
     mid::static_for<STAGES - 1>([&](auto SC) __attribute__((always_inline)) {
         const Src s0 = sources(decltype(SC)::value);
 #pragma unroll
-        for (int d = 0; d < 9; ++d) dma(stage(SC), s0, d);
+        for (int d = 0; d < NDMA; ++d) dma(stage(SC), s0, d);
     });
     int t = 0;
     for (; t + STAGES <= nk; t += STAGES)

@@ -102,7 +102,11 @@ def test_workspace_queries(qgemm):
         assert ws >= 2048 + 2 * m * n * 4 and (ws - 2048) % (m * n * 4) == 0, (m, n, k, ws)
     # enough N tiles for the skinny kernel -> no split
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=7168, k=16384))) == 0
-    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=4096))) == 0
+    # M > 64 with few 256 x 256 tiles: the 128 x 128 kernel, 64 tiles, K
+    # split in two (16 K-tiles per slice at least)
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=4096))) == \
+        2048 + 2 * 128 * 8192 * 4
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=1024))) == 0
     # too few K-tiles to split (8 per slice at least)
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=1536, k=1024))) == 0
     assert L.gemm_a8w8_mxfp8_workspace_bytes(None) == 0
