@@ -1,5 +1,5 @@
-// Four-wave 128 x 128 tile GEMM for fp8 with fp32 block scales (BSF32), with
-// split-K, for the middle of the M range on gfx950.
+// Four-wave 128 x 128 tile GEMM with split-K for the middle of the M range
+// on gfx950: fp8 with fp32 block scales (BSF32), and MXFP8 / MXFP4 (MX).
 //
 // At M ~ 256-4096 with narrow N the 256 x 256 tiles of bsf32_gemm.hpp leave
 // most of the 256 CUs idle (M = 1024, N = 2112: 36 tiles).  This kernel cuts
@@ -21,6 +21,13 @@
 //  * B' (K-panel): the tile's 128 rows of a K-tile are 16 contiguous KB;
 //    B'' (the LDS-bypass entry's fragment order): 8 blocks of 2 KB, copied
 //    as is and read back linearly (the block is the MFMA operand order);
+//  * MX (row-major B, its rows DMA'd like A's): the K-tile's E8M0 bytes of
+//    the tile's 128 A and 128 B rows ride in the stage beside the operands
+//    (4 bytes per row for fp8, 8 for fp4; one or two dword DMAs per wave)
+//    and the scaled MFMA applies them, accumulating in place (no VALU
+//    rescale).  fp8: lane (q, r) holds chunks q and q + 4 of row r with
+//    scale byte q; fp4: two MFMAs per K-tile, chunks 2q and 2q + 1 with
+//    scale bytes 2q and 2q + 1 (op_sel 0 and 1 of one 16-bit read);
 //  * split-K: each workgroup stores its fp32 partial tile device-coherently,
 //    then one relaxed counter atomic per workgroup (common.hpp); the last
 //    workgroup of a tile adds the slices in slice order (deterministic),
