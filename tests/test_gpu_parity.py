@@ -63,9 +63,11 @@ def test_probe_known_answers(qgemm, gpu):
 
 
 # ----------------------------------------------------------------- MXFP8
-# M > 256 runs the 256 x 256 tile kernel, smaller M the skinny kernel
+# M <= 64 runs the stream / skinny / decode kernels; larger M the 256 x 256
+# tile kernel with >= 128 of its tiles ((2100, 4100, 256): 153, tails in M
+# and N), else the 128 x 128 kernel
 MX8_SHAPES = [(256, 256, 128), (256, 512, 1024), (300, 520, 384), (1, 1536, 7168), (32, 1536, 7168),
-              (513, 272, 256), (512, 512, 2048), (768, 1024, 512)]
+              (513, 272, 256), (512, 512, 2048), (768, 1024, 512), (2100, 4100, 256)]
 
 
 @pytest.mark.parametrize("m,n,k", MX8_SHAPES)
@@ -79,7 +81,7 @@ def test_mxfp8(qgemm, gpu, m, n, k, dtype):
     assert_close(ref, out_to_f32(y), f"mxfp8 {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 256, 1024), (512, 512, 4096), (300, 520, 1536)])
+@pytest.mark.parametrize("m,n,k", [(512, 256, 1024), (512, 512, 4096), (300, 520, 1536), (2304, 3600, 1536)])
 def test_mxfp8_k_pattern_scales(qgemm, gpu, m, n, k):
     """Distinct per-K-group scales catch K-group and scale panel misrouting
     (MX4 host.cc:185-187; 32- and 16-byte panels)."""
@@ -94,7 +96,7 @@ def test_mxfp8_k_pattern_scales(qgemm, gpu, m, n, k):
 
 # ----------------------------------------------------------------- MXFP4
 MX4_SHAPES = [(256, 256, 256), (256, 512, 1024), (100, 300, 512), (1, 512, 2048), (257, 256, 768),
-              (512, 512, 2048), (384, 1024, 512), (300, 520, 3072), (512, 768, 4096)]
+              (512, 512, 2048), (384, 1024, 512), (300, 520, 3072), (512, 768, 4096), (2100, 4100, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", MX4_SHAPES)
@@ -106,7 +108,8 @@ def test_mxfp4(qgemm, gpu, m, n, k):
     assert_close(ref, out_to_f32(y), f"mxfp4 {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 256, 4096), (300, 520, 3072), (512, 512, 1536)])
+@pytest.mark.parametrize("m,n,k", [(512, 256, 4096), (300, 520, 3072), (512, 512, 1536), (2304, 3600, 2048),
+                                   (2304, 3600, 1536)])
 def test_mxfp4_k_pattern_scales(qgemm, gpu, m, n, k):
     """Distinct per-K-group scales on both operands catch K-group and scale
     panel misrouting (32-, 16- and 8-byte panels)."""
@@ -187,8 +190,9 @@ def test_mx_wide_scale_panels(qgemm, gpu, fp4, k):
     (E8M0 scales copied panel-major first: 32-byte panels for fp4 with
     K % 1024 == 0, else 16-byte) against the oracle, and bit-equal to the
     same call without a workspace (row-major scales read directly); padded
-    scale row pitches and batch strides, M and N tails."""
-    m, n, batch = 520, 300, 2
+    scale row pitches and batch strides, M and N tails; 144 256 x 256 tiles
+    keep the shape on the wide kernel (below 128 it runs 128 x 128 tiles)."""
+    m, n, batch = 1300, 3000, 2
     make = make_mx4 if fp4 else make_mx8
     data = [make(m, n, k, seed=600 + i + 10 * fp4) for i in range(batch)]
     kb, kg = (k // 2 if fp4 else k), k // 32
