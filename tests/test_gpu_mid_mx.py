@@ -33,6 +33,9 @@ def _run(qgemm, gpu, fp4, qa, qb, ea, eb, dtype=torch.bfloat16, workspace=None):
 # in partial tiles
 MID_SHAPES = [(128, 7168, 16384), (65, 1000, 1024), (200, 2112, 7168), (256, 4096, 2048), (300, 1536, 4096),
               (520, 2112, 2048), (1000, 2112, 1024), (1500, 640, 3072)]
+# one K-tile for fp4 (two for fp8: the prologue's empty-range DMAs and the
+# tail loop alone), N below one tile, 129-row / 129-column tails
+EDGE_SHAPES = [(100, 50, 256), (70, 130, 512), (129, 129, 1024), (80, 16, 768)]
 
 
 @pytest.mark.parametrize("m,n,k", MID_SHAPES)
@@ -43,6 +46,16 @@ def test_mx_mid(qgemm, gpu, fp4, m, n, k, split):
     qa, qb, ea, eb = make(m, n, k, seed=7 * m + n + k + fp4)
     y = _run(qgemm, gpu, fp4, qa, qb, ea, eb, workspace=None if split else False)
     assert_close(gemm(qa, qb, ea, eb), out_to_f32(y), f"{'mxfp4' if fp4 else 'mxfp8'} mid {m}x{n}x{k} split={split}")
+
+
+@pytest.mark.parametrize("m,n,k", EDGE_SHAPES)
+@pytest.mark.parametrize("fp4", [False, True])
+def test_mx_mid_edges(qgemm, gpu, fp4, m, n, k):
+    make, gemm = (make_mx4, O.gemm_mx4) if fp4 else (make_mx8, O.gemm_mx8)
+    qa, qb, ea, eb = make(m, n, k, seed=3 * m + n + k + fp4)
+    for dtype in (torch.bfloat16, torch.float32):
+        y = _run(qgemm, gpu, fp4, qa, qb, ea, eb, dtype=dtype)
+        assert_close(gemm(qa, qb, ea, eb), out_to_f32(y), f"mid edge {m}x{n}x{k} {dtype}")
 
 
 @pytest.mark.parametrize("fp4", [False, True])
