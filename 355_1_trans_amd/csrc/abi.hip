@@ -244,7 +244,8 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
 // fp32 block scales: M <= kMidMinM keeps the decode / skinny plan; larger M
 // runs the 256 x 256 kernel once it has at least kMidBelow tiles, else the
 // 128 x 128 kernel, with K split until about kMidTarget workgroups (two per
-// CU) are in flight, >= kMidMinKt K-tiles per slice.
+// CU) are in flight -- kCUs (one per CU) when the tiles alone split K at
+// least in two -- with >= kMidMinKt K-tiles per slice.
 constexpr int kMidMinM = 64;
 constexpr int kMidBelow = 128;
 constexpr int kMidTarget = 2 * kCUs;
@@ -263,7 +264,12 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch) {
     if (tiles >= kMidTarget / 2 || tiles > kCounterBytes / (long long)sizeof(unsigned) ||
         (long long)m * n >= (1LL << 29))    // partial offsets are 32-bit bytes
         return;
-    const long long split = std::min<long long>(kMidTarget / tiles, k_tiles / kMidMinKt);
+    long long split = std::min<long long>(kMidTarget / tiles, k_tiles / kMidMinKt);
+    // up to kCUs / 2 tiles: at most one workgroup per CU (four LDS stages,
+    // longer slices, fewer partials) -- N = 7168, K = 16384: MXFP8 M = 128
+    // 75.0 -> 61.9 us, BS fp32 M = 128 64.9 -> 47.0, M = 256 76.5 -> 64.0,
+    // MXFP4 M = 256 54.7 -> 50.7; shapes with less K unchanged
+    if (kCUs / tiles >= 2) split = std::min<long long>(split, kCUs / tiles);
     if (split <= 1) return;
     p.kt_per_split = ceil_div(k_tiles, (int)split);
     p.splitk = ceil_div(k_tiles, p.kt_per_split);
