@@ -107,6 +107,15 @@ def test_workspace_queries(qgemm):
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=4096))) == \
         2048 + 2 * 128 * 8192 * 4
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=1024))) == 0
+    # 56 tiles of 128 x 128 at N = 7168: split capped at kCUs / tiles = 4
+    # (one workgroup per CU), not 512 / 56 = 9; MXFP4 K-tiles are 256 deep
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=7168, k=16384))) == \
+        2048 + 4 * 128 * 7168 * 4
+    assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=7168, k=16384))) == \
+        2048 + 4 * 128 * 7168 * 4
+    # 136 tiles (> kCUs / 2): two workgroups per CU, 56 K-tiles / 16 -> 3 slices
+    assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1024, n=2112, k=7168))) == \
+        2048 + 3 * 1024 * 2112 * 4
     # too few K-tiles to split (8 per slice at least)
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=1536, k=1024))) == 0
     assert L.gemm_a8w8_mxfp8_workspace_bytes(None) == 0
