@@ -64,8 +64,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 }  // namespace mid
 
 // SK = BSF32: fp8, fp32 block scales, B' or B''; SK = MX: fp8 or fp4 (FMT),
-// E8M0 scales per 32 K, row-major B, the scales applied by the MFMA
-template <bool BF16, BLay BL, int STAGES, ScaleKind SK = ScaleKind::BSF32, int FMT = kFmtFp8>
+// E8M0 scales per 32 K, row-major B, the scales applied by the MFMA.
+// NTB: B through the nontemporal cache policy (one M tile: B is read once)
+template <bool BF16, BLay BL, int STAGES, ScaleKind SK = ScaleKind::BSF32, int FMT = kFmtFp8, bool NTB = false>
 __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(const MidArgs mp) {
     static_assert(STAGES == 2 || STAGES == 4, "two stages (two workgroups per CU) or four (one)");
     constexpr bool MX = (SK == ScaleKind::MX);
@@ -202,7 +203,10 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
     // DMA d (0 .. NDMA-1) of a K-tile into stage st: 0-3 A, 4-7 B, then scales
     auto dma = [&](QG_LDS uint8_t* st, const Src& s, int d) __attribute__((always_inline)) {
         if (d < 4) dma16_buf(s.a, st + (4 * w + d) * 1024, aoff[d], 0);
-        else if (d < 8) dma16_buf(s.b, st + OPB + (4 * w + d - 4) * 1024, boff[d - 4], 0);
+        else if (d < 8) {
+            if constexpr (NTB) dma16_buf_nt(s.b, st + OPB + (4 * w + d - 4) * 1024, boff[d - 4], 0);
+            else dma16_buf(s.b, st + OPB + (4 * w + d - 4) * 1024, boff[d - 4], 0);
+        }
         else if (d == 8) dma4_buf(s.sc, st + sc_dst[0], sc_voff[0], 0);
         else dma4_buf(s.sc, st + sc_dst[SCD - 1], sc_voff[SCD - 1], 0);
     };
