@@ -147,7 +147,10 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
  * MX8/gemm_a8w8_mxfp8_kernel_template.hpp:300-432). TN layout: A [M,K],
  * B [N,K] K-contiguous; SFA [M,K/32], SFB [N,K/32] uint8 row-major
  * (stride_sfa/stride_sfb = row pitch, MX8 host.cc:282-285). C bf16/fp32.
- * Any M, N >= 1, K a multiple of 128. */
+ * Any M, N >= 1, K a multiple of 128. `workspace` (may be NULL;
+ * gemm_a8w8_mxfp8_workspace_bytes; contract as above): split-K partials for
+ * small and middle M (fewer than 128 256x256 tiles), reduced in the same
+ * launch; at larger M a panel-major copy of both operands' E8M0 scales. */
 hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
@@ -158,9 +161,11 @@ size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
 /* Replaces the launch in MX4/gemm_a4w4_mxfp4_4wave_host.cc:201-216. A [M,K/2],
  * B [N,K/2] bytes (even k in the low nibble), strides in bytes; SFA [M,K/32],
  * SFB [N,K/32] uint8 row-major. C bf16/fp32. Any M, N >= 1; K a multiple of
- * 256. For skinny M the call splits K across workgroups when `workspace`
- * is given (gemm_a4w4_mxfp4_workspace_bytes; contract as above) and reduces
- * the fp32 partials in the same launch. */
+ * 256. For small and middle M (fewer than 128 256x256 tiles) the call
+ * splits K across workgroups when `workspace` is given
+ * (gemm_a4w4_mxfp4_workspace_bytes; contract as above) and reduces the fp32
+ * partials in the same launch; at larger M the workspace holds a
+ * panel-major copy of both operands' E8M0 scales. */
 hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args);
