@@ -26,16 +26,13 @@ buffer per (device, stream); pass a tensor to supply your own, or
 ``workspace=False`` to run without split-K.
 """
 import ctypes
-import os
 from functools import lru_cache
 from pathlib import Path
 
 import torch
 
 _PKG = Path(__file__).resolve().parent
-# QGEMM_LIB selects another build of the same library (A/B tests of kernel
-# variants); by default the in-tree build is loaded.
-LIB_PATH = Path(os.environ.get("QGEMM_LIB", str(_PKG / "libqgemm.so")))
+LIB_PATH = _PKG / "libqgemm.so"
 
 OUT_FP32 = 0
 OUT_BF16 = 1
@@ -97,6 +94,7 @@ EXPORTS = {
     "qgemm_probe_words": (ctypes.c_int, []),
     "qgemm_probe_mfma_layout": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "qgemm_version": (ctypes.c_char_p, []),
+    "qgemm_last_launch": (ctypes.c_char_p, []),
 }
 
 
@@ -112,6 +110,12 @@ def lib():
         fn.restype = res
         fn.argtypes = args
     return L
+
+
+def last_launch():
+    """Kernel instantiations launched by this thread's most recent library
+    call (qgemm_last_launch), e.g. 'wide_gemm<fp8,MX,RAW,bf16,pb16>'."""
+    return lib().qgemm_last_launch().decode()
 
 
 def _check(status, what):

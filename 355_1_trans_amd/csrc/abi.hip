@@ -8,7 +8,9 @@
 #include <algorithm>
 #include <atomic>
 #include <climits>
+#include <cstdarg>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 
 #include "launch.hpp"
@@ -22,6 +24,33 @@ static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "referen
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, stride_sfa) == 80, "reference kargs ABI");
 static_assert(__builtin_offsetof(opus_gemm_ldsbypass_kargs, ptr_c) == 24, "ldsbypass kargs ABI");
 
+namespace qg {
+
+namespace {
+thread_local char g_trace[512];
+thread_local size_t g_trace_len;
+}  // namespace
+
+const char* g_trace_str() { return g_trace; }
+
+void trace_reset() {
+    g_trace_len = 0;
+    g_trace[0] = 0;
+}
+
+void trace_launch(const char* fmt, ...) {
+    if (g_trace_len + 2 >= sizeof(g_trace)) return;
+    if (g_trace_len) g_trace[g_trace_len++] = '+';
+    va_list ap;
+    va_start(ap, fmt);
+    const int w = std::vsnprintf(g_trace + g_trace_len, sizeof(g_trace) - g_trace_len, fmt, ap);
+    va_end(ap);
+    if (w > 0) g_trace_len = std::min(sizeof(g_trace) - 1, g_trace_len + (size_t)w);
+    g_trace[g_trace_len] = 0;
+}
+
+}  // namespace qg
+
 namespace {
 
 using qg::SkinnyArgs;
@@ -30,6 +59,23 @@ using qg::TileArgs;
 
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_arch_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 other
+std::atomic<int> g_cus[kMaxDevices];      // compute units, 0 = not read yet
+
+// Compute units of the current device: every plan sizes its grid and K
+// split to one round of workgroups on this device (256 on MI355X).
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (dev >= 0 && dev < kMaxDevices) {
+        const int known = g_cus[dev].load(std::memory_order_relaxed);
+        if (known > 0) return known;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (dev >= 0 && dev < kMaxDevices) g_cus[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
 
 // Current device must be gfx950 (SNAP launch.cc:55-61).
 hipError_t check_arch() {
@@ -73,7 +119,18 @@ uint64_t span(long long batch, long long batch_stride, long long rows, long long
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-void fill_common(TileArgs& t, const opus_gemm_scale_kargs& a, int kbytes) {
+// Elements per aligned vector store of C: the largest power of two (at
+// most 16 bytes) whose byte size divides ptr_c, the row pitch and, for
+// batch > 1, the batch stride.
+int c_vec_elems(const opus_gemm_scale_kargs& a, int out_elem) {
+    uintptr_t bits = reinterpret_cast<uintptr_t>(a.ptr_c) | (uintptr_t)((long long)a.stride_c * out_elem);
+    if (a.batch > 1) bits |= (uintptr_t)((long long)a.stride_c_batch * out_elem);
+    int align = 16;
+    while (align > out_elem && (bits & (uintptr_t)(align - 1))) align >>= 1;
+    return align / out_elem;
+}
+
+void fill_common(TileArgs& t, const opus_gemm_scale_kargs& a, int kbytes, int out_elem) {
     t.a = static_cast<const uint8_t*>(a.ptr_a);
     t.b = static_cast<const uint8_t*>(a.ptr_b);
     t.c = a.ptr_c;
@@ -85,6 +142,7 @@ void fill_common(TileArgs& t, const opus_gemm_scale_kargs& a, int kbytes) {
     t.lda = a.stride_a;
     t.ldb = a.stride_b;
     t.ldc = a.stride_c;
+    t.c_vec = c_vec_elems(a, out_elem);
     t.a_batch = a.stride_a_batch;
     t.b_batch = a.stride_b_batch;
     t.c_batch = a.stride_c_batch;
@@ -124,18 +182,19 @@ bool dma_aligned(const opus_gemm_scale_kargs& a, bool scales_dword) {
 // HBM bandwidth needs most of the 256 CUs busy: the plan takes the widest N
 // tile (64, 32 or 16 columns) that gives at least kMinTiles workgroups.  When
 // even 16-column tiles give fewer than kSplitBelow, K is split across
-// workgroups -- only up to one round of workgroups (kCUs), keeping >= 16
+// workgroups -- only up to one round of workgroups (cus), keeping >= 16
 // K-tiles per slice and the fp32 partials below a quarter of B's bytes.  The
 // plan depends on the shape only, so the workspace query and the launch
 // always agree.
-constexpr int kCUs = 256;
 constexpr int kMinTiles = 192;
 constexpr int kSplitBelow = 128;
-// Split-K runs only with fewer than kSplitBelow tiles, so its counters fit a
-// fixed block at the start of the workspace; a fixed size keeps the counters
-// of any later call clear of earlier calls' partials.
-constexpr size_t kCounterBytes = 2 * kCUs * sizeof(unsigned);
-static_assert(kSplitBelow <= 2 * kCUs, "counter block too small");
+// Split-K counters sit in a fixed block at the start of the workspace (the
+// 2048 bytes the workspace contract names); a fixed size keeps the counters
+// of any later call clear of earlier calls' partials.  A split needs one
+// counter per output tile, so splits are planned only up to kMaxCounters tiles.
+constexpr size_t kCounterBytes = 2048;
+constexpr long long kMaxCounters = kCounterBytes / sizeof(unsigned);
+static_assert(kSplitBelow <= kMaxCounters, "counter block too small");
 
 struct Plan {
     bool skinny = false;
@@ -152,7 +211,7 @@ struct Plan {
 // in flight wins (8 on a tie: A is shared by more columns).
 constexpr int kDecodeMinKt = 8;
 
-void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_bytes) {
+void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_bytes, int cus) {
     p.decode = true;
     p.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     p.m_tiles = 1;
@@ -160,8 +219,9 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
     for (int nw : {8, 4}) {
         const long long tiles = (long long)ceil_div(n, 16 * nw) * batch;
         long long split = 1;
-        if (tiles < kCUs / 2 && (long long)m * n < (1LL << 29)) {    // partial offsets are 32-bit bytes
-            split = std::min<long long>(kCUs / tiles, k_tiles / kDecodeMinKt);
+        if (tiles < cus / 2 && tiles <= kMaxCounters &&
+            (long long)m * n < (1LL << 29)) {    // partial offsets are 32-bit bytes
+            split = std::min<long long>(cus / tiles, k_tiles / kDecodeMinKt);
             split = std::min<long long>(split, b_bytes / (16LL * m * n));
             split = std::max<long long>(split, 1);
         }
@@ -177,7 +237,7 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
         }
     }
     if (p.splitk > 1) {
-        p.ctr_bytes = kCounterBytes;    // split only below kCUs / 2 tiles
+        p.ctr_bytes = kCounterBytes;    // split only below cus / 2 tiles
         p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
     } else {
         p.kt_per_split = k_tiles;
@@ -204,8 +264,8 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
 // decode_short: the short-K rule alone (MXFP4, which the decode kernel
 // otherwise streams slower than the skinny kernel; M = 16, 32 with 12-16
 // K-tiles: 16.7, 13.6 -> 14.0, 12.6 us, M = 64 alike)
-Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool force_skinny, bool decode_ok = true,
-               bool decode_wide = false, bool decode_short = false) {
+Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, int cus, bool force_skinny,
+               bool decode_ok = true, bool decode_wide = false, bool decode_short = false) {
     Plan p;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
     p.skinny = force_skinny || (m <= 256 && tiles256 < 128);
@@ -223,12 +283,12 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
     if (m <= 64 && ((decode_ok && (base < kSplitBelow || short_k ||
                                    (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32))) ||
                     (decode_short && short_k))) {
-        plan_decode(p, m, n, k_tiles, batch, b_bytes);
+        plan_decode(p, m, n, k_tiles, batch, b_bytes, cus);
         return p;
     }
     if (base >= kSplitBelow) return p;
     if ((long long)m * n >= (1LL << 29)) return p;    // partial offsets are 32-bit bytes
-    long long split = kCUs / base;
+    long long split = cus / base;
     split = std::min<long long>(split, k_tiles / 16);
     split = std::min<long long>(split, b_bytes / (16LL * m * n));
     if (split <= 1) return p;
@@ -243,17 +303,16 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, bool for
 
 // fp32 block scales: M <= kMidMinM keeps the decode / skinny plan; larger M
 // runs the 256 x 256 kernel once it has at least kMidBelow tiles, else the
-// 128 x 128 kernel, with K split until about kMidTarget workgroups (two per
-// CU) are in flight -- kCUs (one per CU) when the tiles alone split K at
+// 128 x 128 kernel, with K split until about 2 * cus workgroups (two per
+// CU) are in flight -- cus (one per CU) when the tiles alone split K at
 // least in two -- with >= kMidMinKt K-tiles per slice.
 constexpr int kMidMinM = 64;
 constexpr int kMidBelow = 128;
-constexpr int kMidTarget = 2 * kCUs;
 constexpr int kMidMinKt = 16;    // 8 measured slower where the split tail dominates (M = 256, N = 4096, K = 7168: 34.4 vs 27.0 us)
 
 // Replaces p with a 128 x 128 plan when M > kMidMinM and the 256 x 256
 // kernel would have fewer than kMidBelow tiles.
-void plan_mid(Plan& p, int m, int n, int k_tiles, int batch) {
+void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus) {
     if (m <= kMidMinM) return;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
     if (tiles256 >= kMidBelow) return;
@@ -261,15 +320,15 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch) {
     p.mid = true;
     p.kt_per_split = k_tiles;
     const long long tiles = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
-    if (tiles >= kMidTarget / 2 || tiles > kCounterBytes / (long long)sizeof(unsigned) ||
-        (long long)m * n >= (1LL << 29))    // partial offsets are 32-bit bytes
+    const long long target = 2LL * cus;    // two workgroups per CU
+    if (tiles >= target / 2 || tiles > kMaxCounters || (long long)m * n >= (1LL << 29))    // 32-bit partial offsets
         return;
-    long long split = std::min<long long>(kMidTarget / tiles, k_tiles / kMidMinKt);
-    // up to kCUs / 2 tiles: at most one workgroup per CU (four LDS stages,
+    long long split = std::min<long long>(target / tiles, k_tiles / kMidMinKt);
+    // up to cus / 2 tiles: at most one workgroup per CU (four LDS stages,
     // longer slices, fewer partials) -- N = 7168, K = 16384: MXFP8 M = 128
     // 75.0 -> 61.9 us, BS fp32 M = 128 64.9 -> 47.0, M = 256 76.5 -> 64.0,
     // MXFP4 M = 256 54.7 -> 50.7; shapes with less K unchanged
-    if (kCUs / tiles >= 2) split = std::min<long long>(split, kCUs / tiles);
+    if (cus / tiles >= 2) split = std::min<long long>(split, cus / tiles);
     if (split <= 1) return;
     p.kt_per_split = ceil_div(k_tiles, (int)split);
     p.splitk = ceil_div(k_tiles, p.kt_per_split);
@@ -280,16 +339,18 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch) {
 }
 
 Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
-    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, false, decode_ok, decode_ok);
-    plan_mid(p, m, n, k_tiles, batch);
+    const int cus = device_cus();
+    Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false, decode_ok, decode_ok);
+    plan_mid(p, m, n, k_tiles, batch, cus);
     return p;
 }
 
 // MX: the same 128 x 128 rule (row-major B, E8M0 scales applied by the MFMA)
 Plan plan_mx(int m, int n, int k_tiles, int batch, long long b_bytes, bool fp4) {
-    Plan p = fp4 ? plan_gemm(m, n, k_tiles, batch, b_bytes, false, false, false, true)
-                 : plan_gemm(m, n, k_tiles, batch, b_bytes, false);
-    plan_mid(p, m, n, k_tiles, batch);
+    const int cus = device_cus();
+    Plan p = fp4 ? plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false, false, false, true)
+                 : plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false);
+    plan_mid(p, m, n, k_tiles, batch, cus);
     return p;
 }
 
@@ -327,7 +388,7 @@ StreamPlan plan_stream(int m, int n, int k, int batch, bool fp4) {
     p.splitk = ceil_div(nseg, p.seg_per_split);
     // about one workgroup per CU; rows bounded by the waves' row groups and
     // by the LDS image of their B scales
-    const long long nblk_target = std::max<long long>(1, kCUs / ((long long)p.splitk * batch));
+    const long long nblk_target = std::max<long long>(1, device_cus() / ((long long)p.splitk * batch));
     long long rows = (n + nblk_target - 1) / nblk_target;
     const int wsp = 1 << qg::stream_ws_log2(p.seg_per_split * 64 / p.wr);
     rows = std::min<long long>(rows, std::min(qg::stream_max_rows(p.wr), qg::kStreamWsBytes / wsp));
@@ -441,7 +502,7 @@ hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, qg::MidKind kind, 
     // four LDS stages, three K-tiles in flight; else two workgroups per CU
     // with two stages each
     const long long wgs = (long long)t.tiles_m * t.tiles_n * batch * a.splitk;
-    return qg::launch_mid(a, batch, bf16, kind, wgs <= kCUs ? 4 : 2, stream);
+    return qg::launch_mid(a, batch, bf16, kind, wgs <= device_cus() ? 4 : 2, stream);
 }
 
 // Launches the skinny or decode kernel.  A NULL workspace runs one K slice
@@ -496,9 +557,38 @@ hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bo
     return qg::launch_skinny(kind, s, pl.mb, pl.nb, batch, bf16, stream);
 }
 
+// Byte ranges of a call's operands (C first), for the overlap checks of the
+// output and of the workspace.
+struct Spans {
+    const void* p[6];
+    uint64_t bytes[6];
+    int n = 0;
+    void add(const void* q, uint64_t b) {
+        p[n] = q;
+        bytes[n++] = b;
+    }
+    bool overlap_any(const void* q, uint64_t b, int from) const {
+        for (int i = from; i < n; ++i)
+            if (overlaps(q, b, p[i], bytes[i])) return true;
+        return false;
+    }
+};
+
+// One workspace rule for every entry point and every route: NULL runs
+// without a workspace (no K split; wide MX kernels read row-major scales
+// directly); a non-NULL workspace must hold the bytes the entry's
+// *_workspace_bytes query returns, be 256-byte aligned and overlap neither C
+// nor an input.  Checked once, before routing.
+hipError_t check_workspace(const void* ws, size_t ws_bytes, size_t need, const Spans& sp) {
+    if (!ws || need == 0) return hipSuccess;
+    if (ws_bytes < need || !aligned(ws, 256) || sp.overlap_any(ws, need, 0)) return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
 // Validation shared by the MX entry points: dense or padded row-major A/B,
 // row-major scales, C [M, N] with stride_c >= N.
-hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kbytes_per_row, int k_align) {
+hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kbytes_per_row, int k_align,
+                       Spans* sp) {
     if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
         !flag01(out_dtype))
         return hipErrorInvalidValue;
@@ -512,6 +602,7 @@ hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kby
         a.stride_sfa_batch % 4 || a.stride_sfb_batch % 4)
         return hipErrorInvalidValue;
     const long long outb = out_dtype ? 2 : 4;
+    if (!aligned(a.ptr_c, (uintptr_t)outb)) return hipErrorInvalidValue;
     if (a.batch > 1 &&
         ((long long)a.stride_a_batch < (long long)a.m * a.stride_a ||
          (long long)a.stride_b_batch < (long long)a.n * a.stride_b ||
@@ -523,12 +614,12 @@ hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kby
         !bounded_count(a.m, a.stride_c, 1, outb) || !bounded_count(a.m, a.stride_sfa, 1, 1) ||
         !bounded_count(a.n, a.stride_sfb, 1, 1))
         return hipErrorInvalidValue;
-    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb);
-    if (overlaps(a.ptr_c, cb, a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, kbytes_per_row, 1)) ||
-        overlaps(a.ptr_c, cb, a.ptr_b, span(a.batch, a.stride_b_batch, a.n, a.stride_b, kbytes_per_row, 1)) ||
-        overlaps(a.ptr_c, cb, a.ptr_sfa, span(a.batch, a.stride_sfa_batch, a.m, a.stride_sfa, kg, 1)) ||
-        overlaps(a.ptr_c, cb, a.ptr_sfb, span(a.batch, a.stride_sfb_batch, a.n, a.stride_sfb, kg, 1)))
-        return hipErrorInvalidValue;
+    sp->add(a.ptr_c, span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb));
+    sp->add(a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, kbytes_per_row, 1));
+    sp->add(a.ptr_b, span(a.batch, a.stride_b_batch, a.n, a.stride_b, kbytes_per_row, 1));
+    sp->add(a.ptr_sfa, span(a.batch, a.stride_sfa_batch, a.m, a.stride_sfa, kg, 1));
+    sp->add(a.ptr_sfb, span(a.batch, a.stride_sfb_batch, a.n, a.stride_sfb, kg, 1));
+    if (sp->overlap_any(sp->p[0], sp->bytes[0], 1)) return hipErrorInvalidValue;
     return hipSuccess;
 }
 
@@ -538,7 +629,7 @@ hipError_t validate_mx(const opus_gemm_scale_kargs* args, int out_dtype, int kby
 // B is checked by the caller (b_data, b_bytes_per_batch).  Returns the SFA
 // element strides along M and K.
 hipError_t validate_bsf32(const opus_gemm_scale_kargs& a, const void* b_data, long long b_bytes_per_batch,
-                          int out_dtype, int* sfa_sm, int* sfa_sk) {
+                          int out_dtype, int* sfa_sm, int* sfa_sk, Spans* sp) {
     if (!a.ptr_a || !b_data || !a.ptr_c || !a.ptr_sfa || !a.ptr_sfb || !flag01(out_dtype))
         return hipErrorInvalidValue;
     if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % 128) return hipErrorInvalidValue;
@@ -550,6 +641,7 @@ hipError_t validate_bsf32(const opus_gemm_scale_kargs& a, const void* b_data, lo
         !aligned(a.ptr_sfa, 4) || !aligned(a.ptr_sfb, 4))
         return hipErrorInvalidValue;
     const long long outb = out_dtype ? 2 : 4;
+    if (!aligned(a.ptr_c, (uintptr_t)outb)) return hipErrorInvalidValue;
     const long long sfa_span = sfa_rowmajor ? (long long)a.m * kg : (long long)(kg - 1) * a.stride_sfa + a.m;
     if (a.batch > 1 &&
         ((long long)a.stride_a_batch < (long long)a.m * a.stride_a ||
@@ -560,11 +652,11 @@ hipError_t validate_bsf32(const opus_gemm_scale_kargs& a, const void* b_data, lo
         !bounded_count(a.m, a.stride_c, 1, outb) || !bounded_count(sfa_span, 1, 1, 4) ||
         !bounded_count(nbk, a.stride_sfb, 1, 4))
         return hipErrorInvalidValue;
-    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb);
-    if (overlaps(a.ptr_c, cb, a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, a.k, 1)) ||
-        overlaps(a.ptr_c, cb, a.ptr_sfa, span(a.batch, a.stride_sfa_batch, 1, 0, sfa_span, 4)) ||
-        overlaps(a.ptr_c, cb, a.ptr_sfb, span(a.batch, a.stride_sfb_batch, nbk, a.stride_sfb, kg, 4)))
-        return hipErrorInvalidValue;
+    sp->add(a.ptr_c, span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, outb));
+    sp->add(a.ptr_a, span(a.batch, a.stride_a_batch, a.m, a.stride_a, a.k, 1));
+    sp->add(a.ptr_sfa, span(a.batch, a.stride_sfa_batch, 1, 0, sfa_span, 4));
+    sp->add(a.ptr_sfb, span(a.batch, a.stride_sfb_batch, nbk, a.stride_sfb, kg, 4));
+    if (sp->overlap_any(sp->p[0], sp->bytes[0], 1)) return hipErrorInvalidValue;
     *sfa_sm = sfa_rowmajor ? kg : 1;
     *sfa_sk = sfa_rowmajor ? 1 : a.stride_sfa;
     return hipSuccess;
@@ -605,13 +697,17 @@ extern "C" {
 // ---------------------------------------------------------------- MXFP8
 hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-    hipError_t st = validate_mx(args, out_dtype, args ? args->k : 0, 128);
+    qg::trace_reset();
+    Spans sp;
+    hipError_t st = validate_mx(args, out_dtype, args ? args->k : 0, 128, &sp);
+    if (st != hipSuccess) return st;
+    st = check_workspace(workspace, workspace_bytes, gemm_a8w8_mxfp8_workspace_bytes(args), sp);
     if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
     const auto& a = *args;
     TileArgs t{};
-    fill_common(t, a, a.k);
+    fill_common(t, a, a.k, out_dtype ? 2 : 4);
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
@@ -642,13 +738,17 @@ size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
 // ---------------------------------------------------------------- MXFP4
 hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-    hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256);
+    qg::trace_reset();
+    Spans sp;
+    hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256, &sp);
+    if (st != hipSuccess) return st;
+    st = check_workspace(workspace, workspace_bytes, gemm_a4w4_mxfp4_workspace_bytes(args), sp);
     if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
     const auto& a = *args;
     TileArgs t{};
-    fill_common(t, a, a.k / 2);
+    fill_common(t, a, a.k / 2, out_dtype ? 2 : 4);
     t.sfa_sm = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
@@ -681,6 +781,7 @@ size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
 // Same checks, in the same order, as SNAP gemm_a8w8_blockscale_bpreshuffle_launch.cc:31-65.
 hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int output_bf16, int tiles,
                                          hipStream_t stream) {
+    qg::trace_reset();
     if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
         !flag01(output_bf16) || !flag01(tiles))
         return hipErrorInvalidValue;
@@ -701,11 +802,11 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
         overlaps(a.ptr_c, c_bytes, a.ptr_sfa, uint64_t(a.stride_sfa_batch) * a.batch) ||
         overlaps(a.ptr_c, c_bytes, a.ptr_sfb, uint64_t(a.stride_sfb_batch) * a.batch))
         return hipErrorInvalidValue;
-    if (!dma_aligned(a, false)) return hipErrorInvalidValue;
+    if (!dma_aligned(a, false) || !aligned(a.ptr_c, output_bf16 ? 2 : 4)) return hipErrorInvalidValue;
     hipError_t st = check_arch();
     if (st != hipSuccess) return st;
     TileArgs t{};
-    fill_common(t, a, a.k);
+    fill_common(t, a, a.k, output_bf16 ? 2 : 4);
     t.sfa_sk = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
     return qg::launch_wide_bs8_w16(t, a.batch, output_bf16 == 1, stream);
@@ -714,21 +815,25 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
 // ------------------------------------------------ block-scale FP8, fp32 scales
 hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
                                             size_t workspace_bytes, hipStream_t stream) {
+    qg::trace_reset();
     if (!args) return hipErrorInvalidValue;
     const auto& a = *args;
     // B is K-panel [K/128][N][128] (stride_b = 128, BPS host.cc:263)
     if (a.stride_b != 128) return hipErrorInvalidValue;
     const long long bk = (long long)a.n * a.k;
     int sfa_sm = 0, sfa_sk = 0;
-    hipError_t st = validate_bsf32(a, a.ptr_b, bk, out_dtype, &sfa_sm, &sfa_sk);
+    Spans sp;
+    hipError_t st = validate_bsf32(a, a.ptr_b, bk, out_dtype, &sfa_sm, &sfa_sk, &sp);
     if (st != hipSuccess) return st;
     if (a.batch > 1 && ((long long)a.stride_b_batch < bk || a.stride_b_batch % 16)) return hipErrorInvalidValue;
-    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, out_dtype ? 2 : 4);
-    if (overlaps(a.ptr_c, cb, a.ptr_b, span(a.batch, a.stride_b_batch, 1, 0, bk, 1))) return hipErrorInvalidValue;
+    sp.add(a.ptr_b, span(a.batch, a.stride_b_batch, 1, 0, bk, 1));
+    if (sp.overlap_any(sp.p[0], sp.bytes[0], sp.n - 1)) return hipErrorInvalidValue;
+    st = check_workspace(workspace, workspace_bytes, gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(args), sp);
+    if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
     TileArgs t{};
-    fill_common(t, a, a.k);
+    fill_common(t, a, a.k, out_dtype ? 2 : 4);
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
@@ -752,21 +857,24 @@ size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* a
 // ------------------------------------------------ LDS-bypass block-scale FP8
 hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args, int out_dtype, void* workspace,
                                           size_t workspace_bytes, hipStream_t stream) {
+    qg::trace_reset();
     if (!args) return hipErrorInvalidValue;
     const opus_gemm_scale_kargs a = from_ldsbypass(*args);
     const long long bpp = a.n > 0 && a.k > 0 ? (long long)frag_bytes(a.n, a.k) : 0;
     int sfa_sm = 0, sfa_sk = 0;
-    hipError_t st = validate_bsf32(a, args->ptr_b_pp, bpp, out_dtype, &sfa_sm, &sfa_sk);
+    Spans sp;
+    hipError_t st = validate_bsf32(a, args->ptr_b_pp, bpp, out_dtype, &sfa_sm, &sfa_sk, &sp);
     if (st != hipSuccess) return st;
     if (a.batch > 1 && ((long long)args->stride_b_pp_batch < bpp || args->stride_b_pp_batch % 16))
         return hipErrorInvalidValue;
-    const uint64_t cb = span(a.batch, a.stride_c_batch, a.m, a.stride_c, a.n, out_dtype ? 2 : 4);
-    if (overlaps(a.ptr_c, cb, args->ptr_b_pp, span(a.batch, args->stride_b_pp_batch, 1, 0, bpp, 1)))
-        return hipErrorInvalidValue;
+    sp.add(args->ptr_b_pp, span(a.batch, args->stride_b_pp_batch, 1, 0, bpp, 1));
+    if (sp.overlap_any(sp.p[0], sp.bytes[0], sp.n - 1)) return hipErrorInvalidValue;
+    st = check_workspace(workspace, workspace_bytes, gemm_a8w8_blockscale_ldsbypass_workspace_bytes(args), sp);
+    if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
     TileArgs t{};
-    fill_common(t, a, a.k);
+    fill_common(t, a, a.k, out_dtype ? 2 : 4);
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
@@ -789,6 +897,7 @@ size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_
 
 // B' (K-panel, ptr_b, stride_b = 128) -> B'' (ptr_b_pp) on the GPU.
 hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs* args, hipStream_t stream) {
+    qg::trace_reset();
     if (!args || !args->ptr_b || !args->ptr_b_pp) return hipErrorInvalidValue;
     const auto& l = *args;
     if (l.n <= 0 || l.k <= 0 || l.k % 128 || l.batch <= 0 || l.stride_b != 128) return hipErrorInvalidValue;
@@ -880,6 +989,8 @@ hipError_t qgemm_probe_mfma_layout(int32_t* dev_out, hipStream_t stream) {
     return qg::launch_probe(dev_out, stream);
 }
 
-const char* qgemm_version(void) { return "qgemm gfx950 1"; }
+const char* qgemm_version(void) { return "qgemm gfx950 2"; }
+
+const char* qgemm_last_launch(void) { return qg::g_trace_str(); }
 
 }  // extern "C"

@@ -349,8 +349,10 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
 
     // ---- epilogue: lane holds C[16i + l16][16jj + 4q + 0..3] of the wave's
     // 64 x 128 block ----
-    const bool vec_ok = (LDC & 3) == 0;
-    if (vec_ok && m0 + BM <= M && n0 + BM <= N) {
+    // 4-element stores need 8- (bf16) or 16-byte (fp32) aligned row starts;
+    // the bf16 whole-tile path stores 16 bytes (8 elements) per lane
+    const bool vec_ok = p.c_vec >= 4;
+    if (p.c_vec >= (BF16 ? 8 : 4) && m0 + BM <= M && n0 + BM <= N) {
         if constexpr (BF16) {
             // bf16 through the wave's own 16 KB of LDS (rows of 256 B, 16-byte
             // chunks XOR-swizzled by row) so that every global store writes

@@ -271,7 +271,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
         if (m >= M) return;
         if constexpr (BF16) {
             uint16_t* c = (uint16_t*)p.c + bz * p.c_batch + (long long)m * LDC + n;
-            if (n + 3 < N && (LDC & 3) == 0) {
+            if (n + 3 < N && p.c_vec >= 4) {
                 *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             } else {
                 for (int r = 0; r < 4; ++r)
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
             }
         } else {
             float* c = (float*)p.c + bz * p.c_batch + (long long)m * LDC + n;
-            if (n + 3 < N && (LDC & 3) == 0) {
+            if (n + 3 < N && p.c_vec >= 4) {
                 *(f32x4*)c = v;
             } else {
                 for (int r = 0; r < 4; ++r)
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
         // the thread's 4 columns start at nn
         if constexpr (BF16) {
             uint16_t* c = (uint16_t*)p.c + bz * p.c_batch + (long long)m * LDC + nn;
-            if (nn + 3 < N && (LDC & 3) == 0) {
+            if (nn + 3 < N && p.c_vec >= 4) {
                 *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             } else {
                 for (int r = 0; r < 4; ++r)
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
             }
         } else {
             float* c = (float*)p.c + bz * p.c_batch + (long long)m * LDC + nn;
-            if (nn + 3 < N && (LDC & 3) == 0) {
+            if (nn + 3 < N && p.c_vec >= 4) {
                 *(f32x4*)c = v;
             } else {
                 for (int r = 0; r < 4; ++r)

@@ -13,6 +13,7 @@ hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipS
         if (bf16) bsf32_gemm_kernel<true, BLay::KPANEL><<<grid, 512, 0, s>>>(a);
         else bsf32_gemm_kernel<false, BLay::KPANEL><<<grid, 512, 0, s>>>(a);
     }
+    trace_launch("bsf32_gemm<fp8,BSF32,%s,%s>", frag ? "FRAG" : "KPANEL", bf16 ? "bf16" : "fp32");
     return hipGetLastError();
 }
 

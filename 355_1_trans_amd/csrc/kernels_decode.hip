@@ -12,6 +12,8 @@ hipError_t launch_decode_family(const DecodeArgs& a, int mb, int nw, int batch, 
     if (mb == MBV && nw == NWV) {                                                                 \
         if (bf16) decode_gemm_kernel<FMT, SK, BL, MBV, NWV, true><<<grid, NWV * 64, 0, s>>>(a);   \
         else decode_gemm_kernel<FMT, SK, BL, MBV, NWV, false><<<grid, NWV * 64, 0, s>>>(a);       \
+        trace_launch("decode_gemm<%s,%s,%s,mb%d,nw%d,%s,splitk%d>", FMT == kFmtFp4 ? "fp4" : "fp8",  \
+                     scale_name(SK), layout_name(BL), MBV, NWV, bf16 ? "bf16" : "fp32", a.splitk);  \
         return hipGetLastError();                                                                 \
     }
     QG_DECODE_CASE(1, 4) QG_DECODE_CASE(2, 4) QG_DECODE_CASE(4, 4)

@@ -9,6 +9,8 @@ template <BLay BL, int ST, ScaleKind SK, int FMT, bool NTB = false>
 static void mid_go(const MidArgs& a, const dim3& grid, bool bf16, hipStream_t s) {
     if (bf16) mid_gemm_kernel<true, BL, ST, SK, FMT, NTB><<<grid, 256, 0, s>>>(a);
     else mid_gemm_kernel<false, BL, ST, SK, FMT, NTB><<<grid, 256, 0, s>>>(a);
+    trace_launch("mid_gemm<%s,%s,%s,%s,st%d%s,splitk%d>", FMT == kFmtFp4 ? "fp4" : "fp8", scale_name(SK),
+                 layout_name(BL), bf16 ? "bf16" : "fp32", ST, NTB ? ",ntb" : "", (int)grid.y);
 }
 
 // MX with one M tile reads B once: nontemporal B loads (N = 7168,

@@ -14,6 +14,8 @@ hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batc
     if (fp4 == F && wr == WRV && mb == MBV) {                                                      \
         if (bf16) stream_gemm_kernel<F, WRV, MBV, true><<<grid, kStreamWaves * 64, 0, s>>>(a);     \
         else stream_gemm_kernel<F, WRV, MBV, false><<<grid, kStreamWaves * 64, 0, s>>>(a);         \
+        trace_launch("stream_gemm<%s,wr%d,mb%d,%s,splitk%d>", F ? "fp4" : "fp8", WRV, MBV,          \
+                     bf16 ? "bf16" : "fp32", a.splitk);                                            \
         return hipGetLastError();                                                                  \
     }
 #define QG_STREAM_FMT(F) QG_STREAM_CASE(F, 1, 1) QG_STREAM_CASE(F, 2, 2) QG_STREAM_CASE(F, 4, 4) QG_STREAM_CASE(F, 4, 8)

@@ -11,6 +11,8 @@ hipError_t launch_wide(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     const dim3 block(256);
     if (bf16) wide_gemm_kernel<FMT, SK, BL, true, PB><<<grid, block, 0, s>>>(a);
     else wide_gemm_kernel<FMT, SK, BL, false, PB><<<grid, block, 0, s>>>(a);
+    trace_launch("wide_gemm<%s,%s,%s,%s,pb%d>", FMT == kFmtFp4 ? "fp4" : "fp8", scale_name(SK), layout_name(BL),
+                 bf16 ? "bf16" : "fp32", PB);
     return hipGetLastError();
 }
 }  // namespace
@@ -52,6 +54,7 @@ hipError_t launch_mx_scale_panels(const ScalePanelArgs& a, int batch, hipStream_
     const long long blocks = (units + 255) / 256;
     const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024), batch, 2);
     mx_scale_panels_kernel<<<grid, 256, 0, s>>>(a);
+    trace_launch("mx_scale_panels<pb%d>", a.pb);
     return hipGetLastError();
 }
 

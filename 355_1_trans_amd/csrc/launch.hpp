@@ -6,6 +6,12 @@
 
 namespace qg {
 
+// Per-thread record of the kernels launched by the calling thread's most
+// recent entry-point call (read back with qgemm_last_launch): the entry
+// point resets it, every launcher appends its exact instantiation.
+void trace_reset();
+const char* g_trace_str();
+void trace_launch(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
 // kernels_bsf32.hip: eight-wave 256 x 256 tiles, fp32 block scales; B' (K-panel) or,
 // with frag, B'' (the LDS-bypass entry's fragment order)

@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
 
     // ---- output: lane holds C[16i + l16][16j + 4q + 0..3] of the wave's block ----
     const int mw = m0 + wm * 64 + l16, nw0 = n0 + wn * 64 + 4 * q;
-    const bool vec_ok = (LDC & 3) == 0;
+    const bool vec_ok = p.c_vec >= 4;    // aligned 4-element C stores
     auto store_c = [&](int m, int n, f32x4 v) __attribute__((always_inline)) {
         if (m >= M) return;
         if constexpr (BF16) {

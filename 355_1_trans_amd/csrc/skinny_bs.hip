@@ -46,6 +46,7 @@ hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int
     const long long units = (long long)((n + 15) / 16) * (k / 128) * 128;
     const int blocks = (int)std::min<long long>((units + 255) / 256, 4096);
     repack_frag_kernel<<<dim3(blocks, batch), 256, 0, s>>>(bk, bpp, n, k / 128, bk_batch, bpp_batch);
+    trace_launch("repack_frag");
     return hipGetLastError();
 }
 

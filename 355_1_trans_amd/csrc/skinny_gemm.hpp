@@ -49,6 +49,7 @@
 #pragma once
 #include <utility>
 
+#include "launch.hpp"
 #include "tile_args.hpp"
 
 namespace qg {
@@ -450,7 +451,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
         if (m >= M) return;
         if constexpr (BF16) {
             uint16_t* c = (uint16_t*)p.c + bz * p.c_batch + (long long)m * LDC + n;
-            if (n + 3 < N && (LDC & 3) == 0) {
+            if (n + 3 < N && p.c_vec >= 4) {
                 *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             } else {
                 for (int r = 0; r < 4; ++r)
@@ -458,7 +459,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
             }
         } else {
             float* c = (float*)p.c + bz * p.c_batch + (long long)m * LDC + n;
-            if (n + 3 < N && (LDC & 3) == 0) {
+            if (n + 3 < N && p.c_vec >= 4) {
                 *(f32x4*)c = v;
             } else {
                 for (int r = 0; r < 4; ++r)
@@ -539,6 +540,9 @@ hipError_t launch_skinny_family(const SkinnyArgs& a, int mb, int nb, int batch, 
 #define QG_SKINNY_LAUNCH(MBV, NBV, SCPV, NTV)                                                        \
     if (bf16) skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, true, SCPV, NTV><<<grid, block, 0, s>>>(a);  \
     else skinny_gemm_kernel<FMT, SK, BL, MBV, NBV, false, SCPV, NTV><<<grid, block, 0, s>>>(a);      \
+    trace_launch("skinny_gemm<%s,%s,%s,mb%d,nb%d,%s%s%s,splitk%d>", FMT == kFmtFp4 ? "fp4" : "fp8",    \
+                 scale_name(SK), layout_name(BL), MBV, NBV, bf16 ? "bf16" : "fp32", SCPV ? ",scp" : "",  \
+                 NTV ? ",ntb" : "", a.splitk);                                                       \
     return hipGetLastError();
 // mb < 4 always means one M tile (the plan takes mb = 4 beyond 32 rows)
 #define QG_SKINNY_NT(MBV, NBV, SCPV)                                                                 \

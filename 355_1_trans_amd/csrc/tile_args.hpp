@@ -27,6 +27,13 @@ namespace qg {
 enum class ScaleKind : int { MX = 0, BS8 = 1, BSF32 = 2 };
 enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2, FRAG = 3 };
 
+constexpr const char* scale_name(ScaleKind k) {
+    return k == ScaleKind::MX ? "MX" : k == ScaleKind::BS8 ? "BS8" : "BSF32";
+}
+constexpr const char* layout_name(BLay l) {
+    return l == BLay::RAW ? "RAW" : l == BLay::KPANEL ? "KPANEL" : l == BLay::W16 ? "W16" : "FRAG";
+}
+
 struct TileArgs {
     const uint8_t* a;
     const uint8_t* b;
@@ -37,6 +44,8 @@ struct TileArgs {
     int kbytes;          // bytes of K per row: K (fp8) or K/2 (fp4); multiple of 128
     int lda, ldb;        // row pitch in bytes (ldb: RAW only)
     int ldc;             // row pitch of C in elements
+    int c_vec;           // elements per aligned C vector store (1, 2, 4 or 8): the largest
+                         // power of two whose byte size divides ptr_c, ldc and c_batch (max 16 B)
     long long a_batch, b_batch, c_batch, sfa_batch, sfb_batch;  // batch strides (bytes / elements)
     // scale addressing (in scale elements):
     //   MX    : sfa(m, g) = sfa[m*sfa_sm + g], sfb(n, g) = sfb[n*sfb_sn + g]; the

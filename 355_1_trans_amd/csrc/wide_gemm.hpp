@@ -479,8 +479,10 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         return FP4 ? 32 * j + 8 * v4 + 4 * g : 16 * j + 4 * q;
     };
     constexpr int NV4 = FP4 ? 4 : 1;
-    const bool vec_ok = (LDC & 3) == 0;
-    if (vec_ok && m0 + BM <= M && n0 + BM <= N) {
+    // 4-element stores need 8- (bf16) or 16-byte (fp32) aligned row starts;
+    // the bf16 whole-tile path stores 16 bytes (8 elements) per lane
+    const bool vec_ok = p.c_vec >= 4;
+    if (p.c_vec >= (BF16 ? 8 : 4) && m0 + BM <= M && n0 + BM <= N) {
         if constexpr (BF16) {
             // Whole tile inside C, bf16: the wave's 128 x 128 block goes
             // through its own 32 KB of LDS (one operand stage, rows of 256 B,

@@ -199,6 +199,15 @@ hipError_t qgemm_probe_mfma_layout(int32_t* dev_out, hipStream_t stream);
 /* Library identification: "gfx950" build string. */
 const char* qgemm_version(void);
 
+/* Diagnostics, no counterpart in the reference: the kernel instantiations
+ * (name<template arguments>, joined by '+') that the calling thread's most
+ * recent entry-point call launched, e.g.
+ * "mx_scale_panels<pb16>+wide_gemm<fp8,MX,RAW,bf16,pb16>"; empty when that
+ * call launched nothing (rejected arguments).  Tests and the benchmark use
+ * it to name the exact kernel they check or time.  The string is owned by
+ * the library and valid until the thread's next entry-point call. */
+const char* qgemm_last_launch(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,8 @@ def lib():
             "ora_quant_bs_wgt": (None, [_f32p, _i, _i, _u8p, _f32p]),
             "ora_quant_mx8": (None, [_f32p, _i, _i, _u8p, _u8p]),
             "ora_quant_mx4": (None, [_f32p, _i, _i, _u8p, _u8p]),
+            "ora_quant_bs_e8m0_act": (None, [_f32p, _i, _i, _u8p, _u8p]),
+            "ora_quant_bs_e8m0_wgt": (None, [_f32p, _i, _i, _u8p, _u8p]),
             "ora_ceil_log2": (_i, [ctypes.c_float]),
             "ora_shuffle_b_kpanel": (None, [_u8p, _u8p, _i, _i, _i]),
             "ora_shuffle_weight_16x16": (None, [_u8p, _u8p, _i, _i]),
@@ -64,9 +66,11 @@ def lib():
             "ora_gemm_bs_fp32": (None, [_u8p, _u8p, _f32p, _f32p, _f32p] + [_i] * 10),
             "ora_gemm_mx8": (None, [_u8p, _u8p, _u8p, _u8p, _f32p] + [_i] * 8),
             "ora_gemm_mx4": (None, [_u8p, _u8p, _u8p, _u8p, _f32p] + [_i] * 8),
+            "ora_gemm_mx4_grouped": (None, [_u8p, _u8p, _u8p, _u8p, _f32p] + [_i] * 8),
             "ora_gemm_bs_e8m0": (None, [_u8p, _u8p, _u8p, _u8p, _f32p, ctypes.c_void_p] + [_i] * 8),
             "ora_gemm_bs_fp32_points": (None, [_u8p, _u8p, _f32p, _f32p] + [_i] * 7 + [_i32p, _i32p, _sz, _f32p]),
             "ora_gemm_mx8_points": (None, [_u8p, _u8p, _u8p, _u8p] + [_i] * 5 + [_i32p, _i32p, _sz, _f32p]),
+            "ora_gemm_bs_e8m0_points": (None, [_u8p, _u8p, _u8p, _u8p] + [_i] * 5 + [_i32p, _i32p, _sz, _f32p]),
             "ora_gemm_mx4_points": (None, [_u8p, _u8p, _u8p, _u8p] + [_i] * 5 + [_i32p, _i32p, _sz, _f32p]),
             "ora_check_tolerance": (_sz, [_f32p, _f32p, _sz, ctypes.c_double,
                                           ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_size_t)]),
@@ -178,6 +182,28 @@ def quant_mx4(x):
     return q, e
 
 
+def quant_bs_e8m0_act(x):
+    """e4m3 [M,K] and E8M0 codes [M,K/128], one 2^ceil(log2(amax/448)) per 1x128 block."""
+    x = _c(x, np.float32)
+    m, k = x.shape
+    assert k % 128 == 0
+    q = np.empty((m, k), np.uint8)
+    e = np.empty((m, k // 128), np.uint8)
+    lib().ora_quant_bs_e8m0_act(x, m, k, q, e)
+    return q, e
+
+
+def quant_bs_e8m0_wgt(w):
+    """e4m3 [N,K] and E8M0 codes [ceil(N/128),K/128], one per 128x128 block."""
+    w = _c(w, np.float32)
+    n, k = w.shape
+    assert k % 128 == 0
+    q = np.empty((n, k), np.uint8)
+    e = np.empty(((n + 127) // 128, k // 128), np.uint8)
+    lib().ora_quant_bs_e8m0_wgt(w, n, k, q, e)
+    return q, e
+
+
 # ---------------------------------------------------------------- layouts
 def shuffle_b_kpanel(b, block_k=128):
     b = _c(b, np.uint8)
@@ -256,13 +282,19 @@ def gemm_mx8_points(a, b, sfa, sfb, rows, cols):
     return out
 
 
-def gemm_mx4(a, b, sfa, sfb):
-    """a [M,K/2], b [N,K/2] packed e2m1 bytes; scales [rows, K/32]."""
+def gemm_mx4(a, b, sfa, sfb, literal=False):
+    """a [M,K/2], b [N,K/2] packed e2m1 bytes; scales [rows, K/32].
+
+    Default: the grouped form of the reference's gemm_ref_gpu (MX4
+    host.cc:66-94); literal=True: the per-element gemm_ref_cpu loop
+    (MX4 host.cc:96-115).  Both are exact up to the final fp32 rounding and
+    agree bit for bit on every recipe here (tests/test_oracle.py)."""
     a, b, sfa, sfb = (_c(t, np.uint8) for t in (a, b, sfa, sfb))
     m, kb = a.shape
     n = b.shape[0]
     c = np.empty((m, n), np.float32)
-    lib().ora_gemm_mx4(a, b, sfa, sfb, c, m, n, 2 * kb, kb, kb, n, sfa.shape[1], sfb.shape[1])
+    fn = lib().ora_gemm_mx4 if literal else lib().ora_gemm_mx4_grouped
+    fn(a, b, sfa, sfb, c, m, n, 2 * kb, kb, kb, n, sfa.shape[1], sfb.shape[1])
     return c
 
 
@@ -286,6 +318,16 @@ def gemm_bs_e8m0(a, b, sfa_km, sfb, with_mag=False):
     lib().ora_gemm_bs_e8m0(a, b, sfa_km, sfb, c, mag.ctypes.data if with_mag else None,
                            m, n, k, k, k, n, m, k // 128)
     return (c, mag) if with_mag else c
+
+
+def gemm_bs_e8m0_points(a, b, sfa_km, sfb, rows, cols):
+    """Sampled (rows[t], cols[t]) outputs of gemm_bs_e8m0."""
+    a, b, sfa_km, sfb = (_c(t, np.uint8) for t in (a, b, sfa_km, sfb))
+    m, k = a.shape
+    rows, cols = _c(rows, np.int32), _c(cols, np.int32)
+    out = np.empty(rows.size, np.float32)
+    lib().ora_gemm_bs_e8m0_points(a, b, sfa_km, sfb, k, k, k, m, k // 128, rows, cols, rows.size, out)
+    return out
 
 
 # ---------------------------------------------------------------- tolerance

@@ -250,6 +250,50 @@ void ora_quant_mx4(const float* x, int rows, int k, uint8_t* q, uint8_t* e) {
     }
 }
 
+/* Block-scale FP8 with E8M0 scales (the input format of the reference's
+ * fastest block-scale kernel, SNAP blockscale_bpreshuffle.py:3-4,54-56):
+ * one power-of-two scale 2^ceil(log2(amax/448)) per 1x128 activation block
+ * or 128x128 weight block, the MX rule at block-scale granularity.
+ * Codes: E + 127; the activation scales are written row-major [M][K/128]. */
+void ora_quant_bs_e8m0_act(const float* x, int m, int k, uint8_t* q, uint8_t* e) {
+    const int kg = k / 128;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < m; ++r) {
+        for (int g = 0; g < kg; ++g) {
+            const float* src = x + (size_t)r * k + (size_t)g * 128;
+            float amax = 0.0f;
+            for (int i = 0; i < 128; ++i) amax = fmaxf(amax, fabsf(src[i]));
+            const int E = mx_exponent(amax, 448.0f);
+            e[(size_t)r * kg + g] = (uint8_t)(E + 127);
+            uint8_t* dst = q + (size_t)r * k + (size_t)g * 128;
+            for (int i = 0; i < 128; ++i) dst[i] = ora_f32_to_e4m3(ldexpf(src[i], -E));
+        }
+    }
+}
+
+void ora_quant_bs_e8m0_wgt(const float* w, int n, int k, uint8_t* q, uint8_t* e) {
+    const int kg = k / 128;
+    const int nb = (n + 127) / 128;
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < nb; ++b) {
+        for (int g = 0; g < kg; ++g) {
+            const int r0 = b * 128;
+            const int r1 = (r0 + 128 < n) ? r0 + 128 : n;
+            float amax = 0.0f;
+            for (int r = r0; r < r1; ++r)
+                for (int i = 0; i < 128; ++i)
+                    amax = fmaxf(amax, fabsf(w[(size_t)r * k + (size_t)g * 128 + i]));
+            const int E = mx_exponent(amax, 448.0f);
+            e[(size_t)b * kg + g] = (uint8_t)(E + 127);
+            for (int r = r0; r < r1; ++r)
+                for (int i = 0; i < 128; ++i) {
+                    const size_t idx = (size_t)r * k + (size_t)g * 128 + i;
+                    q[idx] = ora_f32_to_e4m3(ldexpf(w[idx], -E));
+                }
+        }
+    }
+}
+
 /* ===================================================================== */
 /* layout transforms                                                      */
 /* ===================================================================== */
@@ -391,40 +435,102 @@ void ora_gemm_mx4(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const 
                                               sfa + (size_t)i * sfa_ld, sfb + (size_t)j * sfb_ld, k);
 }
 
+/* Grouped form of the same product, the reference's gemm_ref_gpu
+ * (MX4 host.cc:66-94): per 32-element group an fp32 partial of the E2M1
+ * products (at most 32 products of multiples of 1/4 up to 36, so the
+ * partial is exact in fp32), then sum += partial * 2^(ea+eb-254) in fp64.
+ * g_e2m1_pair[x][y] is one byte pair's two products, t0 + t1, in the
+ * reference's statement order.  Whenever the fp64 sums are exact (scale
+ * spreads below ~2^40, which covers every recipe here) the result is
+ * bit-identical to the literal gemm_ref_cpu loop above. */
+static float g_e2m1_pair[256 * 256];
+static int g_pair_ready = 0;
+
+static void init_pair_lut(void) {
+    if (__atomic_load_n(&g_pair_ready, __ATOMIC_ACQUIRE)) return;
+    #pragma omp critical(ora_pair_lut)
+    {
+        if (!g_pair_ready) {
+            for (int x = 0; x < 256; ++x)
+                for (int y = 0; y < 256; ++y) {
+                    const float t0 = ora_e2m1_to_f32((unsigned)x & 15u) * ora_e2m1_to_f32((unsigned)y & 15u);
+                    const float t1 = ora_e2m1_to_f32((unsigned)x >> 4) * ora_e2m1_to_f32((unsigned)y >> 4);
+                    g_e2m1_pair[x * 256 + y] = t0 + t1;
+                }
+            __atomic_store_n(&g_pair_ready, 1, __ATOMIC_RELEASE);
+        }
+    }
+}
+
+static inline float mx4_elem_grouped(const uint8_t* a_row, const uint8_t* b_row, const uint8_t* sfa_row,
+                                     const uint8_t* sfb_row, int k) {
+    double sum = 0.0;
+    for (int g = 0; g < k / 32; ++g) {
+        float part = 0.0f;
+        for (int p = 0; p < 16; ++p) part += g_e2m1_pair[(unsigned)a_row[g * 16 + p] * 256u + b_row[g * 16 + p]];
+        sum += (double)part * ldexp(1.0, (int)sfa_row[g] + (int)sfb_row[g] - 254);
+    }
+    return (float)sum;
+}
+
+void ora_gemm_mx4_grouped(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
+                          float* c, int m, int n, int k, int lda, int ldb, int ldc, int sfa_ld, int sfb_ld) {
+    init_pair_lut();
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j)
+            c[(size_t)i * ldc + j] = mx4_elem_grouped(a + (size_t)i * lda, b + (size_t)j * ldb,
+                                                      sfa + (size_t)i * sfa_ld, sfb + (size_t)j * sfb_ld, k);
+}
+
 void ora_gemm_mx4_points(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
                          int k, int lda, int ldb, int sfa_ld, int sfb_ld,
                          const int32_t* rows, const int32_t* cols, size_t np, float* out) {
+    init_pair_lut();
     #pragma omp parallel for schedule(static)
     for (size_t t = 0; t < np; ++t) {
         const int i = rows[t], j = cols[t];
-        out[t] = mx4_elem(a + (size_t)i * lda, b + (size_t)j * ldb, sfa + (size_t)i * sfa_ld,
-                          sfb + (size_t)j * sfb_ld, k);
+        out[t] = mx4_elem_grouped(a + (size_t)i * lda, b + (size_t)j * ldb, sfa + (size_t)i * sfa_ld,
+                                  sfb + (size_t)j * sfb_ld, k);
     }
+}
+
+static inline float bs_e8m0_elem(const uint8_t* a_row, const uint8_t* b_row, const uint8_t* sfa,
+                                 const uint8_t* sfb, int i, int j, int k, int sfa_sk, int sfb_sn,
+                                 double* mag_out) {
+    double sum = 0.0, sum_abs = 0.0;
+    for (int g = 0; g < k / 128; ++g) {
+        const double scale = (double)ora_e8m0_to_f32(sfa[(size_t)g * sfa_sk + i]) *
+                             (double)ora_e8m0_to_f32(sfb[(size_t)(j / 128) * sfb_sn + g]);
+        for (int p = g * 128; p < (g + 1) * 128; ++p) {
+            const double term = (double)g_e4m3_lut[a_row[p]] * (double)g_e4m3_lut[b_row[p]] * scale;
+            sum += term;
+            sum_abs += fabs(term);
+        }
+    }
+    if (mag_out) *mag_out = sum_abs;
+    return (float)sum;
 }
 
 void ora_gemm_bs_e8m0(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
                       float* c, double* mag, int m, int n, int k, int lda, int ldb, int ldc,
                       int sfa_sk, int sfb_sn) {
     init_lut();
-    const int groups_k = k / 128;
     #pragma omp parallel for collapse(2) schedule(static)
-    for (int i = 0; i < m; ++i) {
-        for (int j = 0; j < n; ++j) {
-            const uint8_t* a_row = a + (size_t)i * lda;
-            const uint8_t* b_row = b + (size_t)j * ldb;
-            double sum = 0.0, sum_abs = 0.0;
-            for (int g = 0; g < groups_k; ++g) {
-                const double scale = (double)ora_e8m0_to_f32(sfa[(size_t)g * sfa_sk + i]) *
-                                     (double)ora_e8m0_to_f32(sfb[(size_t)(j / 128) * sfb_sn + g]);
-                for (int p = g * 128; p < (g + 1) * 128; ++p) {
-                    const double term = (double)g_e4m3_lut[a_row[p]] * (double)g_e4m3_lut[b_row[p]] * scale;
-                    sum += term;
-                    sum_abs += fabs(term);
-                }
-            }
-            c[(size_t)i * ldc + j] = (float)sum;
-            if (mag) mag[(size_t)i * ldc + j] = sum_abs;
-        }
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j)
+            c[(size_t)i * ldc + j] = bs_e8m0_elem(a + (size_t)i * lda, b + (size_t)j * ldb, sfa, sfb, i, j, k,
+                                                  sfa_sk, sfb_sn, mag ? mag + (size_t)i * ldc + j : NULL);
+}
+
+void ora_gemm_bs_e8m0_points(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
+                             int k, int lda, int ldb, int sfa_sk, int sfb_sn,
+                             const int32_t* rows, const int32_t* cols, size_t np, float* out) {
+    init_lut();
+    #pragma omp parallel for schedule(static)
+    for (size_t t = 0; t < np; ++t) {
+        const int i = rows[t], j = cols[t];
+        out[t] = bs_e8m0_elem(a + (size_t)i * lda, b + (size_t)j * ldb, sfa, sfb, i, j, k, sfa_sk, sfb_sn, NULL);
     }
 }
 

@@ -52,6 +52,11 @@ void ora_quant_mx8(const float* x, int rows, int k, uint8_t* q, uint8_t* e);
 /* MXFP4: per 32-group scale 2^ceil(log2(amax/6)); q [R][K/2], low nibble
  * holds the even element; e [R][K/32]. */
 void ora_quant_mx4(const float* x, int rows, int k, uint8_t* q, uint8_t* e);
+/* Block-scale FP8 with E8M0 scales 2^ceil(log2(amax/448)): per 1x128
+ * activation block (e row-major [M][K/128]) or 128x128 weight block
+ * (e [ceil(N/128)][K/128]); codes E + 127. */
+void ora_quant_bs_e8m0_act(const float* x, int m, int k, uint8_t* q, uint8_t* e);
+void ora_quant_bs_e8m0_wgt(const float* w, int n, int k, uint8_t* q, uint8_t* e);
 /* Exponent helper: ceil(log2(v)) for v > 0. */
 int  ora_ceil_log2(float v);
 
@@ -82,6 +87,11 @@ void ora_gemm_mx8(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const 
  * a [M][lda bytes], b [N][ldb bytes]. */
 void ora_gemm_mx4(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
                   float* c, int m, int n, int k, int lda, int ldb, int ldc, int sfa_ld, int sfb_ld);
+/* The same product in the grouped form of MX4 host.cc:66-94 (gemm_ref_gpu):
+ * exact fp32 partial per 32-element group, fp64 sum of partial * scale.
+ * Bit-identical to ora_gemm_mx4 whenever the fp64 sums are exact. */
+void ora_gemm_mx4_grouped(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
+                          float* c, int m, int n, int k, int lda, int ldb, int ldc, int sfa_ld, int sfb_ld);
 /* Block-scale FP8 with E8M0 scales (SNAP host.cc:219-248): fp64
  * accumulation; also returns sum|term| in mag (may be NULL).
  * sfa physical [K/128][M] (sfa(m,kg) = sfa[kg*sfa_sk + m]); sfb [N/128][sfb_sn]. */
@@ -97,6 +107,9 @@ void ora_gemm_bs_fp32_points(const uint8_t* a, const uint8_t* b, const float* sf
 void ora_gemm_mx8_points(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
                          int k, int lda, int ldb, int sfa_ld, int sfb_ld,
                          const int32_t* rows, const int32_t* cols, size_t np, float* out);
+void ora_gemm_bs_e8m0_points(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
+                             int k, int lda, int ldb, int sfa_sk, int sfb_sn,
+                             const int32_t* rows, const int32_t* cols, size_t np, float* out);
 void ora_gemm_mx4_points(const uint8_t* a, const uint8_t* b, const uint8_t* sfa, const uint8_t* sfb,
                          int k, int lda, int ldb, int sfa_ld, int sfb_ld,
                          const int32_t* rows, const int32_t* cols, size_t np, float* out);

@@ -165,3 +165,83 @@ def test_no_cpu_fallback(qgemm):
     s = torch.zeros(16, 4, dtype=torch.uint8)
     with pytest.raises(ValueError, match="GPU"):
         qgemm.gemm_a8w8_mxfp8(a, a, s, s)
+
+
+# ----------------------------------------------------------------- workspace rule
+def _far_kargs(qgemm, m, n, k, fp4=False, out_bytes=2):
+    """Kargs whose operands sit at widely separated, 256-byte aligned fake
+    addresses (never dereferenced: every call below is rejected before any
+    device work, or, on a machine without a GPU, fails the device check)."""
+    kb = k // 2 if fp4 else k
+    base = [(1 << 44) + (i << 38) for i in range(5)]
+    return qgemm.Kargs(base[0], base[1], base[2], m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
+                       base[3], base[4], k // 32, k // 32, m * (k // 32), n * (k // 32))
+
+
+# one shape per route: wide (panel copy), 128 x 128 split-K, decode split-K,
+# row-streaming split-K
+WS_ROUTES = [("gemm_a8w8_mxfp8", 8192, 8192, 8192, False), ("gemm_a8w8_mxfp8", 128, 7168, 16384, False),
+             ("gemm_a8w8_mxfp8", 32, 1536, 7168, False), ("gemm_a8w8_mxfp8", 4, 7168, 32768, False),
+             ("gemm_a4w4_mxfp4", 8192, 8192, 8192, True), ("gemm_a4w4_mxfp4", 128, 7168, 16384, True),
+             ("gemm_a4w4_mxfp4", 4, 7168, 65536, True)]
+
+
+@pytest.mark.parametrize("name,m,n,k,fp4", WS_ROUTES)
+def test_workspace_rule_is_uniform(qgemm, name, m, n, k, fp4):
+    """Every route applies one rule before launching: a non-NULL workspace
+    smaller than the query, misaligned, or overlapping C or an input is
+    rejected with hipErrorInvalidValue."""
+    L = qgemm.lib()
+    a = _far_kargs(qgemm, m, n, k, fp4)
+    need = getattr(L, name + "_workspace_bytes")(ctypes.byref(a))
+    assert need > 0, (name, m, n, k)
+    ws = (1 << 44) + (7 << 38)
+    fn = getattr(L, name)
+    assert fn(ctypes.byref(a), 1, ws, need - 1, None) == HIP_INVALID_VALUE         # too small
+    assert fn(ctypes.byref(a), 1, ws + 16, need, None) == HIP_INVALID_VALUE        # not 256-byte aligned
+    assert fn(ctypes.byref(a), 1, a.ptr_c, need, None) == HIP_INVALID_VALUE        # overlaps C
+    assert fn(ctypes.byref(a), 1, a.ptr_b, need, None) == HIP_INVALID_VALUE        # overlaps B
+    if not torch.cuda.is_available():
+        # a conforming workspace passes validation and stops at the device check
+        assert fn(ctypes.byref(a), 1, ws, need, None) != HIP_INVALID_VALUE
+
+
+def test_blockscale_workspace_rule(qgemm):
+    L = qgemm.lib()
+    m, n, k = 32, 1536, 7168
+    base = [(1 << 44) + (i << 38) for i in range(5)]
+    a = qgemm.Kargs(base[0], base[1], base[2], m, n, k, 1, k, 128, n, m * k, n * k, m * n, base[3], base[4],
+                    1, k // 128, m * (k // 128), (n // 128) * (k // 128))
+    need = L.gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(ctypes.byref(a))
+    assert need > 0
+    ws = (1 << 44) + (7 << 38)
+    assert L.gemm_a8w8_blockscale_bpreshuffle(ctypes.byref(a), 1, ws, need - 4, None) == HIP_INVALID_VALUE
+    assert L.gemm_a8w8_blockscale_bpreshuffle(ctypes.byref(a), 1, a.ptr_a, need, None) == HIP_INVALID_VALUE
+
+
+def test_misaligned_output_rejected(qgemm):
+    """C must be aligned to its element size; wider vector stores are chosen
+    from the actual alignment of ptr_c, the row pitch and the batch stride."""
+    L = qgemm.lib()
+    a = _far_kargs(qgemm, 32, 256, 512)
+    a.ptr_c += 1
+    assert L.gemm_a8w8_mxfp8(ctypes.byref(a), 1, None, 0, None) == HIP_INVALID_VALUE
+    a.ptr_c += 1                                            # 2-byte aligned: fine for bf16, not fp32
+    assert L.gemm_a8w8_mxfp8(ctypes.byref(a), 0, None, 0, None) == HIP_INVALID_VALUE
+    if not torch.cuda.is_available():
+        assert L.gemm_a8w8_mxfp8(ctypes.byref(a), 1, None, 0, None) != HIP_INVALID_VALUE
+
+
+def test_last_launch_empty_after_rejection(qgemm):
+    L = qgemm.lib()
+    assert L.gemm_a8w8_mxfp8(None, 1, None, 0, None) == HIP_INVALID_VALUE
+    assert qgemm.last_launch() == ""
+
+
+def test_e8m0_adapter_rejects_before_launch(qgemm):
+    f = qgemm.blockscale_bpreshuffle.gemm_a8w8_blockscale_bpreshuffle
+    x = torch.zeros(256, 256, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="2-D"):
+        f(x[0], x, x, x)
+    with pytest.raises(ValueError, match="GPU"):
+        f(x.view(torch.float8_e4m3fn), x, x[:, :2], x[:2, :2])

@@ -147,6 +147,61 @@ def test_blockscale_e8m0(qgemm, gpu, m, n, k, dtype):
     assert_close(ref, out_to_f32(y), f"bs-e8m0 {m}x{n}x{k}")
 
 
+def test_blockscale_e8m0_batch2_c_abi(qgemm, gpu):
+    """The drop-in launcher at batch 2, as the reference's own `make verify`
+    runs it (SNAP Makefile:51): dense batch strides, per-batch scales."""
+    m, n, k, batch = 512, 256, 1152, 2
+    data = [_snap_inputs(m, n, k, seed=90 + i) for i in range(batch)]
+    A = torch.stack([torch.from_numpy(d[0]) for d in data]).to(gpu)
+    B = torch.stack([torch.from_numpy(O.shuffle_weight_16x16(d[1])) for d in data]).to(gpu)
+    SA = torch.stack([torch.from_numpy(d[2]) for d in data]).to(gpu)           # [b][K/128][M]
+    SB = torch.stack([torch.from_numpy(d[3]) for d in data]).to(gpu)
+    kg = k // 128
+    for out_code, odt in ((1, torch.bfloat16), (0, torch.float32)):
+        C = torch.empty(batch, m, n, dtype=odt, device=gpu)
+        args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, k, k, n, m * k, n * k, m * n,
+                           SA.data_ptr(), SB.data_ptr(), m, kg, m * kg, (n // 128) * kg)
+        st = qgemm.lib().launch_blockscale_bpreshuffle(ctypes.byref(args), out_code, 0,
+                                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert st == 0
+        torch.cuda.synchronize()
+        for i, d in enumerate(data):
+            assert_close(O.gemm_bs_e8m0(*d), C[i].float().cpu().numpy(), f"bs-e8m0 batch {i} out={out_code}")
+
+
+def test_blockscale_e8m0_adapter_contract(qgemm, gpu):
+    """The Python adapter raises ValueError where the launcher's contract is
+    broken (SNAP blockscale_bpreshuffle.py:37-97 behaviour), before launching."""
+    f = qgemm.blockscale_bpreshuffle.gemm_a8w8_blockscale_bpreshuffle
+    m, n, k = 256, 256, 256
+    A = torch.zeros(m, k, dtype=torch.uint8, device=gpu).view(torch.float8_e4m3fn)
+    B = torch.zeros(n, k, dtype=torch.uint8, device=gpu)
+    sa = torch.full((k // 128, m), 127, dtype=torch.uint8, device=gpu).t()
+    sb = torch.full((n // 128, k // 128), 127, dtype=torch.uint8, device=gpu)
+    assert torch.count_nonzero(f(A, B, sa, sb).float()) == 0
+    bad = [
+        dict(A=A[:, :128].contiguous()),                                # K mismatch
+        dict(A=torch.zeros(128, k, dtype=torch.uint8, device=gpu).view(torch.float8_e4m3fn)),   # M % 256
+        dict(A_scale=torch.ones(m, k // 128, dtype=torch.float32, device=gpu)),                  # fp32 scales
+        dict(A_scale=torch.full((m, 4), 127, dtype=torch.uint8, device=gpu)[:, :2]),             # strided scales
+        dict(B_scale=sb[:1]),                                            # wrong scale shape
+        dict(dtype=torch.float16),
+        dict(tiles=2),
+        dict(A=A.view(torch.uint8)),                                     # A not e4m3
+    ]
+    for change in bad:
+        kw = dict(A=A, B=B, A_scale=sa, B_scale=sb)
+        kw.update(change)
+        with pytest.raises(ValueError):
+            f(**kw)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        f(A, B, sa, sb, out=out.view(torch.float32))                    # wrong out dtype
+    alias = torch.empty(m * n * 2, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError):                                     # out overlapping B
+        f(A, alias[:n * k].view(n, k), sa, sb, out=alias.view(torch.bfloat16).view(m, n))
+
+
 # ----------------------------------------------- block-scale, fp32 scales
 BS_SHAPES = [(32, 1536, 7168), (256, 256, 128), (300, 520, 384), (1, 2112, 7168), (16, 4096, 1024),
              (600, 384, 256), (512, 768, 1024)]
@@ -185,7 +240,8 @@ def test_blockscale_fp32_tile(qgemm, gpu, m, n, k, dtype):
 
 # ------------------------------------- wide MX kernels: scale-panel copy
 @pytest.mark.parametrize("fp4,k", [(False, 2048), (True, 2048), (True, 1536), (False, 1536)])
-def test_mx_wide_scale_panels(qgemm, gpu, fp4, k):
+@pytest.mark.parametrize("out_code", [0, 1])
+def test_mx_wide_scale_panels(qgemm, gpu, fp4, k, out_code):
     """Batched wide-kernel call through the C ABI with the queried workspace
     (E8M0 scales copied panel-major first: 32-byte panels for fp4 with
     K % 1024 == 0, else 16-byte) against the oracle, and bit-equal to the
@@ -208,19 +264,28 @@ def test_mx_wide_scale_panels(qgemm, gpu, fp4, k):
     name = "gemm_a4w4_mxfp4" if fp4 else "gemm_a8w8_mxfp8"
     L = qgemm.lib()
     outs = []
+    pb = 32 if fp4 and k % 1024 == 0 else 16
+    odt, otag = (torch.float32, "fp32") if out_code == 0 else (torch.bfloat16, "bf16")
     for use_ws in (True, False):
-        C = torch.empty(batch, m, n, dtype=torch.float32, device=gpu)
+        C = torch.empty(batch, m, n, dtype=odt, device=gpu)
         args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, kb, kb, n, m * kb, n * kb,
                            m * n, SA.data_ptr(), SB.data_ptr(), lsa, lsb, m * lsa, n * lsb)
         need = getattr(L, name + "_workspace_bytes")(ctypes.byref(args))
         ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=gpu)
         if use_ws:
             assert need >= batch * (m + n) * kg, "query must cover the scale panels"
-        st = getattr(L, name)(ctypes.byref(args), qgemm.OUT_FP32, ws.data_ptr() if use_ws else None,
+        st = getattr(L, name)(ctypes.byref(args), out_code, ws.data_ptr() if use_ws else None,
                               need if use_ws else 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         assert st == 0, f"{name} returned {st}"
+        # the instantiations bench.py times at 8192^3 (bf16, 16-byte fp8 /
+        # 32-byte fp4 panels after the copy) and their no-workspace twins
+        fmt = "fp4" if fp4 else "fp8"
+        # (without a workspace the same panel width reads the row-major scales)
+        want = (f"mx_scale_panels<pb{pb}>+wide_gemm<{fmt},MX,RAW,{otag},pb{pb}>" if use_ws
+                else f"wide_gemm<{fmt},MX,RAW,{otag},pb{pb}>")
+        assert qgemm.last_launch() == want
         torch.cuda.synchronize()
-        outs.append(C.cpu())
+        outs.append(C.float().cpu())
     gemm = O.gemm_mx4 if fp4 else O.gemm_mx8
     for i, d in enumerate(data):
         assert_close(gemm(*d), outs[0][i].numpy(), f"batch {i}")

@@ -73,8 +73,11 @@ def test_splitk_rearms_workspace(qgemm, gpu):
 
 # ----------------------------------------------------------------- MXFP4
 # (16, 24576, 3072), (40, 16384, 2048): short K with >= 256 skinny tiles -> decode kernel
+# (32, 7168, 16384), (64, 7168, 16384): configs[4] as benched (skinny MB2/NB2
+# and MB4/NB2 with per-wave scale panels and nontemporal B)
 MX4_DECODE = [(1, 2112, 7168), (4, 1000, 2048), (16, 4096, 512), (31, 512, 4096), (64, 7168, 1024),
-              (200, 768, 1536), (8, 7168, 16384), (32, 2048, 16384), (16, 24576, 3072), (40, 16384, 2048)]
+              (200, 768, 1536), (8, 7168, 16384), (32, 2048, 16384), (16, 24576, 3072), (40, 16384, 2048),
+              (32, 7168, 16384), (64, 7168, 16384), (128, 7168, 16384)]
 
 
 @pytest.mark.parametrize("m,n,k", MX4_DECODE)
@@ -129,19 +132,22 @@ def test_ldsbypass_repack_matches_host_pack(qgemm, gpu):
         assert torch.equal(host, dev.cpu()), f"repack != host pack for N={n} K={k}"
 
 
+# (32, 1536, 7168): configs[0] as the ldsbypass_c0 bench workload runs it
 LBP_SHAPES = [(1, 2112, 7168), (16, 1536, 1024), (37, 100, 512), (64, 7168, 1024), (256, 512, 768),
-              (300, 520, 384), (600, 384, 256)]
+              (300, 520, 384), (600, 384, 256), (32, 1536, 7168), (24, 1536, 7168)]
 
 
 @pytest.mark.parametrize("m,n,k", LBP_SHAPES)
 @pytest.mark.parametrize("sfa_layout", ["mk", "km"])
-def test_ldsbypass(qgemm, gpu, m, n, k, sfa_layout):
+@pytest.mark.parametrize("split", [True, False])
+def test_ldsbypass(qgemm, gpu, m, n, k, sfa_layout, split):
     qa, qb, sa, sb = make_bs(m, n, k, seed=m + 3 * n + k)
     ref = O.gemm_bs_fp32(qa, qb, sa, sb)
     Bpp = qgemm.ldsbypass_repack(qgemm.shuffle_b_kpanel(to_dev(qb, None, gpu)))
     A_scale = to_dev(sa, None, gpu) if sfa_layout == "mk" else to_dev(np.ascontiguousarray(sa.T), None, gpu).t()
-    y = qgemm.gemm_a8w8_ldsbypass(_fp8(qa, gpu), Bpp, A_scale, to_dev(sb, None, gpu), n, dtype=torch.bfloat16)
-    assert_close(ref, out_to_f32(y), f"ldsbypass {m}x{n}x{k} {sfa_layout}")
+    y = qgemm.gemm_a8w8_ldsbypass(_fp8(qa, gpu), Bpp, A_scale, to_dev(sb, None, gpu), n, dtype=torch.bfloat16,
+                                  workspace=None if split else False)
+    assert_close(ref, out_to_f32(y), f"ldsbypass {m}x{n}x{k} {sfa_layout} split={split}")
 
 
 # tile-kernel cases of the LDS-bypass entry (M > 256: B'' blocks staged

@@ -148,6 +148,29 @@ def test_mx_exponent_is_minimal_power_of_two(kind, qmax):
     assert np.all(amax[nz] / (p[nz] / 2) > qmax)                 # and one step less would not
 
 
+def test_quant_bs_e8m0_minimal_power_of_two_blocks():
+    """E8M0 block scales: 1x128 activation and 128x128 weight blocks, the
+    minimal power of two that fits amax into e4m3 (448), top code reached."""
+    x = O.randn((4, 384), seed=14) * np.float32(np.logspace(-2, 2, 4))[:, None]
+    x[1, 128:256] = 0.0
+    q, e = O.quant_bs_e8m0_act(x)
+    assert e.shape == (4, 3) and e[1, 1] == 127
+    amax = np.abs(x.reshape(4, 3, 128)).max(-1)
+    p = np.ldexp(1.0, e.astype(np.int64) - 127)
+    nz = amax > 0
+    assert np.all(amax[nz] / p[nz] <= 448.0) and np.all(amax[nz] / (p[nz] / 2) > 448.0)
+    deq = O.e4m3_decode(q) * np.repeat(p, 128, 1)
+    assert _e4m3_err_ok(x, deq, np.repeat(p, 128, 1))
+    w = O.randn((200, 256), seed=15)
+    w[128:, :128] *= 64.0
+    qw, ew = O.quant_bs_e8m0_wgt(w)
+    assert ew.shape == (2, 2)
+    blk = np.abs(w[:128, :128]).max(), np.abs(w[128:, :128]).max()
+    assert ew[1, 0] - ew[0, 0] == int(np.ceil(np.log2(blk[1] / 448))) - int(np.ceil(np.log2(blk[0] / 448)))
+    pw = np.repeat(np.repeat(np.ldexp(1.0, ew.astype(np.int64) - 127), 128, 0), 128, 1)[:200]
+    assert _e4m3_err_ok(w, O.e4m3_decode(qw) * pw, pw)
+
+
 def test_mx4_packing_and_rounding():
     x = np.zeros((1, 64), np.float32)
     x[0, :4] = [1.0, 2.0, -0.5, 6.0]
@@ -216,6 +239,38 @@ def test_gemm_mx4_exact_small_k():
     B = _dec4(qb) * np.repeat(np.ldexp(1.0, eb.astype(np.int64) - 127), 32, 1)
     # every product and partial sum is exact in fp32 at this K
     assert np.array_equal(O.gemm_mx4(qa, qb, ea, eb).astype(np.float64), A @ B.T)
+    assert np.array_equal(O.gemm_mx4(qa, qb, ea, eb, literal=True).astype(np.float64), A @ B.T)
+
+
+@pytest.mark.parametrize("data", ["recipe", "random_bytes", "k_pattern", "scale_spread"])
+def test_gemm_mx4_grouped_equals_literal(data):
+    """The grouped gemm_ref_gpu form (MX4 host.cc:66-94) that the tests use
+    for speed is bit-identical to the literal gemm_ref_cpu loop (MX4
+    host.cc:96-115): BASELINE-recipe data, the reference's own random fp4
+    bytes with scales in [124, 130] (MX4 host.cc:46-54, 178-180), per-K-group
+    scale patterns and a wider scale spread; and the sampled-point entry
+    equals the full grid."""
+    m, n, k = 5, 96, 4096
+    rng = np.random.default_rng(21)
+    if data == "recipe":
+        qa, ea = O.quant_mx4(O.randn((m, k), 21, 0))
+        qb, eb = O.quant_mx4(O.randn((n, k), 21, 1))
+    else:
+        qa = rng.integers(0, 256, (m, k // 2), dtype=np.uint8)
+        qb = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+        lo, hi = (124, 131) if data != "scale_spread" else (112, 143)
+        ea = rng.integers(lo, hi, (m, k // 32)).astype(np.uint8)
+        eb = rng.integers(lo, hi, (n, k // 32)).astype(np.uint8)
+        if data == "k_pattern":
+            ea = np.broadcast_to((120 + np.arange(k // 32) % 13).astype(np.uint8), ea.shape).copy()
+    grouped = O.gemm_mx4(qa, qb, ea, eb)
+    literal = O.gemm_mx4(qa, qb, ea, eb, literal=True)
+    assert np.array_equal(grouped, literal)
+    A = _dec4(qa) * np.repeat(np.ldexp(1.0, ea.astype(np.int64) - 127), 32, 1)
+    B = _dec4(qb) * np.repeat(np.ldexp(1.0, eb.astype(np.int64) - 127), 32, 1)
+    assert np.all(np.abs(grouped - A @ B.T) <= 2.0 ** -24 * np.abs(A @ B.T) + 1e-30)
+    rows, cols = rng.integers(0, m, 200).astype(np.int32), rng.integers(0, n, 200).astype(np.int32)
+    assert np.array_equal(O.gemm_mx4_points(qa, qb, ea, eb, rows, cols), grouped[rows, cols])
 
 
 def test_gemm_mx4_k_group_pattern():
@@ -240,6 +295,8 @@ def test_gemm_bs_e8m0_vs_fp64():
     B = _dec8(b) * np.repeat(np.repeat(np.ldexp(1.0, sfb.astype(np.int64) - 127), 128, 0), 128, 1)
     got = O.gemm_bs_e8m0(a, b, sfa_km, sfb)
     assert np.all(np.abs(got - A @ B.T) <= 1e-6 * (np.abs(A) @ np.abs(B).T) + 1e-30)
+    rows, cols = rng.integers(0, m, 300).astype(np.int32), rng.integers(0, n, 300).astype(np.int32)
+    assert np.array_equal(O.gemm_bs_e8m0_points(a, b, sfa_km, sfb, rows, cols), got[rows, cols])
 
 
 # ----------------------------------------------------------------- tolerance checker
