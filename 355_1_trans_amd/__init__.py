@@ -69,6 +69,8 @@ class LdsBypassKargs(ctypes.Structure):
 assert ctypes.sizeof(Kargs) == 96
 
 
+_V, _I = ctypes.c_void_p, ctypes.c_int
+
 EXPORTS = {
     # name: (restype, argtypes)
     "launch_blockscale_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
@@ -93,6 +95,16 @@ EXPORTS = {
     "qgemm_e8m0_shuffle": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]),
     "qgemm_probe_words": (ctypes.c_int, []),
     "qgemm_probe_mfma_layout": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "qgemm_quant_fp8_blockscale_act": (ctypes.c_int, [_V, _I, _I, _I, _I, _V, _I, _V, _I, _I, _V]),
+    "qgemm_quant_fp8_blockscale_wgt": (ctypes.c_int, [_V, _I, _I, _I, _I, _V, _I, _V, _I, _V]),
+    "qgemm_quant_fp8_e8m0_act": (ctypes.c_int, [_V, _I, _I, _I, _I, _V, _I, _V, _I, _I, _V]),
+    "qgemm_quant_fp8_e8m0_wgt": (ctypes.c_int, [_V, _I, _I, _I, _I, _V, _I, _V, _I, _V]),
+    "qgemm_quant_mxfp8": (ctypes.c_int, [_V, _I, _I, _I, _I, _V, _I, _V, _I, _I, _V]),
+    "qgemm_quant_mxfp4": (ctypes.c_int, [_V, _I, _I, _I, _I, _V, _I, _V, _I, _I, _V]),
+    "qgemm_shuffle_b_kpanel_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
+    "qgemm_shuffle_weight_16x16_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
+    "qgemm_pack_b_ldsbypass_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
+    "qgemm_e8m0_shuffle_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
     "qgemm_version": (ctypes.c_char_p, []),
     "qgemm_last_launch": (ctypes.c_char_p, []),
 }
@@ -291,13 +303,19 @@ def ldsbypass_b_bytes(n, k):
 
 
 def ldsbypass_pack_b(B):
-    """Host pack of B'' from raw B [N, K] (CPU tensor, 1-byte elements)."""
-    if B.is_cuda or B.dim() != 2 or B.element_size() != 1 or not B.is_contiguous():
-        raise ValueError("B must be a contiguous CPU [N, K] tensor of 1-byte elements")
+    """B'' from raw B [N, K] (1-byte elements): on the GPU for a GPU tensor
+    (qgemm_pack_b_ldsbypass_device), else the host pack."""
+    if B.dim() != 2 or B.element_size() != 1:
+        raise ValueError("B must be a 2-D [N, K] tensor of 1-byte elements")
     n, k = B.shape
     nbytes = ldsbypass_b_bytes(n, k)
     if nbytes == 0:
         raise ValueError("requires N >= 1 and K % 128 == 0")
+    if B.is_cuda:
+        from .quant import relayout_device
+        return relayout_device("qgemm_pack_b_ldsbypass_device", _u8(B), nbytes)
+    if not B.is_contiguous():
+        raise ValueError("a host B must be contiguous")
     out = torch.empty(nbytes, dtype=torch.uint8)
     _check(lib().qgemm_pack_b_ldsbypass(B.data_ptr(), out.data_ptr(), n, k), "qgemm_pack_b_ldsbypass")
     return out
@@ -365,19 +383,30 @@ def probe_mfma_layout(device=None):
 
 # ------------------------------------------------------------------ layouts
 def shuffle_b_kpanel(B):
-    """K-panel pre-shuffle (BPS host.cc:92-111): [N, K] -> [K/128, N, 128]."""
+    """K-panel pre-shuffle (BPS host.cc:92-111): [N, K] -> [K/128, N, 128].
+    A GPU tensor is shuffled by qgemm_shuffle_b_kpanel_device."""
     n, k = B.shape
     if k % 128:
         raise ValueError("K must be a multiple of 128")
+    if B.is_cuda:
+        from .quant import relayout_device
+        return relayout_device("qgemm_shuffle_b_kpanel_device", _u8(B), n * k).view(B.dtype).view(k // 128, n, 128)
     return B.reshape(n, k // 128, 128).permute(1, 0, 2).contiguous()
 
 
 def shuffle_weight_16x16(B):
-    """shuffle_weight(layout=(16,16)) over bytes: [N, Kb] -> [N/16, Kb/16, 16, 16] (SNAP host.cc:161-179)."""
+    """shuffle_weight(layout=(16,16)) over bytes: [N, Kb] -> [N/16, Kb/16, 16, 16]
+    (SNAP host.cc:161-179), returned as [N, Kb].  A GPU tensor is shuffled
+    by qgemm_shuffle_weight_16x16_device."""
     n, kb = B.shape
     if n % 16 or kb % 16:
         raise ValueError("N and K bytes must be multiples of 16")
+    if B.is_cuda:
+        from .quant import relayout_device
+        return relayout_device("qgemm_shuffle_weight_16x16_device", _u8(B), n * kb).view(B.dtype).view(n, kb)
     return B.reshape(n // 16, 16, kb // 16, 16).permute(0, 2, 1, 3).contiguous().reshape(n, kb)
 
 
 from . import blockscale_bpreshuffle  # noqa: E402  (reference adapter mirror)
+from .quant import (e8m0_shuffle, quant_fp8_blockscale, quant_fp8_e8m0_blockscale,  # noqa: E402,F401
+                    quant_mxfp4, quant_mxfp8)

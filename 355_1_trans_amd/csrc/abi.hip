@@ -979,6 +979,154 @@ int qgemm_pack_b_ldsbypass(const uint8_t* b_raw, uint8_t* b_pp, int n, int k) {
     return 0;
 }
 
+// ---------------------------------------------------------------- quantizers
+}  // extern "C"
+
+namespace {
+
+// Source of a quantizer: fp32 or bf16 rows of at least k elements, pitch a
+// multiple of 4 elements and the base aligned for 4-element vector loads.
+bool quant_src_ok(const void* x, int in_dtype, int rows, int k, int ldx, int k_align) {
+    if (!x || !flag01(in_dtype) || rows <= 0 || k <= 0 || k % k_align || ldx < k || ldx % 4) return false;
+    return aligned(x, in_dtype ? 8 : 16);
+}
+
+uint64_t src_bytes(int rows, int ldx, int k, int in_dtype) {
+    return ((uint64_t)(rows - 1) * ldx + k) * (in_dtype ? 2 : 4);
+}
+
+}  // namespace
+
+extern "C" {
+
+hipError_t qgemm_quant_fp8_blockscale_act(const void* x, int in_dtype, int m, int k, int ldx, uint8_t* q, int ldq,
+                                          float* scale, int scale_sm, int scale_sk, hipStream_t stream) {
+    qg::trace_reset();
+    if (!quant_src_ok(x, in_dtype, m, k, ldx, 128) || !q || !scale || ldq < k || ldq % 4 || !aligned(q, 4) ||
+        !aligned(scale, 4))
+        return hipErrorInvalidValue;
+    const int kg = k / 128;
+    // scale(m, g) = scale[m*sm + g*sk]: row-major [M][K/128] or column-major [K/128][M]
+    if (!((scale_sk == 1 && scale_sm >= kg) || (scale_sm == 1 && scale_sk >= m))) return hipErrorInvalidValue;
+    const uint64_t xb = src_bytes(m, ldx, k, in_dtype), qb = (uint64_t)(m - 1) * ldq + k;
+    const uint64_t sb = ((uint64_t)(m - 1) * scale_sm + (uint64_t)(kg - 1) * scale_sk + 1) * 4;
+    if (overlaps(x, xb, q, qb) || overlaps(x, xb, scale, sb) || overlaps(q, qb, scale, sb)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_quant_rows(0, 128, in_dtype == 1, false, x, ldx, q, ldq, scale, scale_sm, scale_sk, m, k, stream);
+}
+
+hipError_t qgemm_quant_fp8_blockscale_wgt(const void* w, int in_dtype, int n, int k, int ldw, uint8_t* q, int ldq,
+                                          float* scale, int ld_scale, hipStream_t stream) {
+    qg::trace_reset();
+    if (!quant_src_ok(w, in_dtype, n, k, ldw, 128) || !q || !scale || ldq < k || ldq % 4 || !aligned(q, 4) ||
+        !aligned(scale, 4) || ld_scale < k / 128)
+        return hipErrorInvalidValue;
+    const uint64_t xb = src_bytes(n, ldw, k, in_dtype), qb = (uint64_t)(n - 1) * ldq + k;
+    const uint64_t sb = ((uint64_t)(ceil_div(n, 128) - 1) * ld_scale + k / 128) * 4;
+    if (overlaps(w, xb, q, qb) || overlaps(w, xb, scale, sb) || overlaps(q, qb, scale, sb)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_quant_wgt_blocks(0, in_dtype == 1, w, ldw, q, ldq, scale, ld_scale, n, k, stream);
+}
+
+hipError_t qgemm_quant_fp8_e8m0_act(const void* x, int in_dtype, int m, int k, int ldx, uint8_t* q, int ldq,
+                                    uint8_t* e, int e_sm, int e_sk, hipStream_t stream) {
+    qg::trace_reset();
+    if (!quant_src_ok(x, in_dtype, m, k, ldx, 128) || !q || !e || ldq < k || ldq % 4 || !aligned(q, 4))
+        return hipErrorInvalidValue;
+    const int kg = k / 128;
+    if (!((e_sk == 1 && e_sm >= kg) || (e_sm == 1 && e_sk >= m))) return hipErrorInvalidValue;
+    const uint64_t xb = src_bytes(m, ldx, k, in_dtype), qb = (uint64_t)(m - 1) * ldq + k;
+    const uint64_t eb = (uint64_t)(m - 1) * e_sm + (uint64_t)(kg - 1) * e_sk + 1;
+    if (overlaps(x, xb, q, qb) || overlaps(x, xb, e, eb) || overlaps(q, qb, e, eb)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_quant_rows(1, 128, in_dtype == 1, false, x, ldx, q, ldq, e, e_sm, e_sk, m, k, stream);
+}
+
+hipError_t qgemm_quant_fp8_e8m0_wgt(const void* w, int in_dtype, int n, int k, int ldw, uint8_t* q, int ldq,
+                                    uint8_t* e, int ld_e, hipStream_t stream) {
+    qg::trace_reset();
+    if (!quant_src_ok(w, in_dtype, n, k, ldw, 128) || !q || !e || ldq < k || ldq % 4 || !aligned(q, 4) ||
+        ld_e < k / 128)
+        return hipErrorInvalidValue;
+    const uint64_t xb = src_bytes(n, ldw, k, in_dtype), qb = (uint64_t)(n - 1) * ldq + k;
+    const uint64_t eb = (uint64_t)(ceil_div(n, 128) - 1) * ld_e + k / 128;
+    if (overlaps(w, xb, q, qb) || overlaps(w, xb, e, eb) || overlaps(q, qb, e, eb)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_quant_wgt_blocks(1, in_dtype == 1, w, ldw, q, ldq, e, ld_e, n, k, stream);
+}
+
+// MXFP8 / MXFP4 share the checks; fp4 packs two codes per byte
+static hipError_t quant_mx(bool fp4, const void* x, int in_dtype, int rows, int k, int ldx, uint8_t* q, int ldq,
+                           uint8_t* e, int lde, int shuffle, hipStream_t stream) {
+    qg::trace_reset();
+    const int qrow = fp4 ? k / 2 : k;
+    if (!quant_src_ok(x, in_dtype, rows, k, ldx, 32) || !q || !e || !flag01(shuffle) || ldq < qrow ||
+        ldq % (fp4 ? 2 : 4) || !aligned(q, fp4 ? 2 : 4) || (!shuffle && lde < k / 32))
+        return hipErrorInvalidValue;
+    const uint64_t xb = src_bytes(rows, ldx, k, in_dtype), qb = (uint64_t)(rows - 1) * ldq + qrow;
+    const uint64_t eb = shuffle ? qgemm_e8m0_shuffle_bytes(rows, k / 32) : (uint64_t)(rows - 1) * lde + k / 32;
+    if (overlaps(x, xb, q, qb) || overlaps(x, xb, e, eb) || overlaps(q, qb, e, eb)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_quant_rows(fp4 ? 2 : 1, 32, in_dtype == 1, shuffle == 1, x, ldx, q, ldq, e, lde, 1, rows, k,
+                                 stream);
+}
+
+hipError_t qgemm_quant_mxfp8(const void* x, int in_dtype, int rows, int k, int ldx, uint8_t* q, int ldq, uint8_t* e,
+                             int lde, int shuffle, hipStream_t stream) {
+    return quant_mx(false, x, in_dtype, rows, k, ldx, q, ldq, e, lde, shuffle, stream);
+}
+
+hipError_t qgemm_quant_mxfp4(const void* x, int in_dtype, int rows, int k, int ldx, uint8_t* q, int ldq, uint8_t* e,
+                             int lde, int shuffle, hipStream_t stream) {
+    return quant_mx(true, x, in_dtype, rows, k, ldx, q, ldq, e, lde, shuffle, stream);
+}
+
+// ---------------------------------------------------------------- device layouts
+static hipError_t relayout(int layout, const uint8_t* src, uint8_t* dst, int n, int k_bytes, int ld_src,
+                           int k_align, hipStream_t stream) {
+    qg::trace_reset();
+    if (!src || !dst || n <= 0 || k_bytes <= 0 || k_bytes % k_align || ld_src < k_bytes || ld_src % 16 ||
+        !aligned(src, 16) || !aligned(dst, 16) || (layout == 1 && n % 16))
+        return hipErrorInvalidValue;
+    const uint64_t sb = (uint64_t)(n - 1) * ld_src + k_bytes;
+    const uint64_t db = layout == 2 ? frag_bytes(n, k_bytes) : (uint64_t)n * k_bytes;
+    if (overlaps(src, sb, dst, db)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_relayout(layout, src, dst, n, k_bytes, ld_src, stream);
+}
+
+hipError_t qgemm_shuffle_b_kpanel_device(const uint8_t* src, uint8_t* dst, int n, int k_bytes, int ld_src,
+                                         hipStream_t stream) {
+    return relayout(0, src, dst, n, k_bytes, ld_src, 128, stream);
+}
+
+hipError_t qgemm_shuffle_weight_16x16_device(const uint8_t* src, uint8_t* dst, int n, int k_bytes, int ld_src,
+                                             hipStream_t stream) {
+    return relayout(1, src, dst, n, k_bytes, ld_src, 16, stream);
+}
+
+hipError_t qgemm_pack_b_ldsbypass_device(const uint8_t* b_raw, uint8_t* b_pp, int n, int k, int ld_src,
+                                         hipStream_t stream) {
+    return relayout(2, b_raw, b_pp, n, k, ld_src, 128, stream);
+}
+
+hipError_t qgemm_e8m0_shuffle_device(const uint8_t* src, uint8_t* dst, int rows, int groups_k, int ld_src,
+                                     hipStream_t stream) {
+    qg::trace_reset();
+    if (!src || !dst || rows <= 0 || groups_k <= 0 || ld_src < groups_k) return hipErrorInvalidValue;
+    if (overlaps(src, (uint64_t)(rows - 1) * ld_src + groups_k, dst, qgemm_e8m0_shuffle_bytes(rows, groups_k)))
+        return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_e8m0_shuffle(src, dst, rows, groups_k, ld_src, stream);
+}
+
 // ---------------------------------------------------------------- probe
 int qgemm_probe_words(void) { return qg::kProbeWords; }
 

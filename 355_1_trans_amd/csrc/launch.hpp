@@ -56,6 +56,21 @@ hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batc
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);
 
+// quant.hip: device-side quantizers and weight layouts.
+// fmt 0: e4m3 + fp32 scale amax/448; 1: e4m3 + E8M0; 2: e2m1 + E8M0.
+// group: 128 (1x128 blocks) or 32 (MX); scale(r, g) = s[r*s_sm + g*s_sk]
+// unless shuffle (e8m0_shuffle order).
+hipError_t launch_quant_rows(int fmt, int group, bool bf16in, bool shuffle, const void* x, long long ldx,
+                             uint8_t* q, long long ldq, void* s, long long s_sm, long long s_sk, int rows, int k,
+                             hipStream_t st);
+// 128 x 128 weight blocks; scale(nb, g) = s[nb*ld_s + g]; fmt 0 or 1
+hipError_t launch_quant_wgt_blocks(int fmt, bool bf16in, const void* w, long long ldw, uint8_t* q, long long ldq,
+                                   void* s, long long ld_s, int n, int k, hipStream_t st);
+// layout 0: K-panel, 1: shuffle_weight(16,16), 2: B'' (ldsbypass fragment order)
+hipError_t launch_relayout(int layout, const uint8_t* src, uint8_t* dst, int n, int kbytes, long long ld,
+                           hipStream_t st);
+hipError_t launch_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int kg, long long ld, hipStream_t st);
+
 // probe.hip
 hipError_t launch_probe(int32_t* dev_out, hipStream_t s);
 constexpr int kProbeWords = 8264;

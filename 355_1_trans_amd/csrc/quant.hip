@@ -78,7 +78,9 @@ __device__ __forceinline__ int ceil_log2(float v) {
 // clamped to the E8M0 range; 0 (code 127) for an all-zero group.
 __device__ __forceinline__ int mx_exp(float amax, float qmax) {
     if (!(amax > 0.0f)) return 0;
-    const int e = ceil_log2(amax / qmax);                 // IEEE division
+    const float v = amax / qmax;                          // IEEE division
+    if (v == 0.0f) return -127;                           // the quotient underflows: the clamp
+    const int e = ceil_log2(v);
     return e < -127 ? -127 : (e > 127 ? 127 : e);
 }
 

@@ -2,27 +2,38 @@
 
 Default workload (the configuration the headline
 metric is quoted on): MXFP8 TN GEMM, M = N = K = 8192, e4m3 operands with one
-E8M0 scale per 32 K elements, bf16 output.  A "step" is one GEMM launch on
-synthetic N(0,1) data (seed 0) quantized per the BASELINE recipe; inputs are
-resident in HBM before the timed region.  Other workloads (--workload) cover
-configs[0] (block-scale FP8 decode, both B layouts), configs[3] (MXFP4
-8192^3) and configs[4] (MXFP4 decode).
+E8M0 scale per 32 K elements, bf16 output.  A "step" is one GEMM launch.
+Other workloads (--workload) cover configs[0] (block-scale FP8 decode, both
+B layouts), configs[2] (--sweep), configs[3] (MXFP4 8192^3), configs[4]
+(MXFP4 decode, --m) and the device quantizers.
 
-Launches go straight through the C ABI with prebuilt argument blocks.  The
-MFMA-bound 8192^3 workloads are timed launch by launch; the HBM-bound decode
-workloads are captured in a HIP graph over rotating copies of the weights
-(more bytes than the 256 MB last-level cache, so B streams from HBM) and the
-replays are timed.  Either way the timing is HIP events on the launch stream.
+Inputs: N(0,1) fp32 drawn on the GPU from a generator seeded with 0 (A) and
+1 (B), quantized on the GPU by this library's quantizers per the BASELINE
+recipe, resident in HBM before the timed region.  Launches go straight
+through the C ABI with prebuilt argument blocks.
 
-Prints ONE JSON line with the metric, a roofline block for the GEMM kernel
-(algorithmic FLOPs or bytes per launch / average launch time) and a
-cpu_baseline block (the CPU oracle's restatement of the reference CPU GEMM,
-timed on a bounded row band on this host).
+Timing: a clock-settle phase of back-to-back launches (>= --settle-s
+seconds; short warm-ups sit in the power controller's downclock window,
+MX4 HANDOVER.md:8), then --warmup launches, then exactly --steps launches
+between HIP events on the launch stream.  MFMA-bound workloads are timed
+launch by launch (an event after every launch gives the spread);
+HBM-bound decode workloads run as one HIP graph over rotating weight copies
+(more bytes than the 256 MB last-level cache, so B streams from HBM).
+
+After timing, 4096 output points are checked against the CPU oracle on the
+same quantized bytes (tolerance |y - y_ref| <= 2^-7|y_ref| + 1e-3 rms);
+a failure exits non-zero.  The oracle is used only for that check and for
+the cpu_baseline leg (its restatement of the reference CPU GEMM, timed on a
+bounded row band on this host).
+
+Prints ONE JSON line with the metric, a roofline block for the dominant
+kernel and the cpu_baseline block.
 """
 import argparse
 import ctypes
 import importlib
 import json
+import os
 import re
 import sys
 import time
@@ -37,6 +48,7 @@ METRIC = "TFLOPS and % of MI355X peak: block-FP8/MXFP8/MXFP4 GEMM at 8192^3 + de
 PEAK_TFLOPS = {"fp8": 5000.0, "fp4": 10100.0}
 HBM_GBPS = 8000.0
 ROTATE_BYTES = 512 << 20
+CHECK_POINTS = 4096
 
 WORKLOADS = {
     # name: (family, M, N, K, BASELINE config index)
@@ -51,17 +63,26 @@ WORKLOADS = {
     "bs_e8m0_8192": ("bs8", 8192, 8192, 8192, None),
 }
 
+NAMES = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
+         "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
+         "bs": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, K-panel B (bpreshuffle)",
+         "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)",
+         "bs8": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, shuffle_weight(16,16) B"}
+
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--settle-s", type=float, default=1.0,
+                   help="seconds of back-to-back launches before the warm-up (clock settle)")
     p.add_argument("--workload", default="mxfp8_8192", choices=sorted(WORKLOADS))
     p.add_argument("--m", type=int, default=None, help="override M (decode sweeps)")
     p.add_argument("--n", type=int, default=None, help="override N")
     p.add_argument("--k", type=int, default=None, help="override K")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-check", action="store_true", help="skip the output check against the oracle")
     p.add_argument("--sfa-km", action="store_true",
                    help="block-scale fp32 workloads: pass A's scales column-major [K/128][M] (the reference's "
                         "layout) instead of BASELINE's row-major [M][K/128]")
@@ -83,80 +104,246 @@ def traffic_from_profiles(kernel_tag):
     return float(m.group(1)) if m else None
 
 
-SWEEP_M = (1, 16, 64, 256, 1024, 4096, 16384)
-SWEEP_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168))
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
-def _gpu_quant_bs(rows, k, block_rows, gen, dev):
-    """N(0,1) data quantized to e4m3 with one fp32 scale (amax / 448) per
-    block_rows x 128 block, on the GPU (the sweep's operands are too large for
-    the host quantizer to be quick); returns (uint8 [rows, k], fp32 scales
-    [ceil(rows / block_rows), k / 128])."""
+# ------------------------------------------------------------------ inputs
+def randn(shape, seed, dev):
+    """N(0,1) fp32 on the GPU from a generator seeded with `seed`."""
     import torch
-    rp = -(-rows // block_rows) * block_rows
-    x = torch.randn((rp, k), generator=gen, device=dev)
-    blk = x.view(rp // block_rows, block_rows, k // 128, 128)
-    sc = blk.abs().amax(dim=(1, 3)).clamp_min(1e-12) / 448.0
-    qx = (blk / sc[:, None, :, None]).to(torch.float8_e4m3fn).view(rp, k)[:rows]
-    return qx.contiguous().view(torch.uint8), sc.contiguous()
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
 
 
-def _gpu_quant_e8m0(rows, k, block_rows, gen, dev):
-    """N(0,1) data quantized to e4m3 with one E8M0 scale 2^ceil(log2(amax /
-    448)) per block_rows x 128 block, on the GPU; returns (uint8 [rows, k],
-    uint8 exponent codes [ceil(rows / block_rows), k / 128])."""
+def make_operands(q, fam, M, N, K, dev, sfa_km=False):
+    """Quantized operands on the GPU (this library's device quantizers, the
+    BASELINE recipes).  Returns a dict with the GEMM inputs and the host
+    copies the checker and the CPU baseline use."""
     import torch
-    rp = -(-rows // block_rows) * block_rows
-    x = torch.randn((rp, k), generator=gen, device=dev)
-    blk = x.view(rp // block_rows, block_rows, k // 128, 128)
-    e = torch.ceil(torch.log2(blk.abs().amax(dim=(1, 3)).clamp_min(1e-30) / 448.0)).clamp(-127, 127)
-    qx = (blk / torch.exp2(e)[:, None, :, None]).to(torch.float8_e4m3fn).view(rp, k)[:rows]
-    return qx.contiguous().view(torch.uint8), (e + 127).to(torch.uint8).contiguous()
+    a, b = randn((M, K), 0, dev), randn((N, K), 1, dev)
+    ops = {}
+    if fam == "mx8":
+        A, SA = q.quant_mxfp8(a)
+        B, SB = q.quant_mxfp8(b)
+        ops.update(A=A.view(torch.uint8), SA=SA, B=B.view(torch.uint8), SB=SB)
+    elif fam == "mx4":
+        A, SA = q.quant_mxfp4(a)
+        B, SB = q.quant_mxfp4(b)
+        ops.update(A=A, SA=SA, B=B, SB=SB)
+    elif fam == "bs8":
+        A, SA = q.quant_fp8_e8m0_blockscale(a, "1x128")          # SA: [M, K/128] view of [K/128][M] bytes
+        B, SB = q.quant_fp8_e8m0_blockscale(b, "128x128")
+        ops.update(A=A.view(torch.uint8), SA=SA, B=B.view(torch.uint8), SB=SB)
+    else:
+        A, SA = q.quant_fp8_blockscale(a, "1x128", "km" if sfa_km else "mk")
+        B, SB = q.quant_fp8_blockscale(b, "128x128")
+        ops.update(A=A.view(torch.uint8), SA=SA, B=B.view(torch.uint8), SB=SB)
+    del a, b
+    ops["B_raw"] = ops["B"]
+    if fam == "bs":
+        ops["B"] = q.shuffle_b_kpanel(ops["B"]).reshape(-1)
+    elif fam == "lbp":
+        ops["B"] = q.ldsbypass_pack_b(ops["B"])
+    elif fam == "bs8":
+        ops["B"] = q.shuffle_weight_16x16(ops["B"])
+    torch.cuda.synchronize()
+    return ops
 
 
-def _time_calls(calls, ws, stream, graph_mode, steps, warmup):
-    """Average launch time (ms) of `steps` launches cycling through `calls`:
-    back-to-back launches, or (graph_mode) one HIP graph replay of them."""
+def kargs_for(q, fam, M, N, K, A, B, C, SA, SB, sfa_km):
+    kg32, kg128 = K // 32, K // 128
+    kb = K // 2 if fam == "mx4" else K
+    if fam in ("mx8", "mx4"):
+        return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, kb, kb, N, M * kb, N * kb, M * N,
+                       SA.data_ptr(), SB.data_ptr(), kg32, kg32, M * kg32, N * kg32)
+    if fam == "bs8":
+        return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, K, N, M * K, N * K, M * N,
+                       SA.data_ptr(), SB.data_ptr(), M, kg128, M * kg128, SB.numel())
+    sfa_stride = M if sfa_km else (1 if M > 1 else M)
+    if fam == "bs":
+        return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K, N * K, M * N,
+                       SA.data_ptr(), SB.data_ptr(), sfa_stride, kg128, M * kg128, SB.numel())
+    return q.LdsBypassKargs(A.data_ptr(), None, B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K, N * K,
+                            M * N, SA.data_ptr(), SB.data_ptr(), sfa_stride, kg128, M * kg128, SB.numel(), B.numel())
+
+
+def entry_for(L, fam):
+    """(launch(kargs_ptr, ws_ptr, ws_bytes, stream), workspace query) of a family."""
+    if fam == "bs8":
+        return (lambda ka, wp, wb, s: L.launch_blockscale_bpreshuffle(ka, 1, 0, s)), (lambda ka: 0)
+    name = {"mx8": "gemm_a8w8_mxfp8", "mx4": "gemm_a4w4_mxfp4", "bs": "gemm_a8w8_blockscale_bpreshuffle",
+            "lbp": "gemm_a8w8_blockscale_ldsbypass"}[fam]
+    fn = getattr(L, name)
+    return (lambda ka, wp, wb, s: fn(ka, 1, wp, wb, s)), getattr(L, name + "_workspace_bytes")
+
+
+# ------------------------------------------------------------------ timing
+def run_timed(launch, n_calls, stream, graph_mode, steps, warmup, settle_s):
+    """Settle, warm up, then time exactly `steps` launches.  Returns
+    (ms per launch, timing dict)."""
     import torch
-    sptr = ctypes.c_void_p(stream.cuda_stream)
-
-    def launch(i):
-        fn, ka = calls[i % len(calls)]
-        st = fn(ctypes.byref(ka), 1, ws.data_ptr(), ws.numel(), sptr)
-        if st:
-            raise RuntimeError(f"{fn.__name__} failed: HIP error {st}")
-
     with torch.cuda.stream(stream):
         launch(0)
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    graph = None
     if graph_mode:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             for i in range(steps):
                 launch(i)
+
+    # clock settle: back-to-back work for >= settle_s seconds; one batch is
+    # queued while the previous one runs (the host never runs far ahead)
+    t0 = time.perf_counter()
+    settle, prev = 0, None
+    while True:
         with torch.cuda.stream(stream):
-            for i in range(warmup):
-                launch(i)
-            graph.replay()
-        torch.cuda.synchronize()
-        e0.record(stream)
-        with torch.cuda.stream(stream):
-            graph.replay()
-        e1.record(stream)
-    else:
-        with torch.cuda.stream(stream):
-            for i in range(warmup):
-                launch(i)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        with torch.cuda.stream(stream):
-            for i in range(steps):
-                launch(i)
-        e1.record(stream)
+            if graph_mode:
+                graph.replay()
+                settle += steps
+            else:
+                for i in range(32):
+                    launch(settle + i)
+                settle += 32
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        if prev is not None:
+            prev.synchronize()
+        prev = ev
+        if time.perf_counter() - t0 >= settle_s:
+            break
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    settle_wall = time.perf_counter() - t0
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            launch(i)
+    torch.cuda.synchronize()
+
+    timing = {"settle_s": round(settle_wall, 3), "settle_launches": settle, "warmup": warmup}
+    if graph_mode:
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        wall0 = time.perf_counter()
+        evs[0].record(stream)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        evs[1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        # spread: four more replays, each timed on its own (not part of the value)
+        reps = []
+        for r in range(4):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            with torch.cuda.stream(stream):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            reps.append(e0.elapsed_time(e1) / steps)
+        ms = evs[0].elapsed_time(evs[1]) / steps
+        timing.update(mode=f"one HIP graph of {steps} launches over {n_calls} rotating weight copies",
+                      replay_us=[round(ms * 1e3, 3)] + [round(x * 1e3, 3) for x in reps], wall_s_timed=round(wall, 4))
+        return ms, timing
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    wall0 = time.perf_counter()
+    evs[0].record(stream)
+    with torch.cuda.stream(stream):
+        for i in range(steps):
+            launch(i)
+            evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = evs[0].elapsed_time(evs[-1]) / steps
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]) * 1e3
+    quart = max(1, steps // 4)
+    timing.update(mode="back-to-back launches, an event after each",
+                  launch_us={"min": round(float(per.min()), 2), "median": round(float(np.median(per)), 2),
+                             "max": round(float(per.max()), 2),
+                             "first_vs_last_quartile": round(float(per[:quart].mean() / per[-quart:].mean()), 4)},
+                  wall_s_timed=round(wall, 4))
+    return ms, timing
+
+
+# ------------------------------------------------------------------ checker
+def check_points(O, fam, M, N, K, host, C, sfa_km):
+    """4096 sampled outputs against the oracle on the same quantized bytes."""
+    rng = np.random.default_rng(12345)
+    rows = rng.integers(0, M, CHECK_POINTS).astype(np.int32)
+    cols = rng.integers(0, N, CHECK_POINTS).astype(np.int32)
+    A, B, SA, SB = host["A"], host["B_raw"], host["SA"], host["SB"]
+    if fam == "mx8":
+        ref = O.gemm_mx8_points(A, B, SA, SB, rows, cols)
+    elif fam == "mx4":
+        ref = O.gemm_mx4_points(A, B, SA, SB, rows, cols)
+    elif fam == "bs8":
+        ref = O.gemm_bs_e8m0_points(A, B, SA, SB, rows, cols)     # SA physical [K/128][M]
+    else:
+        ref = O.gemm_bs_fp32_points(A, B, SA, SB, rows, cols, sfa_layout="km" if sfa_km else "mk")
+    got = C.float().cpu().numpy()[rows, cols]
+    bad, ratio, _ = O.check_tolerance(ref, got)
+    return {"points": CHECK_POINTS, "violations": bad, "max_err_over_bound": round(ratio, 4), "ok": bad == 0}
+
+
+def host_copies(fam, ops, sfa_km):
+    """Host arrays of the quantized operands in the oracle's layouts."""
+    h = {k: ops[k].cpu().numpy() for k in ("A", "B_raw", "SB")}
+    sa = ops["SA"]
+    if fam == "bs8":
+        h["SA"] = sa.t().contiguous().cpu().numpy()               # physical [K/128][M]
+    elif fam in ("bs", "lbp") and sfa_km:
+        h["SA"] = sa.t().contiguous().cpu().numpy()
+    else:
+        h["SA"] = sa.contiguous().cpu().numpy()
+    return h
+
+
+def cpu_baseline(O, fam, M, N, K, h, sfa_km, seconds):
+    """The oracle's restatement of the reference CPU GEMM on a bounded row
+    band of the same GEMM, OpenMP over this host's cores, extrapolated per
+    FLOP."""
+    A, B, SA, SB = h["A"], h["B_raw"], h["SA"], h["SB"]
+    if fam == "mx8":
+        fn = lambda r: O.gemm_mx8(A[r], B, SA[r], SB)
+        which = "MX8 gemm_ref (mxfp8_gemm/gemm_a8w8_mxfp8_host.cc:96-122)"
+    elif fam == "mx4":
+        fn = lambda r: O.gemm_mx4(A[r], B, SA[r], SB)
+        which = "MX4 gemm_ref_gpu grouped form (gemm_a4w4_mxfp4_4wave_host.cc:66-94)"
+    elif fam == "bs8":
+        fn = lambda r: O.gemm_bs_e8m0(A[r], B, np.ascontiguousarray(SA[:, r]), SB)
+        which = "SNAP gemm_ref (gemm_a8w8_blockscale_bpreshuffle_host.cc:219-248)"
+    else:
+        if sfa_km:
+            fn = lambda r: O.gemm_bs_fp32(A[r], B, np.ascontiguousarray(SA[:, r]), SB, sfa_layout="km")
+        else:
+            fn = lambda r: O.gemm_bs_fp32(A[r], B, SA[r], SB)
+        which = "BPS gemm_ref (gemm_a8w8_blockscale_bpreshuffle_host.cc:66-90)"
+    rows, elapsed = 1, 0.0
+    while True:
+        t = time.perf_counter()
+        fn(slice(0, rows))
+        elapsed = time.perf_counter() - t
+        if elapsed * 2 > seconds or rows >= M:
+            break
+        rows = min(M, max(rows * 2, int(rows * seconds / max(elapsed, 1e-3) * 0.5)))
+    tflops = 2.0 * rows * N * K / elapsed / 1e12
+    full = rows >= M
+    return {"value": round(tflops, 6), "unit": "TFLOPS", "cores": O.num_threads(), "kind": "port",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": (f"rows 0..{rows - 1} of the same {M}x{N}x{K} GEMM ({elapsed:.2f} s"
+                       + (", the whole GEMM)" if full else ", extrapolated per FLOP)")
+                       + f"; oracle restatement of the {which}, OpenMP")}
+
+
+# ------------------------------------------------------------------ sweep
+SWEEP_M = (1, 16, 64, 256, 1024, 4096, 16384)
+SWEEP_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168))
 
 
 def sweep(args):
@@ -168,16 +355,15 @@ def sweep(args):
     L = q.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0)
     stream = torch.cuda.Stream(dev)
     for n, k in SWEEP_NK:
-        qb, sb = _gpu_quant_bs(n, k, 128, gen, dev)
-        bk = q.shuffle_b_kpanel(qb)
-        bpp = q.ldsbypass_repack(bk)
+        qb, sb = q.quant_fp8_blockscale(randn((n, k), 1, dev), "128x128")
+        bk = q.shuffle_b_kpanel(qb.view(torch.uint8))
+        bpp = q.ldsbypass_pack_b(qb.view(torch.uint8))
         kg = k // 128
         for m in SWEEP_M:
-            qa, sa = _gpu_quant_bs(m, k, 1, gen, dev)
+            qa, sa = q.quant_fp8_blockscale(randn((m, k), 0, dev), "1x128")
+            qa = qa.view(torch.uint8)
             C = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
             hbm = m <= 256
             for variant, B0 in (("bpreshuffle", bk), ("ldsbypass", bpp)):
@@ -185,36 +371,35 @@ def sweep(args):
                 copies = max(2, ROTATE_BYTES // b_bytes + 1) if hbm else 1
                 Bs = [B0] + [B0.clone() for _ in range(copies - 1)]
                 SBs = [sb] + [sb.clone() for _ in range(copies - 1)]
-                calls = []
-                for B, SB in zip(Bs, SBs):
-                    if variant == "bpreshuffle":
-                        ka = q.Kargs(qa.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, 1, k, 128, n, m * k, n * k,
-                                     m * n, sa.data_ptr(), SB.data_ptr(), 1 if m > 1 else m, kg, m * kg, SB.numel())
-                        fn, wq = L.gemm_a8w8_blockscale_bpreshuffle, L.gemm_a8w8_blockscale_bpreshuffle_workspace_bytes
-                    else:
-                        ka = q.LdsBypassKargs(qa.data_ptr(), None, B.data_ptr(), C.data_ptr(), m, n, k, 1, k, 128, n,
-                                              m * k, n * k, m * n, sa.data_ptr(), SB.data_ptr(), 1 if m > 1 else m, kg,
-                                              m * kg, SB.numel(), B.numel())
-                        fn, wq = L.gemm_a8w8_blockscale_ldsbypass, L.gemm_a8w8_blockscale_ldsbypass_workspace_bytes
-                    calls.append((fn, ka))
-                wsb = max(1, wq(ctypes.byref(calls[0][1])))
+                fam = "bs" if variant == "bpreshuffle" else "lbp"
+                launch_fn, wq = entry_for(L, fam)
+                calls = [kargs_for(q, fam, m, n, k, qa, B, C, sa, SB, False) for B, SB in zip(Bs, SBs)]
+                wsb = max(1, wq(ctypes.byref(calls[0])))
                 ws = torch.zeros((wsb + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+                sptr = ctypes.c_void_p(stream.cuda_stream)
+
+                def launch(i):
+                    st = launch_fn(ctypes.byref(calls[i % len(calls)]), ws.data_ptr(), ws.numel(), sptr)
+                    if st:
+                        raise RuntimeError(f"{variant} failed: HIP error {st}")
+
                 flops = 2.0 * m * n * k
                 steps = max(8, min(50, int(2e13 / flops)))
-                ms = _time_calls(calls, ws, stream, hbm, steps, max(4, steps // 2))
+                ms, timing = run_timed(launch, len(calls), stream, hbm, steps, max(4, steps // 2), 0.2)
                 alg = m * k + sa.numel() * 4 + b_bytes + m * n * 2
                 tf = flops / (ms * 1e-3) / 1e12
                 gbps = alg / (ms * 1e-3) / 1e9
                 print(json.dumps({"sweep": "configs[2]", "variant": variant, "M": m, "N": n, "K": k,
                                   "us": round(ms * 1e3, 2), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / 5000.0, 4),
                                   "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_GBPS, 4),
-                                  "bound": "hbm" if hbm else "mfma"}), flush=True)
+                                  "bound": "hbm" if hbm else "mfma", "kernel": q.last_launch()}), flush=True)
                 del Bs, SBs, calls, ws
             del qa, sa, C
         del qb, sb, bk, bpp
         torch.cuda.empty_cache()
 
 
+# ------------------------------------------------------------------ main
 def main():
     args = parse()
     if args.gpus != 1:
@@ -241,144 +426,38 @@ def main():
         sweep(args)
         return
 
-    import oracle as O
-
     q = importlib.import_module("355_1_trans_amd")
     L = q.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
     fam, M, N, K, cfg = WORKLOADS[args.workload]
-    if args.m:
-        M = args.m
-    if args.n:
-        N = args.n
-    if args.k:
-        K = args.k
+    M, N, K = args.m or M, args.n or N, args.k or K
     hbm_bound = M <= 256
-    kg32, kg128 = K // 32, K // 128
-    if fam == "bs8":
-        # N(0,1) quantized on the GPU with E8M0 block scales 2^ceil(log2(amax / 448))
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(0)
-        qa, sa = _gpu_quant_e8m0(M, K, 1, gen, dev)
-        qb, sb = _gpu_quant_e8m0(N, K, 128, gen, dev)
-        A = qa
-        SA = sa.t().contiguous()                        # physical [K/128][M], stride_sfa = M
-        B0 = q.shuffle_weight_16x16(qb)
-        SB0 = sb
-        a = b = None
-    else:
-        a = O.randn((M, K), 0, 0)
-        b = O.randn((N, K), 0, 1)
-
-    # quantize once on the host (BASELINE recipe); device copies of the operands
-    if fam == "bs8":
-        pass
-    elif fam == "mx8":
-        qa, sa = O.quant_mx8(a)
-        qb, sb = O.quant_mx8(b)
-    elif fam == "mx4":
-        qa, sa = O.quant_mx4(a)
-        qb, sb = O.quant_mx4(b)
-    else:
-        qa, sa = O.quant_bs_act(a)
-        qb, sb = O.quant_bs_wgt(b)
-    if fam != "bs8":
-        A = torch.from_numpy(qa).to(dev)
-        SA = torch.from_numpy(np.ascontiguousarray(sa.T) if args.sfa_km else sa).to(dev)
-        B0 = torch.from_numpy(qb).to(dev)
-        SB0 = torch.from_numpy(sb).to(dev)
-    if fam == "bs":
-        B0 = q.shuffle_b_kpanel(B0)
-    elif fam == "lbp":
-        B0 = q.ldsbypass_repack(q.shuffle_b_kpanel(B0))
+    ops = make_operands(q, fam, M, N, K, dev, args.sfa_km)
+    A, SA, B0, SB0 = ops["A"], ops["SA"], ops["B"], ops["SB"]
     C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     b_bytes = B0.numel() * B0.element_size() + SB0.numel() * SB0.element_size()
     copies = max(2, ROTATE_BYTES // b_bytes + 1) if hbm_bound else 1
     Bs = [B0] + [B0.clone() for _ in range(copies - 1)]
     SBs = [SB0] + [SB0.clone() for _ in range(copies - 1)]
 
-    kb = K // 2 if fam == "mx4" else K
-    calls = []
-    for B, SB in zip(Bs, SBs):
-        if fam in ("mx8", "mx4"):
-            args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, kb, kb, N, M * kb, N * kb, M * N,
-                            SA.data_ptr(), SB.data_ptr(), kg32, kg32, M * kg32, N * kg32)
-            fn = L.gemm_a8w8_mxfp8 if fam == "mx8" else L.gemm_a4w4_mxfp4
-            wq = L.gemm_a8w8_mxfp8_workspace_bytes if fam == "mx8" else L.gemm_a4w4_mxfp4_workspace_bytes
-        elif fam == "bs8":
-            args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, K, N, M * K, N * K, M * N,
-                            SA.data_ptr(), SB.data_ptr(), M, kg128, M * kg128, SB.numel())
-
-            def fn(ka, out_bf16, ws_ptr, ws_bytes, stream):
-                return L.launch_blockscale_bpreshuffle(ka, out_bf16, 0, stream)
-            fn.__name__ = "launch_blockscale_bpreshuffle"
-
-            def wq(ka):
-                return 0
-        elif fam == "bs":
-            args_ = q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K, N * K, M * N,
-                            SA.data_ptr(), SB.data_ptr(), M if args.sfa_km else (1 if M > 1 else M), kg128,
-                            M * kg128, SB.numel())
-            fn, wq = L.gemm_a8w8_blockscale_bpreshuffle, L.gemm_a8w8_blockscale_bpreshuffle_workspace_bytes
-        else:
-            args_ = q.LdsBypassKargs(A.data_ptr(), None, B.data_ptr(), C.data_ptr(), M, N, K, 1, K, 128, N, M * K,
-                                     N * K, M * N, SA.data_ptr(), SB.data_ptr(),
-                                     M if args.sfa_km else (1 if M > 1 else M), kg128, M * kg128, SB.numel(),
-                                     B.numel())
-            fn, wq = L.gemm_a8w8_blockscale_ldsbypass, L.gemm_a8w8_blockscale_ldsbypass_workspace_bytes
-        calls.append((fn, args_))
-    ws_bytes = max(1, wq(ctypes.byref(calls[0][1])))
+    launch_fn, wq = entry_for(L, fam)
+    calls = [kargs_for(q, fam, M, N, K, A, B, C, SA, SB, args.sfa_km) for B, SB in zip(Bs, SBs)]
+    ws_bytes = max(1, wq(ctypes.byref(calls[0])))
     ws = torch.zeros((ws_bytes + 255) // 256 * 256, dtype=torch.uint8, device=dev)
-
     stream = torch.cuda.Stream(dev)
     sptr = ctypes.c_void_p(stream.cuda_stream)
 
     def launch(i):
-        fn, ka = calls[i % len(calls)]
-        st = fn(ctypes.byref(ka), 1, ws.data_ptr(), ws.numel(), sptr)
+        st = launch_fn(ctypes.byref(calls[i % len(calls)]), ws.data_ptr(), ws.numel(), sptr)
         if st:
-            raise RuntimeError(f"{fn.__name__} failed: HIP error {st}")
+            raise RuntimeError(f"{args.workload} launch failed: HIP error {st}")
 
     with torch.cuda.stream(stream):
         launch(0)
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    if hbm_bound:
-        # one graph of exactly `steps` launches over the rotating weight copies;
-        # a warm replay, then the timed replay
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(args.steps):
-                launch(i)
-        with torch.cuda.stream(stream):
-            for i in range(args.warmup):
-                launch(i)
-            graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(stream)
-        with torch.cuda.stream(stream):
-            graph.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-    else:
-        with torch.cuda.stream(stream):
-            for i in range(args.warmup):
-                launch(i)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(stream)
-        with torch.cuda.stream(stream):
-            for i in range(args.steps):
-                launch(i)
-        e1.record(stream)
-        torch.cuda.synchronize()
-    launches = args.steps
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / launches
+    kernel = q.last_launch()
+    ms, timing = run_timed(launch, len(calls), stream, hbm_bound, args.steps, args.warmup, args.settle_s)
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
 
@@ -386,61 +465,42 @@ def main():
     tag = args.workload + (f"_m{M}" if args.m else "") + (f"_n{N}" if args.n else "") + (f"_k{K}" if args.k else "")
     if hbm_bound:
         # algorithmic bytes: A, B and both scale arrays read once, C written once
-        alg = (A.numel() * A.element_size() + SA.numel() * SA.element_size() + b_bytes + C.numel() * 2)
+        alg = A.numel() * A.element_size() + SA.numel() * SA.element_size() + b_bytes + C.numel() * 2
         gbps = alg / (ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_GBPS, "unit": "GB/s",
                     "frac": round(gbps / HBM_GBPS, 4), "traffic": traffic_from_profiles(tag),
-                    "algorithmic_bytes": alg}
+                    "algorithmic_bytes": int(alg)}
     else:
         peak = PEAK_TFLOPS[kind]
         roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
                     "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(tag)}
 
-    cpu = None
-    if not args.no_cpu:
-        if fam == "mx8":
-            cpu_fn = lambda rows: O.gemm_mx8(qa[rows], qb, sa[rows], sb)
-        elif fam == "mx4":
-            cpu_fn = lambda rows: O.gemm_mx4(qa[rows], qb, sa[rows], sb)
-        elif fam == "bs8":
-            qa_h, qb_h = qa.cpu().numpy(), qb.cpu().numpy()
-            sa_h, sb_h = SA.cpu().numpy(), sb.cpu().numpy()
-            cpu_fn = lambda rows: O.gemm_bs_e8m0(qa_h[rows], qb_h, np.ascontiguousarray(sa_h[:, rows]), sb_h)
-        else:
-            cpu_fn = lambda rows: O.gemm_bs_fp32(qa[rows], qb, sa[rows], sb)
-        # bounded row band of the same GEMM on this host's cores, extrapolated per FLOP
-        rows, elapsed = 1, 0.0
-        while True:
-            t = time.perf_counter()
-            cpu_fn(slice(0, rows))
-            elapsed = time.perf_counter() - t
-            if elapsed * 2 > args.cpu_seconds or rows >= M:
-                break
-            rows = min(M, max(rows * 2, int(rows * args.cpu_seconds / max(elapsed, 1e-3) * 0.5)))
-        cpu_tflops = 2.0 * rows * N * K / elapsed / 1e12
-        cpu = {"value": round(cpu_tflops, 6), "unit": "TFLOPS", "cores": O.num_threads(), "kind": "port",
-               "sample": f"rows 0..{rows - 1} of the same {M}x{N}x{K} GEMM ({elapsed:.1f} s, extrapolated "
-                         f"per FLOP); oracle restatement of the reference CPU gemm_ref, OpenMP"}
+    check, cpu = None, None
+    if not (args.no_check and args.no_cpu):
+        import oracle as O
+        h = host_copies(fam, ops, args.sfa_km)
+        if not args.no_check:
+            torch.cuda.synchronize()
+            check = check_points(O, fam, M, N, K, h, C, args.sfa_km)
+        if not args.no_cpu:
+            cpu = cpu_baseline(O, fam, M, N, K, h, args.sfa_km, args.cpu_seconds)
 
-    names = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
-             "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
-             "bs": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, K-panel B (bpreshuffle)",
-             "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)",
-             "bs8": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, shuffle_weight(16,16) B"}
     line = {
-        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": launches,
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": kind, "data": "synthetic N(0,1) seed 0, BASELINE quantization recipe",
-        "config": {"workload": f"{names[fam]} M={M} N={N} K={K}, bf16 out " +
+        "vs_baseline": None, "dtype": kind,
+        "data": "synthetic N(0,1) (torch GPU generator, seeds 0 / 1), quantized on the GPU per the BASELINE recipe",
+        "config": {"workload": f"{NAMES[fam]} M={M} N={N} K={K}, bf16 out " +
                                (f"(BASELINE configs[{cfg}])" if cfg is not None
                                 else "(the reference's headline block-scale kernel, BASELINE.md)"),
-                   "M": M, "N": N, "K": K, "out": "bf16",
-                   "timing": ("one HIP graph of the timed launches over %d rotating weight copies" % len(calls))
-                   if hbm_bound else "back-to-back launches"},
-        "roofline": roofline, "cpu_baseline": cpu,
-        "wall_s_timed": round(wall, 4),
+                   "M": M, "N": N, "K": K, "out": "bf16", "kernel": kernel},
+        "timing": timing, "roofline": roofline, "cpu_baseline": cpu, "check": check,
     }
     print(json.dumps(line), flush=True)
+    if check is not None and not check["ok"]:
+        print(f"bench.py: output check FAILED ({check['violations']} of {CHECK_POINTS} points out of tolerance)",
+              file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

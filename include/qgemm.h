@@ -187,6 +187,59 @@ size_t qgemm_ldsbypass_b_bytes(int n, int k);
 int qgemm_pack_b_ldsbypass(const uint8_t* b_raw, uint8_t* b_pp, int n, int k);
 
 /* ------------------------------------------------------------------ */
+/* Device-side quantizers (the step before the GEMM, on the GPU).       */
+/* ------------------------------------------------------------------ */
+/* Source: fp32 (in_dtype QGEMM_IN_FP32) or bf16 (QGEMM_IN_BF16) rows of K
+ * elements, row pitch ldx >= K a multiple of 4 elements, base aligned to 16
+ * (fp32) or 8 (bf16) bytes.  Codes are round-to-nearest-even, saturating,
+ * bit-identical to the host recipes of BASELINE.json's configs.  Outputs
+ * must not overlap the source or each other.  The reference quantizes with
+ * aiter (not in the container; its MXFP4 path is quant(..., shuffle=True),
+ * MX4/candidate_m9/README.md:6-12), so these replace that step; the recipes
+ * themselves are the ones BASELINE.json configs[0-4] state. */
+#define QGEMM_IN_FP32 0
+#define QGEMM_IN_BF16 1
+
+/* e4m3 [M,K] (pitch ldq bytes) + fp32 scale amax/448 per 1x128 block
+ * (1.0 for an all-zero block): scale(m, g) = scale[m*scale_sm + g*scale_sk],
+ * row-major [M][K/128] (scale_sm >= K/128, scale_sk = 1) or the BPS
+ * column-major [K/128][M] (scale_sm = 1, scale_sk >= M, BPS host.cc:78,270).
+ * K a multiple of 128.  Feeds gemm_a8w8_blockscale_bpreshuffle/_ldsbypass. */
+hipError_t qgemm_quant_fp8_blockscale_act(const void* x, int in_dtype, int m, int k, int ldx, uint8_t* q, int ldq,
+                                          float* scale, int scale_sm, int scale_sk, hipStream_t stream);
+/* e4m3 [N,K] + fp32 scale per 128x128 block, scale [ceil(N/128)][ld_scale]. */
+hipError_t qgemm_quant_fp8_blockscale_wgt(const void* w, int in_dtype, int n, int k, int ldw, uint8_t* q, int ldq,
+                                          float* scale, int ld_scale, hipStream_t stream);
+/* The same blocks with E8M0 scales 2^ceil(log2(amax/448)) (codes E+127):
+ * the inputs of launch_blockscale_bpreshuffle (SNAP blockscale_bpreshuffle.py:3-4);
+ * pass e_sm = 1, e_sk = M for its column-major SFA. */
+hipError_t qgemm_quant_fp8_e8m0_act(const void* x, int in_dtype, int m, int k, int ldx, uint8_t* q, int ldq,
+                                    uint8_t* e, int e_sm, int e_sk, hipStream_t stream);
+hipError_t qgemm_quant_fp8_e8m0_wgt(const void* w, int in_dtype, int n, int k, int ldw, uint8_t* q, int ldq,
+                                    uint8_t* e, int ld_e, hipStream_t stream);
+/* MXFP8: e4m3 [rows,K] + E8M0 2^ceil(log2(amax/448)) per 32 K elements;
+ * MXFP4: e2m1 [rows,K/2] bytes (even k in the low nibble) + E8M0
+ * 2^ceil(log2(amax/6)).  Scales row-major [rows][lde] (shuffle = 0) or in
+ * aiter's e8m0_shuffle order (shuffle = 1; qgemm_e8m0_shuffle_bytes bytes,
+ * padding 0x7F; lde ignored).  K a multiple of 32. */
+hipError_t qgemm_quant_mxfp8(const void* x, int in_dtype, int rows, int k, int ldx, uint8_t* q, int ldq, uint8_t* e,
+                             int lde, int shuffle, hipStream_t stream);
+hipError_t qgemm_quant_mxfp4(const void* x, int in_dtype, int rows, int k, int ldx, uint8_t* q, int ldq, uint8_t* e,
+                             int lde, int shuffle, hipStream_t stream);
+
+/* On-device twins of the offline layout helpers below (same byte maps);
+ * src rows of k_bytes with pitch ld_src (multiple of 16), 16-byte aligned
+ * buffers, dst packed. */
+hipError_t qgemm_shuffle_b_kpanel_device(const uint8_t* src, uint8_t* dst, int n, int k_bytes, int ld_src,
+                                         hipStream_t stream);
+hipError_t qgemm_shuffle_weight_16x16_device(const uint8_t* src, uint8_t* dst, int n, int k_bytes, int ld_src,
+                                             hipStream_t stream);
+hipError_t qgemm_pack_b_ldsbypass_device(const uint8_t* b_raw, uint8_t* b_pp, int n, int k, int ld_src,
+                                         hipStream_t stream);
+hipError_t qgemm_e8m0_shuffle_device(const uint8_t* src, uint8_t* dst, int rows, int groups_k, int ld_src,
+                                     hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* Layout probe (the reference's mfma_layout_probe/ known answers).     */
 /* ------------------------------------------------------------------ */
 /* Launches the one-wave scaled-MFMA and LDS-DMA probes on `stream`;

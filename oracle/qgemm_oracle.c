@@ -208,7 +208,9 @@ void ora_quant_bs_wgt(const float* w, int n, int k, uint8_t* q, float* s) {
  * amax == 0 gives the neutral byte 127 (all quanta are then 0). */
 static int mx_exponent(float amax, float qmax) {
     if (!(amax > 0.0f)) return 0;
-    int e = ora_ceil_log2(amax / qmax);
+    const float v = amax / qmax;
+    if (v == 0.0f) return -127;                           /* quotient underflows: the clamp */
+    int e = ora_ceil_log2(v);
     if (e < -127) e = -127;
     if (e > 127) e = 127;
     return e;

@@ -245,3 +245,30 @@ def test_e8m0_adapter_rejects_before_launch(qgemm):
         f(x[0], x, x, x)
     with pytest.raises(ValueError, match="GPU"):
         f(x.view(torch.float8_e4m3fn), x, x[:, :2], x[:2, :2])
+
+
+# ----------------------------------------------------------------- quantizer entries
+def test_quantizers_reject_bad_arguments(qgemm):
+    """Bad sources, pitches, alignments, scale layouts and overlaps return
+    hipErrorInvalidValue before any device work (fake, separated addresses)."""
+    L = qgemm.lib()
+    x, q, s = 1 << 44, (1 << 44) + (1 << 38), (1 << 44) + (2 << 38)
+    m, k = 64, 1024
+    act = L.qgemm_quant_fp8_blockscale_act
+    assert act(None, 0, m, k, k, q, k, s, k // 128, 1, None) == HIP_INVALID_VALUE
+    assert act(x, 2, m, k, k, q, k, s, k // 128, 1, None) == HIP_INVALID_VALUE          # dtype code
+    assert act(x, 0, m, 1000, 1000, q, 1000, s, 8, 1, None) == HIP_INVALID_VALUE      # K % 128
+    assert act(x, 0, m, k, k - 4, q, k, s, k // 128, 1, None) == HIP_INVALID_VALUE     # pitch < K
+    assert act(x + 4, 0, m, k, k, q, k, s, k // 128, 1, None) == HIP_INVALID_VALUE     # fp32 source not 16-B aligned
+    assert act(x, 0, m, k, k, q, k, s, 2, 1, None) == HIP_INVALID_VALUE                # scale rows overlap
+    assert act(x, 0, m, k, k, q, k, s, 1, m - 1, None) == HIP_INVALID_VALUE            # column-major pitch < M
+    assert act(x, 0, m, k, k, x + 64, k, s, k // 128, 1, None) == HIP_INVALID_VALUE    # q overlaps x
+    mx = L.qgemm_quant_mxfp4
+    assert mx(x, 0, m, 100, 100, q, 50, s, 3, 0, None) == HIP_INVALID_VALUE             # K % 32
+    assert mx(x, 0, m, 96, 96, q, 47, s, 3, 0, None) == HIP_INVALID_VALUE               # q pitch < K/2
+    assert mx(x, 0, m, 96, 96, q, 48, s, 2, 0, None) == HIP_INVALID_VALUE               # scale pitch < K/32
+    assert mx(x, 0, m, 96, 96, q, 48, s, 3, 2, None) == HIP_INVALID_VALUE               # shuffle flag
+    lay = L.qgemm_shuffle_weight_16x16_device
+    assert lay(x, q, 40, 256, 256, None) == HIP_INVALID_VALUE                            # N % 16
+    assert L.qgemm_shuffle_b_kpanel_device(x, q, 40, 200, 208, None) == HIP_INVALID_VALUE   # K % 128
+    assert L.qgemm_shuffle_b_kpanel_device(x, x + 256, 40, 256, 256, None) == HIP_INVALID_VALUE  # overlap

@@ -146,6 +146,11 @@ def test_mx_exponent_is_minimal_power_of_two(kind, qmax):
     nz = amax > 0
     assert np.all(amax[nz] / p[nz] <= qmax)                      # fits the element range
     assert np.all(amax[nz] / (p[nz] / 2) > qmax)                 # and one step less would not
+    # a subnormal group amax: amax / qmax underflows in fp32, the exponent is the clamp -127
+    tiny = np.zeros((1, 64), np.float32)
+    tiny[0, 0], tiny[0, 32] = np.float32(1e-44), np.float32(1e-30)
+    _, e = O.quant_mx8(tiny) if kind == "mx8" else O.quant_mx4(tiny)
+    assert e[0, 0] == 0 and e[0, 1] == 127 + int(np.ceil(np.log2(1e-30 / qmax)))
 
 
 def test_quant_bs_e8m0_minimal_power_of_two_blocks():
