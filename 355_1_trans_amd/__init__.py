@@ -83,6 +83,8 @@ EXPORTS = {
     "gemm_a4w4_mxfp4": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),
     "gemm_a4w4_mxfp4_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "gemm_a4w4_mxfp4_noalloc": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p]),
+    "gemm_a4w4_mxfp4_noalloc_max_workspace_bytes": (ctypes.c_size_t, []),
     "gemm_a8w8_blockscale_ldsbypass": (ctypes.c_int, [ctypes.POINTER(LdsBypassKargs), ctypes.c_int,
                                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "gemm_a8w8_blockscale_ldsbypass_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LdsBypassKargs)]),

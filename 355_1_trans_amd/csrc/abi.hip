@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "launch.hpp"
 #include "qgemm.h"
@@ -775,6 +776,80 @@ size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
     const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, true);
     const Plan pl = plan_mx(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, true);
     return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny || pl.mid ? 0 : scale_panel_bytes(*args)});
+}
+
+// ------------------------------------------------ MXFP4 without a caller workspace
+}  // extern "C"
+
+namespace {
+
+// Scratch memory of gemm_a4w4_mxfp4_noalloc: split-K counters and fp32
+// partials, or the wide kernel's panel-major scale copy -- what a caller
+// otherwise passes as `workspace`.  Each GPU the library runs on holds its
+// own copy of this array until the process ends.  Host code must never pass
+// `scratch` itself to a kernel or a copy (on the host it is only a stand-in
+// symbol): scratch_ptr() returns this device's address of it.
+constexpr size_t kScratchBytes = 32u << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::atomic<uint8_t*> g_scratch_ptr[kMaxDevices];
+
+__global__ void zero_words_kernel(unsigned* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// This device's address of `scratch`, looked up (hipGetSymbolAddress, with the
+// device current) on the first call on each device; that call also zeroes the
+// split-K counter block on `stream` (a kernel, not a memset, so that the
+// first call may be captured into a HIP graph).  Later calls find the
+// counters zero again: every split-K launch re-arms the counters it used.
+hipError_t scratch_ptr(hipStream_t stream, uint8_t** out) {
+    int dev = 0;
+    hipError_t st = hipGetDevice(&dev);
+    if (st != hipSuccess) return st;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    uint8_t* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* addr = nullptr;
+            st = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (st != hipSuccess) return st;
+            p = static_cast<uint8_t*>(addr);
+            zero_words_kernel<<<1, 256, 0, stream>>>(reinterpret_cast<unsigned*>(p),
+                                                     (int)(kCounterBytes / sizeof(unsigned)));
+            st = hipGetLastError();
+            if (st != hipSuccess) return st;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t gemm_a4w4_mxfp4_noalloc_max_workspace_bytes(void) { return kScratchBytes; }
+
+// gemm_a4w4_mxfp4 with the library's static per-device scratch as its
+// workspace: no allocation and no caller buffer beyond A, B, scales and C.
+hipError_t gemm_a4w4_mxfp4_noalloc(const opus_gemm_scale_kargs* args, int out_dtype, hipStream_t stream) {
+    qg::trace_reset();
+    const size_t need = gemm_a4w4_mxfp4_workspace_bytes(args);
+    if (need > kScratchBytes) return hipErrorInvalidValue;    // beyond the static scratch
+    Spans sp;
+    hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256, &sp);
+    if (st != hipSuccess) return st;
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    uint8_t* ws = nullptr;
+    st = scratch_ptr(stream, &ws);
+    if (st != hipSuccess) return st;
+    return gemm_a4w4_mxfp4(args, out_dtype, need ? ws : nullptr, need ? kScratchBytes : 0, stream);
 }
 
 // ------------------------------------------------ block-scale FP8, E8M0 scales

@@ -170,6 +170,19 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args);
 
+/* No counterpart in the reference.  gemm_a4w4_mxfp4 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same kernels and results,
+ * with a static per-device scratch array of
+ * gemm_a4w4_mxfp4_noalloc_max_workspace_bytes() bytes (32 MiB) inside the
+ * library in place of `workspace`.  Returns hipErrorInvalidValue when the
+ * call needs more (gemm_a4w4_mxfp4_workspace_bytes(args) above the limit).
+ * Allocates nothing; each GPU keeps its array until the process ends.  All
+ * calls on one GPU share that array: calls that overlap in time on one GPU
+ * (different streams, or threads without stream order) race. */
+hipError_t gemm_a4w4_mxfp4_noalloc(const opus_gemm_scale_kargs* args, int out_dtype, hipStream_t stream);
+size_t gemm_a4w4_mxfp4_noalloc_max_workspace_bytes(void);
+
 /* ------------------------------------------------------------------ */
 /* Offline layout helpers (host, CPU).                                  */
 /* ------------------------------------------------------------------ */
