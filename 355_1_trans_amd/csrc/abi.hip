@@ -16,6 +16,7 @@
 
 #include "launch.hpp"
 #include "qgemm.h"
+#include "burst_gemm.hpp"
 #include "decode_gemm.hpp"
 #include "mid_gemm.hpp"
 #include "stream_gemm.hpp"
@@ -337,6 +338,32 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus) {
         p.ctr_bytes = kCounterBytes;
         p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
     }
+}
+
+// Burst kernel (burst_gemm.hpp) for fp32-block-scale decode shapes: its own
+// cost-model plan when that plan is accepted; workspace = counters +
+// splitk * batch * M * N fp32 partials when K is split.
+qg::BurstPlan plan_bsf32_burst(int m, int n, int k_tiles, int batch) {
+    return qg::burst_plan(m, n, k_tiles, batch, device_cus(), kMaxCounters);
+}
+
+size_t burst_ws_bytes(const qg::BurstPlan& b, int m, int n, int batch) {
+    return b.ok && b.splitk > 1 ? kCounterBytes + (size_t)b.splitk * batch * m * n * 4 : 0;
+}
+
+hipError_t run_burst(const TileArgs& t, int batch, const qg::BurstPlan& pl, bool frag, long long b_bytes, bool bf16,
+                     void* ws, hipStream_t stream) {
+    qg::BurstArgs a{};
+    a.t = t;
+    a.splitk = pl.splitk;
+    a.kt_per_split = pl.kt_per_split;
+    a.n_tiles = pl.n_tiles;
+    a.b_bytes = b_bytes;
+    if (pl.splitk > 1) {    // the caller brought the workspace (checked before routing)
+        a.counters = static_cast<unsigned*>(ws);
+        a.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+    }
+    return qg::launch_burst(a, frag, pl.mb, pl.nb, pl.waves, batch, bf16, stream);
 }
 
 Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
@@ -913,6 +940,9 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
     const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    const qg::BurstPlan bp = plan_bsf32_burst(a.m, a.n, a.k / 128, a.batch);
+    // (a split plan needs the workspace; without one the kernels below run unsplit)
+    if (bp.ok && (bp.splitk == 1 || workspace)) return run_burst(t, a.batch, bp, false, bk, bf16, workspace, stream);
     const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bk, true);
     if (pl.mid)
         return run_mid(t, a.batch, pl, bf16, qg::MidKind::BS_KPANEL, workspace, workspace_bytes, a.k / 128, stream);
@@ -926,6 +956,8 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
 
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
+    const qg::BurstPlan bp = plan_bsf32_burst(args->m, args->n, args->k / 128, args->batch);
+    if (bp.ok) return burst_ws_bytes(bp, args->m, args->n, args->batch);
     return plan_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, true).ws_bytes;
 }
 
@@ -953,8 +985,12 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
-    // small M: the skinny kernel streams B'' straight into registers; large
-    // M: the eight-wave tile kernel stages B'' blocks through LDS like B'
+    // decode shapes: the burst kernel (B'' fragments straight into
+    // registers); other small M: the skinny kernel streams B'' into
+    // registers; large M: the tile kernels stage B'' blocks through LDS
+    const qg::BurstPlan bp = plan_bsf32_burst(a.m, a.n, a.k / 128, a.batch);
+    if (bp.ok && (bp.splitk == 1 || workspace))
+        return run_burst(t, a.batch, bp, true, bpp, out_dtype == QGEMM_OUT_BF16, workspace, stream);
     const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bpp, false);
     if (pl.mid)
         return run_mid(t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, qg::MidKind::BS_FRAG, workspace,
@@ -966,6 +1002,8 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
 
 size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args) {
     if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
+    const qg::BurstPlan bp = plan_bsf32_burst(args->m, args->n, args->k / 128, args->batch);
+    if (bp.ok) return burst_ws_bytes(bp, args->m, args->n, args->batch);
     return plan_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), false)
         .ws_bytes;
 }

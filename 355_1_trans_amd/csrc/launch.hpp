@@ -52,6 +52,12 @@ hipError_t launch_decode(SkinnyKind kind, const DecodeArgs& a, int mb, int nw, i
 // of B per MFMA; (wr, mb) in {(1,1), (2,2), (4,4), (4,8)})
 struct StreamArgs;
 hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batch, bool bf16, hipStream_t s);
+// kernels_burst.hip: burst kernel (fp8, fp32 block scales, M <= 64; mb row
+// blocks, nb 16-column blocks and 4, 8 or 16 waves per workgroup; frag: B''
+// instead of B')
+struct BurstArgs;
+hipError_t launch_burst(const BurstArgs& a, bool frag, int mb, int nb, int waves, int batch, bool bf16,
+                        hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);
