@@ -14,7 +14,10 @@ and launch on the current stream:
   (LBP host.cc:283-294), with ``ldsbypass_repack`` (GPU, from the K-panel
   B') and ``ldsbypass_pack_b`` (CPU, from raw B) to build B'';
 * ``gemm_a8w8_mxfp8`` -- MXFP8 TN GEMM (MX8 host.cc:96-122, 266-296);
-* ``gemm_a4w4_mxfp4`` -- MXFP4 A4W4 GEMM (MX4 host.cc:96-115, 201-216).
+* ``gemm_a4w4_mxfp4`` -- MXFP4 A4W4 GEMM (MX4 host.cc:96-115, 201-216);
+* ``gemm_a4w4`` -- MXFP4 with aiter's ``gemm_a4w4(..., bpreshuffle=True)``
+  operands: B in shuffle_weight(16,16) order, both scales in e8m0_shuffle
+  order (MX4 candidate_m10/gemm_a4w4_mxfp4_4wave_host.cc:194-250).
 
 There is no CPU fallback: every wrapper raises if the library is missing or
 the tensors are not on a GPU.
@@ -66,7 +69,14 @@ class LdsBypassKargs(ctypes.Structure):
     )
 
 
+class Mxfp4Kargs(ctypes.Structure):
+    """opus_gemm_mxfp4_scale_kargs: the 96-byte block plus grid_blocks."""
+
+    _fields_ = Kargs._fields_ + [("grid_blocks", ctypes.c_int)]
+
+
 assert ctypes.sizeof(Kargs) == 96
+assert Mxfp4Kargs.grid_blocks.offset == 96
 
 
 _V, _I = ctypes.c_void_p, ctypes.c_int
@@ -77,6 +87,7 @@ EXPORTS = {
     "gemm_a8w8_blockscale_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p,
                                                         ctypes.c_size_t, ctypes.c_void_p]),
     "gemm_a8w8_blockscale_bpreshuffle_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "gemm_a4w4_mxfp4_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_void_p]),
     "gemm_a8w8_mxfp8": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),
     "gemm_a8w8_mxfp8_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
@@ -254,6 +265,56 @@ def gemm_a4w4_mxfp4(A, B, A_scale, B_scale, dtype=torch.bfloat16, out=None, work
                                    ctypes.c_void_p(s.cuda_stream))
         _record(s, A, B, A_scale, B_scale, out, _ws_tensor(workspace))
     _check(st, "gemm_a4w4_mxfp4")
+    return out
+
+
+def _shuffled_scale(e, rows, kg, name):
+    """Bytes per 32-row block of an e8m0_shuffle'd scale tensor (rows padded
+    to 32, groups to 8; any shape with that many contiguous bytes)."""
+    kg8 = (kg + 7) // 8 * 8
+    need = (rows + 31) // 32 * 32 * kg8
+    if e.element_size() != 1 or not e.is_contiguous() or e.numel() < need:
+        raise ValueError(f"{name} must be contiguous e8m0_shuffle bytes, at least {need} of them")
+    return 32 * kg8
+
+
+def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, bpreshuffle=True, *,
+              dtype=None, grid_blocks=0):
+    """MXFP4 GEMM with aiter's gemm_a4w4 operand formats.
+
+    A [M, K/2] packed e2m1 (row-major); B [N, K/2] bytes in
+    shuffle_weight(16,16) order (``shuffle_weight_16x16``), N % 16 == 0;
+    A_scale / B_scale: E8M0 in e8m0_shuffle order (``e8m0_shuffle``, or
+    ``quant_mxfp4(x, shuffle=True)``), rows padded to 32; out [M, N], bf16
+    unless ``dtype`` (or a given ``out``) says fp32.  ``grid_blocks`` > 0 runs a persistent grid of that
+    many workgroups.  The epilogue has no bias or alpha/beta: anything but
+    the defaults raises, and so does bpreshuffle=False (row-major B goes
+    through gemm_a4w4_mxfp4)."""
+    if bias is not None or alpha != 1.0 or beta != 0.0:
+        raise NotImplementedError("gemm_a4w4: bias, alpha and beta are not supported")
+    if not bpreshuffle:
+        raise NotImplementedError("gemm_a4w4: row-major B goes through gemm_a4w4_mxfp4")
+    dev = _require_gpu(A, B, A_scale, B_scale)
+    if dtype is None:
+        dtype = out.dtype if out is not None else torch.bfloat16
+    m, kb = A.shape
+    k = 2 * kb
+    if B.dim() != 2 or B.shape[1] != kb or k % 256 or B.shape[0] % 16:
+        raise ValueError("requires B [N, K/2] with N % 16 == 0 and K % 256 == 0")
+    n = B.shape[0]
+    if not (A.is_contiguous() and B.is_contiguous()):
+        raise ValueError("A and B must be contiguous")
+    sfa = _shuffled_scale(A_scale, m, k // 32, "A_scale")
+    sfb = _shuffled_scale(B_scale, n, k // 32, "B_scale")
+    out = _out(out, (m, n), dtype, dev)
+    args = Mxfp4Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
+                      A_scale.data_ptr(), B_scale.data_ptr(), sfa, sfb, A_scale.numel(), B_scale.numel(),
+                      int(grid_blocks))
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        st = lib().gemm_a4w4_mxfp4_bpreshuffle(ctypes.byref(args), _out_code(dtype), ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B, A_scale, B_scale, out)
+    _check(st, "gemm_a4w4_mxfp4_bpreshuffle")
     return out
 
 

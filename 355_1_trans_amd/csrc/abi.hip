@@ -25,6 +25,7 @@ static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 by
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, ptr_sfa) == 64, "reference kargs ABI");
 static_assert(__builtin_offsetof(opus_gemm_scale_kargs, stride_sfa) == 80, "reference kargs ABI");
 static_assert(__builtin_offsetof(opus_gemm_ldsbypass_kargs, ptr_c) == 24, "ldsbypass kargs ABI");
+static_assert(__builtin_offsetof(opus_gemm_mxfp4_scale_kargs, grid_blocks) == 96, "mxfp4 kargs: common block first");
 
 namespace qg {
 
@@ -805,7 +806,56 @@ size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
     return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny || pl.mid ? 0 : scale_panel_bytes(*args)});
 }
 
-// ------------------------------------------------ MXFP4 without a caller workspace
+// ------------------------------------------------ MXFP4, aiter bpreshuffle operands
+hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream) {
+    qg::trace_reset();
+    if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
+        !flag01(out_dtype) || args->grid_blocks < 0)
+        return hipErrorInvalidValue;
+    const auto& x = *args;
+    if (x.m <= 0 || x.n <= 0 || x.k <= 0 || x.batch <= 0 || x.k % 256 || x.n % 16) return hipErrorInvalidValue;
+    const int kb = x.k / 2, rows32a = ceil_div(x.m, 32), rows32b = ceil_div(x.n, 32);
+    // e8m0_shuffle blocks: 32 rows x K/32 groups (K % 256 == 0: no group padding)
+    if (x.stride_a < kb || x.stride_b != kb || x.stride_c < x.n || x.stride_sfa < x.k || x.stride_sfb < x.k)
+        return hipErrorInvalidValue;
+    if (!aligned(x.ptr_a, 16) || !aligned(x.ptr_b, 16) || !aligned(x.ptr_sfa, 16) || !aligned(x.ptr_sfb, 16) ||
+        x.stride_a % 16 || x.stride_sfa % 16 || x.stride_sfb % 16)
+        return hipErrorInvalidValue;
+    const long long outb = out_dtype ? 2 : 4;
+    if (!aligned(x.ptr_c, (uintptr_t)outb)) return hipErrorInvalidValue;
+    if (x.batch > 1 &&
+        ((long long)x.stride_a_batch < (long long)x.m * x.stride_a || x.stride_a_batch % 16 ||
+         (long long)x.stride_b_batch < (long long)x.n * kb || x.stride_b_batch % 16 ||
+         (long long)x.stride_c_batch < (long long)x.m * x.stride_c ||
+         (long long)x.stride_sfa_batch < (long long)rows32a * x.stride_sfa || x.stride_sfa_batch % 16 ||
+         (long long)x.stride_sfb_batch < (long long)rows32b * x.stride_sfb || x.stride_sfb_batch % 16))
+        return hipErrorInvalidValue;
+    if (!bounded_count(x.m, x.stride_a, 1, 1) || !bounded_count(x.n, kb, 1, 1) ||
+        !bounded_count(x.m, x.stride_c, 1, outb) || !bounded_count(rows32a, x.stride_sfa, 1, 1) ||
+        !bounded_count(rows32b, x.stride_sfb, 1, 1))
+        return hipErrorInvalidValue;
+    Spans sp;
+    sp.add(x.ptr_c, span(x.batch, x.stride_c_batch, x.m, x.stride_c, x.n, outb));
+    sp.add(x.ptr_a, span(x.batch, x.stride_a_batch, x.m, x.stride_a, kb, 1));
+    sp.add(x.ptr_b, span(x.batch, x.stride_b_batch, 1, 0, (long long)x.n * kb, 1));
+    sp.add(x.ptr_sfa, span(x.batch, x.stride_sfa_batch, rows32a, x.stride_sfa, x.k, 1));
+    sp.add(x.ptr_sfb, span(x.batch, x.stride_sfb_batch, rows32b, x.stride_sfb, x.k, 1));
+    if (sp.overlap_any(sp.p[0], sp.bytes[0], 1)) return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    opus_gemm_scale_kargs a{};
+    std::memcpy(&a, &x, sizeof(a));    // the leading 96 bytes are the common block
+    TileArgs t{};
+    fill_common(t, a, kb, (int)outb);
+    t.sfa_sm = x.stride_sfa;
+    t.sfb_sn = x.stride_sfb;
+    t.sfa_sk = t.sfb_sk = 256;
+    const long long tiles = (long long)t.tiles_m * t.tiles_n * x.batch;
+    const int blocks = x.grid_blocks > 0 ? (int)std::min<long long>(x.grid_blocks, tiles) : 0;
+    // 4 K-tiles of scales per DMA when they come whole (K % 1024 == 0)
+    return qg::launch_wide_mx4_w16s(t, x.batch, out_dtype == QGEMM_OUT_BF16, x.k % 1024 == 0 ? 32 : 8, blocks, stream);
+}
+
 }  // extern "C"
 
 namespace {

@@ -15,6 +15,17 @@ hipError_t launch_wide(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
                  bf16 ? "bf16" : "fp32", PB);
     return hipGetLastError();
 }
+// persistent grid of `blocks` workgroups (a.persist = 1, a.batch set)
+template <int FMT, ScaleKind SK, BLay BL, int PB>
+hipError_t launch_wide_persist(const TileArgs& a, int blocks, bool bf16, hipStream_t s) {
+    const dim3 grid(blocks, 1, 1);
+    const dim3 block(256);
+    if (bf16) wide_gemm_kernel<FMT, SK, BL, true, PB, true><<<grid, block, 0, s>>>(a);
+    else wide_gemm_kernel<FMT, SK, BL, false, PB, true><<<grid, block, 0, s>>>(a);
+    trace_launch("wide_gemm<%s,%s,%s,%s,pb%d,persist%d>", FMT == kFmtFp4 ? "fp4" : "fp8", scale_name(SK),
+                 layout_name(BL), bf16 ? "bf16" : "fp32", PB, blocks);
+    return hipGetLastError();
+}
 }  // namespace
 
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s) {
@@ -25,6 +36,19 @@ hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int pane
     if (panel_bytes == 32) return launch_wide<kFmtFp4, ScaleKind::MX, BLay::RAW, 32>(a, batch, bf16, s);
     if (panel_bytes == 16) return launch_wide<kFmtFp4, ScaleKind::MX, BLay::RAW, 16>(a, batch, bf16, s);
     return launch_wide<kFmtFp4, ScaleKind::MX, BLay::RAW, 8>(a, batch, bf16, s);
+}
+hipError_t launch_wide_mx4_w16s(const TileArgs& a, int batch, bool bf16, int panel_bytes, int persist_blocks,
+                                hipStream_t s) {
+    if (persist_blocks > 0) {
+        TileArgs t = a;
+        t.persist = 1;
+        t.batch = batch;
+        if (panel_bytes == 32)
+            return launch_wide_persist<kFmtFp4, ScaleKind::MXS, BLay::W16, 32>(t, persist_blocks, bf16, s);
+        return launch_wide_persist<kFmtFp4, ScaleKind::MXS, BLay::W16, 8>(t, persist_blocks, bf16, s);
+    }
+    if (panel_bytes == 32) return launch_wide<kFmtFp4, ScaleKind::MXS, BLay::W16, 32>(a, batch, bf16, s);
+    return launch_wide<kFmtFp4, ScaleKind::MXS, BLay::W16, 8>(a, batch, bf16, s);
 }
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::W16>(a, batch, bf16, s);

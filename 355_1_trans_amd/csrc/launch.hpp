@@ -21,6 +21,11 @@ hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipS
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s);
 // panel_bytes: MX4 scale panel width, 32, 16 or 8 bytes per row
 hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s);
+// MXFP4 in aiter's bpreshuffle formats: B shuffle_weight(16,16), scales
+// e8m0_shuffle (sfa_sm / sfb_sn = bytes per 32-row block, sfa_sk = sfb_sk =
+// 256); panel_bytes 32 (K % 1024 == 0) or 8; persist_blocks > 0: persistent grid
+hipError_t launch_wide_mx4_w16s(const TileArgs& a, int batch, bool bf16, int panel_bytes, int persist_blocks,
+                                hipStream_t s);
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // E8M0 scales of A and B into the wide kernel's panel-major layout
 // [ngroups/pb][rows][pb] (pb = 16 or 32 bytes, ngroups % pb == 0)

@@ -11,6 +11,11 @@
 //   BS8   one E8M0 per 128 K elements: SFA column-major [K/128][M], SFB
 //         [N/128][K/128] (SNAP gemm_a8w8_mxfp8_scale_common.h:28-35), broadcast
 //         to the four 32-element lane groups in the matrix core.
+//   MXS   the MX scales in aiter's e8m0_shuffle order (MX4 candidate_m10/
+//         gemm_a4w4_mxfp4_4wave_host.cc:194-208): per 32-row block and 8-group
+//         K-tile 256 contiguous bytes, byte (g%4)*64 + (r%16)*4 + (g/4)*2 + r/16,
+//         so one dword read gives a lane the scales of two fp4 sub-tiles; the
+//         blocks' K-tiles are contiguous, so the tile kernel DMAs them as they lie.
 //   BSF32 fp32 scales per 1x128 (A) and 128x128 (B) block (BPS host.cc:66-90):
 //         the MFMA runs unscaled (E8M0 127 = 1.0) into a fresh fp32 partial
 //         and the VALU adds partial * (sfa*sfb) into the accumulator, the
@@ -24,11 +29,11 @@
 
 namespace qg {
 
-enum class ScaleKind : int { MX = 0, BS8 = 1, BSF32 = 2 };
+enum class ScaleKind : int { MX = 0, BS8 = 1, BSF32 = 2, MXS = 3 };
 enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2, FRAG = 3 };
 
 constexpr const char* scale_name(ScaleKind k) {
-    return k == ScaleKind::MX ? "MX" : k == ScaleKind::BS8 ? "BS8" : "BSF32";
+    return k == ScaleKind::MX ? "MX" : k == ScaleKind::BS8 ? "BS8" : k == ScaleKind::MXS ? "MXS" : "BSF32";
 }
 constexpr const char* layout_name(BLay l) {
     return l == BLay::RAW ? "RAW" : l == BLay::KPANEL ? "KPANEL" : l == BLay::W16 ? "W16" : "FRAG";
@@ -52,6 +57,7 @@ struct TileArgs {
     //           wide kernel also reads a panel-major copy (sfa_sk / sfb_sk below)
     //   BS8   : sfa(m, kt) = sfa[kt*sfa_sk + m], sfb(nb, kt) = sfb[nb*sfb_sn + kt]
     //   BSF32 : sfa(m, kt) = sfa[kt*sfa_sk + m*sfa_sm], sfb(nb, kt) = sfb[nb*sfb_sn + kt]
+    //   MXS   : K-tile kt of 32-row block rb at sfa[rb*sfa_sm + 256*kt] (sfb: sfb_sn)
     int sfa_sm, sfa_sk, sfb_sn;
     // MX, wide kernel: bytes from one K-tile's scales to the next (KT_BYTES =
     // 4 (fp8) or 8 (fp4) row-major; rows * KT_BYTES in the panel-major copy
@@ -60,6 +66,9 @@ struct TileArgs {
     int tiles_m, tiles_n;
     int group_m;         // tile-rows per raster group
     int unit_scale;      // E8M0 127, passed at run time
+    int batch;           // batch count (the persistent tile kernel walks batch x tiles)
+    int persist;         // wide kernel: 1 = persistent grid (each workgroup walks the tile
+                         // list with stride gridDim.x), 0 = one tile per workgroup
 };
 
 }  // namespace qg

@@ -25,6 +25,8 @@
 //    t+2 issued in quadrant 2), so the DMA queue never runs empty;
 //  * DMAs go through buffer descriptors whose range is empty past the last
 //    K-tile, so the steady-state code has no branches around them.
+//  * PERSIST: a grid of about one workgroup per CU, each walking the tile
+//    list (aiter's persistent grid_blocks mode); otherwise one tile each.
 //
 // Register layouts of the two MFMAs (pinned by the layout probes,
 // csrc/probe.hip; srcA = B rows, srcB = A rows):
@@ -98,18 +100,22 @@ __device__ __forceinline__ void mfma_fp4(f32x16& acc, const i32x4& b, const i32x
 }
 }  // namespace wide
 
-template <int FMT, ScaleKind SK, BLay BL, bool BF16, int PB = 16>
+template <int FMT, ScaleKind SK, BLay BL, bool BF16, int PB = 16, bool PERSIST = false>
 __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     constexpr bool FP4 = (FMT == kFmtFp4);
-    static_assert(SK != ScaleKind::BSF32 && (!FP4 || SK == ScaleKind::MX), "MFMA-applied scales");
-    constexpr bool MX = (SK == ScaleKind::MX);
+    // MXS (e8m0_shuffle scales) goes with fp4 and shuffle_weight(16,16) B:
+    // aiter's gemm_a4w4 bpreshuffle operands
+    constexpr bool MXS = (SK == ScaleKind::MXS);
+    static_assert(SK != ScaleKind::BSF32 && (!FP4 || SK == ScaleKind::MX || MXS), "MFMA-applied scales");
+    static_assert(!MXS || (FP4 && BL == BLay::W16 && (PB == 32 || PB == 8)), "shuffled scales: fp4, W16 B");
+    constexpr bool MX = (SK == ScaleKind::MX) || MXS;
     constexpr int BKB = 128, BM = 256;
     constexpr int RB = FP4 ? 32 : 16;          // rows per MFMA block
     constexpr int NBLK = 128 / RB;             // blocks per wave and operand
     constexpr int KT_BYTES = FP4 ? 8 : 4;      // MX scale bytes per row per K-tile
     static_assert(PB == 16 || PB == 32 || PB == KT_BYTES, "panel width");
     constexpr bool WIDE = PB >= 16;               // [row][PB] panels of whole 16-byte pieces
-    constexpr int SPAN = MX ? PB / KT_BYTES : 1;  // K-tiles per scale DMA
+    constexpr int SPAN = MX ? PB / KT_BYTES : 1;  // K-tiles per scale DMA (MXS: 4 or 1)
     constexpr int PANEL = 256 * (PB > 16 ? PB : 16);
     // BS8: a 256-byte SFA slot per stage, then the landing slots of the no-op
     // SFA DMAs of waves 1-3 (an empty-range buffer DMA still writes zeros to
@@ -129,437 +135,508 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     __shared__ __attribute__((aligned(256))) uint8_t lSA[SA_BYTES];
     __shared__ __attribute__((aligned(256))) uint8_t lSB[SB_BYTES];
 
-    // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
+    // ---- tile loop: one tile per workgroup (grid = tiles x batch), or with
+    // PERSIST each workgroup walks the batch x tiles list with stride
+    // gridDim.x.  Tile ids go through an XCD-contiguous remap (workgroup b
+    // runs on XCD b % 8; with a grid that is a multiple of 8 the tiles an XCD
+    // holds at one time stay neighbours), then a grouped raster. ----
     const int T = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
-    if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
-    const int gfull = p.group_m * p.tiles_n;
-    const int gi = bid / gfull;
-    const int first_m = gi * p.group_m;
-    const int gm = min(p.tiles_m - first_m, p.group_m);
-    const int within = bid - gi * gfull;
-    const int tm = first_m + within % gm;
-    const int tn = within / gm;
-    const int bz = blockIdx.z;
-    const int m0 = tm * BM, n0 = tn * BM;
+    const int total = PERSIST ? T * p.batch : 1;
+    for (int it = PERSIST ? (int)blockIdx.x : 0; it < total; it += PERSIST ? (int)gridDim.x : 1) {
+        // the previous tile's epilogue read its C image from the operand
+        // stages and left stores in flight: drain both before the DMAs
+        if (PERSIST && it != (int)blockIdx.x) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int bz = PERSIST ? it / T : (int)blockIdx.z;
+        int bid = PERSIST ? it - bz * T : (int)blockIdx.x;
+        if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
+        const int gfull = p.group_m * p.tiles_n;
+        const int gi = bid / gfull;
+        const int first_m = gi * p.group_m;
+        const int gm = min(p.tiles_m - first_m, p.group_m);
+        const int within = bid - gi * gfull;
+        const int tm = first_m + within % gm;
+        const int tn = within / gm;
+        const int m0 = tm * BM, n0 = tn * BM;
 
-    const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
-    const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
-    // MX: bytes from one K-tile's scales to the next along K -- KT_BYTES in
-    // the callers' row-major [rows][K/32], rows * KT_BYTES in the panel-major
-    // copy [K/32/PB][rows][PB] (row pitch PB), whose panel DMAs read 1 KB
-    // contiguously instead of one cache line per row
-    const int SFA_KT = MX ? SFA_SK : 0, SFB_KT = MX ? p.sfb_sk : 0;
+        const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
+        const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
+        // MX: bytes from one K-tile's scales to the next along K -- KT_BYTES in
+        // the callers' row-major [rows][K/32], rows * KT_BYTES in the panel-major
+        // copy [K/32/PB][rows][PB] (row pitch PB), whose panel DMAs read 1 KB
+        // contiguously instead of one cache line per row
+        const int SFA_KT = MX ? SFA_SK : 0, SFB_KT = MX ? p.sfb_sk : 0;
 
-    const int tid = threadIdx.x;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
-    const int wm = w >> 1, wn = w & 1;
+        int tid = threadIdx.x;
+        // persistent loop: an opaque copy per tile keeps the lane offsets
+        // derived from tid out of loop-invariant code motion, whose hoisted
+        // values would stay live across the whole K loop
+        if constexpr (PERSIST) asm volatile("" : "+v"(tid));
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
+        const int wm = w >> 1, wn = w & 1;
 
-    const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
-    const uint8_t* B = p.b + bz * p.b_batch +
-                       (BL == BLay::RAW ? (long long)n0 * LDB
-                                        : BL == BLay::KPANEL ? (long long)n0 * BKB : (long long)(n0 >> 4) * 16 * KB);
-    const uint8_t* SFA = p.sfa + bz * p.sfa_batch;
-    const uint8_t* SFB = p.sfb + bz * p.sfb_batch;
+        const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
+        const uint8_t* B = p.b + bz * p.b_batch +
+                           (BL == BLay::RAW ? (long long)n0 * LDB
+                                            : BL == BLay::KPANEL ? (long long)n0 * BKB : (long long)(n0 >> 4) * 16 * KB);
+        const uint8_t* SFA = p.sfa + bz * p.sfa_batch;
+        const uint8_t* SFB = p.sfb + bz * p.sfb_batch;
 
-    // ---- per-lane DMA offsets: wave w fills rows [64w, 64w + 64) of A and
-    // B, eight 8-row DMAs each; lane L writes row +L/8, physical chunk L%8 =
-    // logical chunk (L%8) ^ swizzle(row).  B in shuffle_weight(16,16) order
-    // (W16) instead moves whole 16-row blocks as is: a block's K-tile is 2 KB
-    // contiguous ([8 chunks][16 rows][16 B], already the 16x16x128 operand
-    // order), two linear 1 KB DMAs, read back linearly.  (Gathering W16 into
-    // 128-byte rows made every lane of a DMA hit a different cache line:
-    // 18% more cycles per K-tile.) ----
-    int aoff[8], boff[8];
+        // ---- per-lane DMA offsets: wave w fills rows [64w, 64w + 64) of A and
+        // B, eight 8-row DMAs each; lane L writes row +L/8, physical chunk L%8 =
+        // logical chunk (L%8) ^ swizzle(row).  B in shuffle_weight(16,16) order
+        // (W16) instead moves whole 16-row blocks as is: a block's K-tile is 2 KB
+        // contiguous ([8 chunks][16 rows][16 B], already the 16x16x128 operand
+        // order), two linear 1 KB DMAs, read back linearly.  (Gathering W16 into
+        // 128-byte rows made every lane of a DMA hit a different cache line:
+        // 18% more cycles per K-tile.) ----
+        int aoff[8], boff[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int r = (w * 8 + t) * 8 + (L >> 3);
-        const int c = (L & 7) ^ (FP4 ? ((r >> 1) & 7) : (r & 7));
-        aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
-        const int gn = min(n0 + r, N - 1) - n0;
-        if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
-        else if constexpr (BL == BLay::KPANEL) boff[t] = gn * BKB + c * 16;
-        else {
-            const int blk = min((n0 >> 4) + w * 4 + (t >> 1), ((N + 15) >> 4) - 1) - (n0 >> 4);
-            boff[t] = blk * 16 * KB + (t & 1) * 1024 + L * 16;
+        for (int t = 0; t < 8; ++t) {
+            const int r = (w * 8 + t) * 8 + (L >> 3);
+            const int c = (L & 7) ^ (FP4 ? ((r >> 1) & 7) : (r & 7));
+            aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
+            const int gn = min(n0 + r, N - 1) - n0;
+            if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
+            else if constexpr (BL == BLay::KPANEL) boff[t] = gn * BKB + c * 16;
+            else {
+                const int blk = min((n0 >> 4) + w * 4 + (t >> 1), ((N + 15) >> 4) - 1) - (n0 >> 4);
+                boff[t] = blk * 16 * KB + (t & 1) * 1024 + L * 16;
+            }
         }
-    }
 
-    // ---- scale sources (buffer DMAs; empty range = no-op) ----
-    // MX panels: wave w moves the panel rows of A quarter w and B quarter w:
-    // lane L = row 64w + L (PB <= 16), or with 32-byte panels two lanes per
-    // row (row 64w + 32u + L/2, 16-byte half L%2, DMA u = 0, 1), so that a
-    // DMA touches 32 cache lines instead of 64
-    const uint8_t* SFA_t = SFA + (long long)m0 * (MX ? SFA_SM : 1);
-    const uint8_t* SFB_t = SFB + (MX ? (long long)n0 * SFB_SN : 0ll);
-    int mx_voff_a[2], mx_voff_b[2];
+        // ---- scale sources (buffer DMAs; empty range = no-op) ----
+        // MX panels: wave w moves the panel rows of A quarter w and B quarter w:
+        // lane L = row 64w + L (PB <= 16), or with 32-byte panels two lanes per
+        // row (row 64w + 32u + L/2, 16-byte half L%2, DMA u = 0, 1), so that a
+        // DMA touches 32 cache lines instead of 64
+        // MXS: the tile's eight 32-row blocks per operand, each block's K-tile
+        // 256 contiguous bytes: with PB = 32 four K-tiles (1 KB) per block and
+        // DMA, wave w moving blocks 2w + u; with PB = 8 one K-tile, waves 0-1
+        // moving A's blocks 4(w%2) + L/16 and waves 2-3 B's.  Blocks past the
+        // last row re-read the last block (the buffer holds ceil(rows/32)).
+        const uint8_t* SFA_t = SFA + (MXS ? (long long)(m0 >> 5) * SFA_SM : (long long)m0 * (MX ? SFA_SM : 1));
+        const uint8_t* SFB_t = SFB + (MXS ? (long long)(n0 >> 5) * SFB_SN : MX ? (long long)n0 * SFB_SN : 0ll);
+        int mx_voff_a[2], mx_voff_b[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int r = PB == 32 ? w * 64 + 32 * u + (L >> 1) : w * 64 + L;
-        const int h = PB == 32 ? (L & 1) * 16 : 0;
-        mx_voff_a[u] = (min(m0 + r, M - 1) - m0) * SFA_SM + h;
-        mx_voff_b[u] = (min(n0 + r, N - 1) - n0) * SFB_SN + h;
-    }
-    // BS8: SFA's 256 row bytes of a K-tile by wave 0; SFB's byte of the
-    // wave's 128-column block as the aligned dword holding it
-    const long long bs_b_idx = (long long)min((n0 >> 7) + wn, (N - 1) >> 7) * SFB_SN;
-
-    QG_LDS uint8_t* pA0 = (QG_LDS uint8_t*)lA0;
-    QG_LDS uint8_t* pA1 = (QG_LDS uint8_t*)lA1;
-    QG_LDS uint8_t* pB0 = (QG_LDS uint8_t*)lB0;
-    QG_LDS uint8_t* pB1 = (QG_LDS uint8_t*)lB1;
-    QG_LDS uint8_t* pSA = (QG_LDS uint8_t*)lSA;
-    QG_LDS uint8_t* pSB = (QG_LDS uint8_t*)lSB;
-
-    const int nk = KB / BKB;
-
-    auto rsrc = [&](const uint8_t* base, bool valid) __attribute__((always_inline)) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
-                                                 0x00020000);
-    };
-    auto b_ktile = [&](int kt) __attribute__((always_inline)) -> const uint8_t* {
-        if constexpr (BL == BLay::RAW) return B + kt * BKB;
-        else if constexpr (BL == BLay::KPANEL) return B + (long long)kt * N * BKB;
-        else return B + kt * 2048;
-    };
-    auto dma_a = [&](int kt, bool valid, QG_LDS uint8_t* sA) __attribute__((always_inline)) {
-        const auto r = rsrc(A + kt * BKB, valid);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) dma16_buf(r, sA + (w * 8 + t) * 8 * BKB, aoff[t], 0);
-    };
-    auto dma_b = [&](int kt, bool valid, QG_LDS uint8_t* sB) __attribute__((always_inline)) {
-        const auto r = rsrc(b_ktile(kt), valid);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) dma16_buf(r, sB + (w * 8 + t) * 8 * BKB, boff[t], 0);
-    };
-    // scale DMAs that go with K-tile kt (MX: only when kt starts a panel,
-    // which the callers know at compile time); `valid` false = no-op DMAs.
-    // MX panel images: PB = 16, 32: [row][PB]; PB = 4 (fp8): [row][4 B];
-    // PB = 8 (fp4): [2 halves][row][4 B]
-    auto dma_scales = [&](int kt, bool valid) __attribute__((always_inline)) {
-        if constexpr (MX) {
-            const int buf = ((kt / SPAN) & 1) * PANEL;
-            const auto ra = rsrc(SFA_t + (long long)kt * SFA_KT, valid);
-            const auto rb = rsrc(SFB_t + (long long)kt * SFB_KT, valid);
-            if constexpr (PB == 32) {
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    dma16_buf(ra, pSA + buf + w * 2048 + u * 1024, mx_voff_a[u], 0);
-                    dma16_buf(rb, pSB + buf + w * 2048 + u * 1024, mx_voff_b[u], 0);
-                }
-            } else if constexpr (PB == 16) {
-                dma16_buf(ra, pSA + buf + w * 1024, mx_voff_a[0], 0);
-                dma16_buf(rb, pSB + buf + w * 1024, mx_voff_b[0], 0);
+        for (int u = 0; u < 2; ++u) {
+            if constexpr (MXS) {
+                const int j = PB == 32 ? 2 * w + u : 4 * (w & 1) + (L >> 4);
+                const int off = PB == 32 ? L * 16 : (L & 15) * 16;
+                mx_voff_a[u] = (min((m0 >> 5) + j, ((M + 31) >> 5) - 1) - (m0 >> 5)) * SFA_SM + off;
+                mx_voff_b[u] = (min((n0 >> 5) + j, ((N + 31) >> 5) - 1) - (n0 >> 5)) * SFB_SN + off;
             } else {
-                dma4_buf(ra, pSA + buf + w * 256, mx_voff_a[0], 0);
-                dma4_buf(rb, pSB + buf + w * 256, mx_voff_b[0], 0);
-                if constexpr (PB == 8) {
-                    dma4_buf(ra, pSA + buf + 1024 + w * 256, mx_voff_a[0] + 4, 0);
-                    dma4_buf(rb, pSB + buf + 1024 + w * 256, mx_voff_b[0] + 4, 0);
-                }
-            }
-        } else {
-            const int st = kt & 1;
-            const auto ra = rsrc(SFA_t + (long long)kt * SFA_SK, valid && w == 0);
-            const auto rb = rsrc(SFB + ((bs_b_idx + kt) & ~3ll), valid);
-            dma4_buf(ra, w == 0 ? pSA + st * 256 : pSA + 256 + w * 256, 4 * L, 0);
-            dma4_buf(rb, pSB + st * 1024 + w * 256, 0, 0);
-        }
-    };
-    // Scale registers of K-tile kt, x = 0..7 (A and B rows of the wave):
-    //  fp8: block x's byte for lane group q (sa[x], sb[x]); BS8 has one B
-    //       scale per wave, read with x = 0;
-    //  fp4: block x/2, word x%2, which holds the lane group's blocks of
-    //       instructions 2(x%2) (byte 0) and 2(x%2)+1 (byte 2) once
-    //       finish_scale has shifted the lane group's bytes down.  The shift
-    //       is a separate step, issued a few MFMAs after the read, so the
-    //       wave does not stall on the LDS latency.
-    const int q = L >> 4, l16 = L & 15, g = L >> 5, l32 = L & 31;
-    auto read_scale = [&](int kt, int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
-        if constexpr (MX && !FP4) {
-            const int buf = ((kt / SPAN) & 1) * PANEL;
-            const int col = WIDE ? (kt % SPAN) * KT_BYTES + q : q;
-            sa[x] = pSA[buf + (wm * 128 + x * 16 + l16) * PB + col];
-            sb[x] = pSB[buf + (wn * 128 + x * 16 + l16) * PB + col];
-        } else if constexpr (MX) {
-            const int buf = ((kt / SPAN) & 1) * PANEL;
-            const int ra = wm * 128 + (x >> 1) * 32 + l32, rb = wn * 128 + (x >> 1) * 32 + l32;
-            if constexpr (WIDE) {
-                // both words of the block in one read (x even; x odd is a no-op)
-                if ((x & 1) == 0) {
-                    const i32x2 va = *(const QG_LDS i32x2*)(pSA + buf + ra * PB + (kt % SPAN) * KT_BYTES);
-                    const i32x2 vb = *(const QG_LDS i32x2*)(pSB + buf + rb * PB + (kt % SPAN) * KT_BYTES);
-                    sa[x] = va[0];
-                    sa[x + 1] = va[1];
-                    sb[x] = vb[0];
-                    sb[x + 1] = vb[1];
-                }
-            } else {
-                sa[x] = (int)*(const QG_LDS uint32_t*)(pSA + buf + (x & 1) * 1024 + ra * 4);
-                sb[x] = (int)*(const QG_LDS uint32_t*)(pSB + buf + (x & 1) * 1024 + rb * 4);
-            }
-        } else {
-            const int st = kt & 1;
-            sa[x] = pSA[st * 256 + wm * 128 + x * 16 + l16];
-            if (x == 0) {
-                const int v = pSB[st * 1024 + w * 256 + (int)((bs_b_idx + kt) & 3)];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) sb[j] = v;
+                const int r = PB == 32 ? w * 64 + 32 * u + (L >> 1) : w * 64 + L;
+                const int h = PB == 32 ? (L & 1) * 16 : 0;
+                mx_voff_a[u] = (min(m0 + r, M - 1) - m0) * SFA_SM + h;
+                mx_voff_b[u] = (min(n0 + r, N - 1) - n0) * SFB_SN + h;
             }
         }
-    };
-    auto finish_scale = [&](int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
-        if constexpr (FP4) {
-            sa[x] = (int)((uint32_t)sa[x] >> (8 * g));
-            sb[x] = (int)((uint32_t)sb[x] >> (8 * g));
-        }
-    };
+        // BS8: SFA's 256 row bytes of a K-tile by wave 0; SFB's byte of the
+        // wave's 128-column block as the aligned dword holding it
+        const long long bs_b_idx = (long long)min((n0 >> 7) + wn, (N - 1) >> 7) * SFB_SN;
 
-    // per-lane operand read offsets: fp8 chunks q and q+4 of row l16 of a
-    // 16-row block; fp4 chunk 2s+g of row l32 of a 32-row block
-    const int rd8 = l16 * BKB + ((q ^ (l16 & 7)) << 4);
-    auto rd4 = [&](int s) __attribute__((always_inline)) {
-        return l32 * BKB + (((2 * s + g) ^ ((l32 >> 1) & 7)) << 4);
-    };
+        QG_LDS uint8_t* pA0 = (QG_LDS uint8_t*)lA0;
+        QG_LDS uint8_t* pA1 = (QG_LDS uint8_t*)lA1;
+        QG_LDS uint8_t* pB0 = (QG_LDS uint8_t*)lB0;
+        QG_LDS uint8_t* pB1 = (QG_LDS uint8_t*)lB1;
+        QG_LDS uint8_t* pSA = (QG_LDS uint8_t*)lSA;
+        QG_LDS uint8_t* pSB = (QG_LDS uint8_t*)lSB;
 
-    Acc acc[NBLK][NBLK];
-#pragma unroll
-    for (int i = 0; i < NBLK; ++i)
-#pragma unroll
-        for (int j = 0; j < NBLK; ++j)
-#pragma unroll
-            for (int v = 0; v < (FP4 ? 16 : 4); ++v) acc[i][j][v] = 0.f;
-    Frag ah[2][NF], bh[2][NF];
+        const int nk = KB / BKB;
 
-    // read unit x (0..3) of register half h of A (is_a) or B: two
-    // ds_read_b128 -- fp8: the 16-row block x; fp4: sub-tiles 2(x%2) and
-    // 2(x%2)+1 of the 32-row block x/2
-    auto read_one = [&](bool is_a, int h, int x, const QG_LDS uint8_t* sA,
-                        const QG_LDS uint8_t* sB) __attribute__((always_inline)) {
-        const QG_LDS uint8_t* base = is_a ? sA + wm * 128 * BKB : sB + wn * 128 * BKB;
-        Frag(&dst)[2][NF] = is_a ? ah : bh;
-        if constexpr (FP4) {
-            const QG_LDS uint8_t* blk = base + (2 * h + (x >> 1)) * 32 * BKB;
-            const int s0 = 2 * (x & 1);
-            dst[h][4 * (x >> 1) + s0] = *(const QG_LDS i32x4*)(blk + rd4(s0));
-            dst[h][4 * (x >> 1) + s0 + 1] = *(const QG_LDS i32x4*)(blk + rd4(s0 + 1));
-        } else {
-            const QG_LDS uint8_t* blk = base + (4 * h + x) * 16 * BKB;
-            const bool lin = BL == BLay::W16 && !is_a;    // W16 blocks: operand order
-            const i32x4 lo = *(const QG_LDS i32x4*)(blk + (lin ? L * 16 : rd8));
-            const i32x4 hi = *(const QG_LDS i32x4*)(blk + (lin ? 1024 + L * 16 : rd8 ^ 64));
-            dst[h][x] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-    };
-    // quadrant (ha, hb): 16 MFMAs; after MFMA k, fill(k) issues this step's
-    // share of LDS reads and DMAs.  Each step is fenced so the order stays
-    // as written: the LDS reads and DMAs spread between MFMAs, and no read
-    // of a register half moves above the last MFMA that uses its old rows.
-    // fp4 walks the 4 sub-tiles outermost, so consecutive MFMAs never chain
-    // on one accumulator.
-    auto quadrant = [&](int ha, int hb, const int (&sa)[8], const int (&sb)[8],
-                        auto&& fill) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            if constexpr (FP4) {
-                const int s = k >> 2, bi = (k >> 1) & 1, bj = k & 1;
-                const int i = 2 * ha + bi, j = 2 * hb + bj;
-                if (s & 1)
-                    wide::mfma_fp4<true>(acc[i][j], bh[hb][4 * bj + s], ah[ha][4 * bi + s], sb[2 * j + (s >> 1)],
-                                         sa[2 * i + (s >> 1)]);
-                else
-                    wide::mfma_fp4<false>(acc[i][j], bh[hb][4 * bj + s], ah[ha][4 * bi + s], sb[2 * j + (s >> 1)],
-                                          sa[2 * i + (s >> 1)]);
-            } else {
-                const int i = k >> 2, j = k & 3;
-                wide::mfma_fp8(acc[4 * ha + i][4 * hb + j], bh[hb][j], ah[ha][i], sb[4 * hb + j], sa[4 * ha + i]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            fill(k);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    // One K-tile t in phase P = t % 4 (LDS stage P & 1 holds t and then
-    // t + 2).  sa/sb: this K-tile's scales; san/sbn receive K-tile t + 1's.
-    auto ktile = [&](auto PC, int t, const int (&sa)[8], const int (&sb)[8], int (&san)[8],
-                     int (&sbn)[8]) __attribute__((always_inline)) {
-        constexpr int P = decltype(PC)::value;
-        QG_LDS uint8_t* sA = (P & 1) ? pA1 : pA0;
-        QG_LDS uint8_t* sB = (P & 1) ? pB1 : pB0;
-        QG_LDS uint8_t* nA = (P & 1) ? pA0 : pA1;
-        QG_LDS uint8_t* nB = (P & 1) ? pB0 : pB1;
-        constexpr bool r1a = wide::shared_is_a(P, 1), r2a = wide::shared_is_a(P, 2), r0a = wide::shared_is_a(P, 0);
-        constexpr int r1 = wide::shared_half(P, 1), r2 = wide::shared_half(P, 2), r0 = wide::shared_half(P, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        // quadrant 1: K-tile t's two halves freed at the end of the previous
-        // K-tile, one read unit after each of the first 8 MFMAs
-        quadrant(wide::qa(P), wide::qb(P), sa, sb, [&](int k) __attribute__((always_inline)) {
-            if (k < 4) read_one(r1a, r1, k, sA, sB);
-            else if (k < 8) read_one(r2a, r2, k - 4, sA, sB);
-        });
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1: stage P&1 is free
-        // quadrants 2-4: the 16 operand DMAs of K-tile t + 2 (A rows 0-7,
-        // then B rows 0-7, in 8-row groups) into this K-tile's stage, one
-        // after every third MFMA, so the CU's texture path is never asked
-        // for more than it streams (a wave blocks on a DMA it cannot queue);
-        // the scale DMAs go first, so B2's vmcnt covers them
-        const bool more = t + 2 < nk;
-        if constexpr ((P + 2) % SPAN == 0) dma_scales(t + 2, more);
-        const auto rA = rsrc(A + (t + 2) * BKB, more);
-        const auto rB = rsrc(b_ktile(t + 2), more);
-        auto dma_op = [&](int d) __attribute__((always_inline)) {
-            if (d < 8) dma16_buf(rA, sA + (w * 8 + d) * 8 * BKB, aoff[d], 0);
-            else dma16_buf(rB, sB + (w * 8 + d - 8) * 8 * BKB, boff[d - 8], 0);
+        auto rsrc = [&](const uint8_t* base, bool valid) __attribute__((always_inline)) {
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
+                                                     0x00020000);
         };
-        // quadrant 2: DMAs 0-5
-        quadrant(wide::qa(P + 1), wide::qb(P + 1), sa, sb, [&](int k) __attribute__((always_inline)) {
-            if (k % 3 == 0) dma_op(k / 3);
-        });
-        asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");  // B2: K-tile t + 1 landed
-        // quadrant 3: DMAs 6-10; first half of t + 1
-        quadrant(wide::qa(P + 2), wide::qb(P + 2), sa, sb, [&](int k) __attribute__((always_inline)) {
-            if (k % 3 == 2) dma_op(6 + k / 3);
-            if (k < 8 && (k & 1) == 0) read_one(r0a, r0, k >> 1, nA, nB);
-        });
-        // quadrant 4: DMAs 11-15; second half and scales of t + 1
-        quadrant(wide::qa(P + 3), wide::qb(P + 3), sa, sb, [&](int k) __attribute__((always_inline)) {
-            if (k % 3 == 1) dma_op(11 + k / 3);
-            if (k < 4) read_one(r1a, r1, k, nA, nB);
-            if (k < 8) read_scale(t + 1, k, san, sbn);
-            else finish_scale(k - 8, san, sbn);
-        });
-    };
-
-    // ---- prologue: DMA K-tiles 0 and 1 (scales of 1 first, so vmcnt(16)
-    // leaves only the operand DMAs of K-tile 1 outstanding) ----
-    dma_scales(0, true);
-    dma_a(0, true, pA0);
-    dma_b(0, true, pB0);
-    if constexpr (SPAN == 1) dma_scales(1, nk > 1);
-    dma_a(1, nk > 1, pA1);
-    dma_b(1, nk > 1, pB1);
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-    // halves and scales used by quadrant 1 of K-tile 0
-    int s0a[8], s0b[8], s1a[8], s1b[8];
+        auto b_ktile = [&](int kt) __attribute__((always_inline)) -> const uint8_t* {
+            if constexpr (BL == BLay::RAW) return B + kt * BKB;
+            else if constexpr (BL == BLay::KPANEL) return B + (long long)kt * N * BKB;
+            else return B + kt * 2048;
+        };
+        auto dma_a = [&](int kt, bool valid, QG_LDS uint8_t* sA) __attribute__((always_inline)) {
+            const auto r = rsrc(A + kt * BKB, valid);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-        read_one(wide::shared_is_a(0, 3), wide::shared_half(0, 3), x, pA0, pB0);
-        read_one(wide::shared_is_a(0, 0), wide::shared_half(0, 0), x, pA0, pB0);
-    }
+            for (int t = 0; t < 8; ++t) dma16_buf(r, sA + (w * 8 + t) * 8 * BKB, aoff[t], 0);
+        };
+        auto dma_b = [&](int kt, bool valid, QG_LDS uint8_t* sB) __attribute__((always_inline)) {
+            const auto r = rsrc(b_ktile(kt), valid);
 #pragma unroll
-    for (int x = 0; x < 8; ++x) read_scale(0, x, s0a, s0b);
+            for (int t = 0; t < 8; ++t) dma16_buf(r, sB + (w * 8 + t) * 8 * BKB, boff[t], 0);
+        };
+        // scale DMAs that go with K-tile kt (MX: only when kt starts a panel,
+        // which the callers know at compile time); `valid` false = no-op DMAs.
+        // MX panel images: PB = 16, 32: [row][PB]; PB = 4 (fp8): [row][4 B];
+        // PB = 8 (fp4): [2 halves][row][4 B]
+        auto dma_scales = [&](int kt, bool valid) __attribute__((always_inline)) {
+            if constexpr (MXS) {
+                // images [block][SPAN K-tiles][256 B]
+                const int buf = ((kt / SPAN) & 1) * PANEL;
+                const auto ra = rsrc(SFA_t + (long long)kt * 256, valid);
+                const auto rb = rsrc(SFB_t + (long long)kt * 256, valid);
+                if constexpr (PB == 32) {
 #pragma unroll
-    for (int x = 0; x < 8; ++x) finish_scale(x, s0a, s0b);
-
-    // the loop runs U K-tiles per iteration: the quadrant rotation repeats
-    // every 4 and the scale-panel DMA every SPAN, both at compile time
-    constexpr int U = SPAN > 4 ? SPAN : 4;
-    auto step = [&](auto PC, int tt) __attribute__((always_inline)) {
-        if constexpr (decltype(PC)::value & 1) ktile(PC, tt, s1a, s1b, s0a, s0b);
-        else ktile(PC, tt, s0a, s0b, s1a, s1b);
-    };
-    int t = 0;
-    for (; t + U <= nk; t += U) wide::static_for<U>([&](auto pc) __attribute__((always_inline)) { step(pc, t + pc.value); });
-    wide::static_for<U - 1>([&](auto pc) __attribute__((always_inline)) {
-        if (t + pc.value < nk) step(pc, t + pc.value);
-    });
-    wait_vmcnt<0>();
-    // the accumulators come from inline-asm MFMAs, which the compiler's hazard
-    // tracking does not see: cover the MFMA-result-to-VALU-read latency
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-
-    // ---- epilogue ----
-    // Output element (r, c) of the wave's 128 x 128 block for accumulator
-    // element 4*v4 + e of block (i, j):
-    //   fp8: r = 16i + l16, c = 16j + 4q + e            (v4 = 0)
-    //   fp4: r = 32i + l32, c = 32j + 8*v4 + 4g + e     (v4 = 0..3)
-    auto out_row = [&](int i) __attribute__((always_inline)) { return FP4 ? 32 * i + l32 : 16 * i + l16; };
-    auto out_col = [&](int j, int v4) __attribute__((always_inline)) {
-        return FP4 ? 32 * j + 8 * v4 + 4 * g : 16 * j + 4 * q;
-    };
-    constexpr int NV4 = FP4 ? 4 : 1;
-    // 4-element stores need 8- (bf16) or 16-byte (fp32) aligned row starts;
-    // the bf16 whole-tile path stores 16 bytes (8 elements) per lane
-    const bool vec_ok = p.c_vec >= 4;
-    if (p.c_vec >= (BF16 ? 8 : 4) && m0 + BM <= M && n0 + BM <= N) {
-        if constexpr (BF16) {
-            // Whole tile inside C, bf16: the wave's 128 x 128 block goes
-            // through its own 32 KB of LDS (one operand stage, rows of 256 B,
-            // 16-byte chunks XOR-swizzled by row) so that every global store
-            // writes whole 128-byte lines: 16 B per lane, 4 rows of 256 B
-            // per instruction, instead of 16 rows x 32 B.
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            QG_LDS uint8_t* img = w == 0 ? pA0 : w == 1 ? pA1 : w == 2 ? pB0 : pB1;
-#pragma unroll
-            for (int i = 0; i < NBLK; ++i)
-#pragma unroll
-                for (int j = 0; j < NBLK; ++j)
-#pragma unroll
-                    for (int v4 = 0; v4 < NV4; ++v4) {
-                        const int r = out_row(i), cbyte = 2 * out_col(j, v4);
-                        const int c = (cbyte >> 4) ^ (r & 15);
-                        const Acc& a = acc[i][j];
-                        *(QG_LDS u32x2*)(img + r * 256 + c * 16 + (cbyte & 15)) =
-                            u32x2{pack_bf16x2(a[4 * v4], a[4 * v4 + 1]), pack_bf16x2(a[4 * v4 + 2], a[4 * v4 + 3])};
+                    for (int u = 0; u < 2; ++u) {
+                        dma16_buf(ra, pSA + buf + w * 2048 + u * 1024, mx_voff_a[u], 0);
+                        dma16_buf(rb, pSB + buf + w * 2048 + u * 1024, mx_voff_b[u], 0);
                     }
-            const int rr = L >> 4, cc = L & 15;
-            uint16_t* cbase = (uint16_t*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128 + rr) * LDC +
-                              n0 + wn * 128 + cc * 8;
+                } else if (w < 2) {
+                    dma16_buf(ra, pSA + buf + (w & 1) * 1024, mx_voff_a[0], 0);
+                } else {
+                    dma16_buf(rb, pSB + buf + (w & 1) * 1024, mx_voff_b[0], 0);
+                }
+            } else if constexpr (MX) {
+                const int buf = ((kt / SPAN) & 1) * PANEL;
+                const auto ra = rsrc(SFA_t + (long long)kt * SFA_KT, valid);
+                const auto rb = rsrc(SFB_t + (long long)kt * SFB_KT, valid);
+                if constexpr (PB == 32) {
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                const int r = u * 4 + rr;
-                const i32x4 v = *(const QG_LDS i32x4*)(img + r * 256 + ((cc ^ (r & 15)) << 4));
-                // non-temporal: the output is not re-read, keep L2 and MALL for A and B
-                __builtin_nontemporal_store(v, (i32x4*)(cbase + (long long)u * 4 * LDC));
+                    for (int u = 0; u < 2; ++u) {
+                        dma16_buf(ra, pSA + buf + w * 2048 + u * 1024, mx_voff_a[u], 0);
+                        dma16_buf(rb, pSB + buf + w * 2048 + u * 1024, mx_voff_b[u], 0);
+                    }
+                } else if constexpr (PB == 16) {
+                    dma16_buf(ra, pSA + buf + w * 1024, mx_voff_a[0], 0);
+                    dma16_buf(rb, pSB + buf + w * 1024, mx_voff_b[0], 0);
+                } else {
+                    dma4_buf(ra, pSA + buf + w * 256, mx_voff_a[0], 0);
+                    dma4_buf(rb, pSB + buf + w * 256, mx_voff_b[0], 0);
+                    if constexpr (PB == 8) {
+                        dma4_buf(ra, pSA + buf + 1024 + w * 256, mx_voff_a[0] + 4, 0);
+                        dma4_buf(rb, pSB + buf + 1024 + w * 256, mx_voff_b[0] + 4, 0);
+                    }
+                }
+            } else {
+                const int st = kt & 1;
+                const auto ra = rsrc(SFA_t + (long long)kt * SFA_SK, valid && w == 0);
+                const auto rb = rsrc(SFB + ((bs_b_idx + kt) & ~3ll), valid);
+                dma4_buf(ra, w == 0 ? pSA + st * 256 : pSA + 256 + w * 256, 4 * L, 0);
+                dma4_buf(rb, pSB + st * 1024 + w * 256, 0, 0);
             }
-        } else {
-            float* cw = (float*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128) * LDC + n0 + wn * 128;
-#pragma unroll
-            for (int i = 0; i < NBLK; ++i)
-#pragma unroll
-                for (int j = 0; j < NBLK; ++j)
-#pragma unroll
-                    for (int v4 = 0; v4 < NV4; ++v4) {
-                        const Acc& a = acc[i][j];
-                        *(f32x4*)(cw + (long long)out_row(i) * LDC + out_col(j, v4)) =
-                            f32x4{a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]};
+        };
+        // Scale registers of K-tile kt, x = 0..7 (A and B rows of the wave):
+        //  fp8: block x's byte for lane group q (sa[x], sb[x]); BS8 has one B
+        //       scale per wave, read with x = 0;
+        //  fp4: block x/2, word x%2, which holds the lane group's blocks of
+        //       instructions 2(x%2) (byte 0) and 2(x%2)+1 (byte 2) once
+        //       finish_scale has shifted the lane group's bytes down.  The shift
+        //       is a separate step, issued a few MFMAs after the read, so the
+        //       wave does not stall on the LDS latency.
+        const int q = L >> 4, l16 = L & 15, g = L >> 5, l32 = L & 31;
+        //  MXS: block x/2, words x%2 = the dwords at g*64 and g*64 + 128 of
+        //       the block's K-tile: after the shift by the lane's row half
+        //       (l32/16), sub-tile s reads word s%2, byte 2(s/2).
+        auto read_scale = [&](int kt, int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
+            if constexpr (MXS) {
+                if ((x & 1) == 0) {
+                    const int off = ((kt / SPAN) & 1) * PANEL + (kt % SPAN) * 256 + g * 64 + (l32 & 15) * 4;
+                    const QG_LDS uint8_t* ba = pSA + off + (wm * 4 + (x >> 1)) * SPAN * 256;
+                    const QG_LDS uint8_t* bb = pSB + off + (wn * 4 + (x >> 1)) * SPAN * 256;
+                    sa[x] = *(const QG_LDS int*)ba;
+                    sa[x + 1] = *(const QG_LDS int*)(ba + 128);
+                    sb[x] = *(const QG_LDS int*)bb;
+                    sb[x + 1] = *(const QG_LDS int*)(bb + 128);
+                }
+            } else if constexpr (MX && !FP4) {
+                const int buf = ((kt / SPAN) & 1) * PANEL;
+                const int col = WIDE ? (kt % SPAN) * KT_BYTES + q : q;
+                sa[x] = pSA[buf + (wm * 128 + x * 16 + l16) * PB + col];
+                sb[x] = pSB[buf + (wn * 128 + x * 16 + l16) * PB + col];
+            } else if constexpr (MX) {
+                const int buf = ((kt / SPAN) & 1) * PANEL;
+                const int ra = wm * 128 + (x >> 1) * 32 + l32, rb = wn * 128 + (x >> 1) * 32 + l32;
+                if constexpr (WIDE) {
+                    // both words of the block in one read (x even; x odd is a no-op)
+                    if ((x & 1) == 0) {
+                        const i32x2 va = *(const QG_LDS i32x2*)(pSA + buf + ra * PB + (kt % SPAN) * KT_BYTES);
+                        const i32x2 vb = *(const QG_LDS i32x2*)(pSB + buf + rb * PB + (kt % SPAN) * KT_BYTES);
+                        sa[x] = va[0];
+                        sa[x + 1] = va[1];
+                        sb[x] = vb[0];
+                        sb[x + 1] = vb[1];
                     }
-        }
-        return;
-    }
-    // edge tiles: masked element stores
+                } else {
+                    sa[x] = (int)*(const QG_LDS uint32_t*)(pSA + buf + (x & 1) * 1024 + ra * 4);
+                    sb[x] = (int)*(const QG_LDS uint32_t*)(pSB + buf + (x & 1) * 1024 + rb * 4);
+                }
+            } else {
+                const int st = kt & 1;
+                sa[x] = pSA[st * 256 + wm * 128 + x * 16 + l16];
+                if (x == 0) {
+                    const int v = pSB[st * 1024 + w * 256 + (int)((bs_b_idx + kt) & 3)];
 #pragma unroll
-    for (int i = 0; i < NBLK; ++i) {
-        const int mm = m0 + wm * 128 + out_row(i);
-        if (mm < M) {
+                    for (int j = 0; j < 8; ++j) sb[j] = v;
+                }
+            }
+        };
+        auto finish_scale = [&](int x, int (&sa)[8], int (&sb)[8]) __attribute__((always_inline)) {
+            if constexpr (FP4) {
+                const int sh = MXS ? 8 * (l32 >> 4) : 8 * g;
+                sa[x] = (int)((uint32_t)sa[x] >> sh);
+                sb[x] = (int)((uint32_t)sb[x] >> sh);
+            }
+        };
+
+        // per-lane operand read offsets: fp8 chunks q and q+4 of row l16 of a
+        // 16-row block; fp4 chunk 2s+g of row l32 of a 32-row block
+        const int rd8 = l16 * BKB + ((q ^ (l16 & 7)) << 4);
+        auto rd4 = [&](int s) __attribute__((always_inline)) {
+            return l32 * BKB + (((2 * s + g) ^ ((l32 >> 1) & 7)) << 4);
+        };
+        // fp4 B in W16 blocks: row l32 % 16 of block l32 / 16, chunk 2s + g (+ 512 s).
+        // The offset passes through an empty asm: written as a plain lane-id
+        // expression, the compiler lost track of which LDS array these reads
+        // hit and put a vmcnt(0) (wait for every DMA in flight) before them.
+        int rdw = (l32 >> 4) * 2048 + g * 256 + (l32 & 15) * 16;
+        asm("" : "+v"(rdw));
+
+        Acc acc[NBLK][NBLK];
+#pragma unroll
+        for (int i = 0; i < NBLK; ++i)
 #pragma unroll
             for (int j = 0; j < NBLK; ++j)
 #pragma unroll
-                for (int v4 = 0; v4 < NV4; ++v4) {
-                    const int nn = n0 + wn * 128 + out_col(j, v4);
-                    const Acc& a = acc[i][j];
-                    const f32x4 v = f32x4{a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]};
-                    if constexpr (BF16) {
-                        uint16_t* crow = (uint16_t*)p.c + bz * p.c_batch + (long long)mm * LDC;
-                        if (vec_ok && nn + 3 < N) {
-                            *(u32x2*)(crow + nn) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                        } else {
-                            for (int r = 0; r < 4; ++r)
-                                if (nn + r < N) crow[nn + r] = bf16_bits(v[r]);
+                for (int v = 0; v < (FP4 ? 16 : 4); ++v) acc[i][j][v] = 0.f;
+        Frag ah[2][NF], bh[2][NF];
+
+        // read unit x (0..3) of register half h of A (is_a) or B: two
+        // ds_read_b128 -- fp8: the 16-row block x; fp4: sub-tiles 2(x%2) and
+        // 2(x%2)+1 of the 32-row block x/2
+        auto read_one = [&](bool is_a, int h, int x, const QG_LDS uint8_t* sA,
+                            const QG_LDS uint8_t* sB) __attribute__((always_inline)) {
+            const QG_LDS uint8_t* base = is_a ? sA + wm * 128 * BKB : sB + wn * 128 * BKB;
+            Frag(&dst)[2][NF] = is_a ? ah : bh;
+            if constexpr (FP4) {
+                const QG_LDS uint8_t* blk = base + (2 * h + (x >> 1)) * 32 * BKB;
+                const int s0 = 2 * (x & 1);
+                if (BL == BLay::W16 && !is_a) {
+                    // the 32-row block is W16 blocks 2b, 2b + 1 ([8 chunks][16 rows][16 B] each)
+                    dst[h][4 * (x >> 1) + s0] = *(const QG_LDS i32x4*)(blk + rdw + 2 * s0 * 256);
+                    dst[h][4 * (x >> 1) + s0 + 1] = *(const QG_LDS i32x4*)(blk + rdw + 2 * (s0 + 1) * 256);
+                } else {
+                    dst[h][4 * (x >> 1) + s0] = *(const QG_LDS i32x4*)(blk + rd4(s0));
+                    dst[h][4 * (x >> 1) + s0 + 1] = *(const QG_LDS i32x4*)(blk + rd4(s0 + 1));
+                }
+            } else {
+                const QG_LDS uint8_t* blk = base + (4 * h + x) * 16 * BKB;
+                const bool lin = BL == BLay::W16 && !is_a;    // W16 blocks: operand order
+                const i32x4 lo = *(const QG_LDS i32x4*)(blk + (lin ? L * 16 : rd8));
+                const i32x4 hi = *(const QG_LDS i32x4*)(blk + (lin ? 1024 + L * 16 : rd8 ^ 64));
+                dst[h][x] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+        };
+        // quadrant (ha, hb): 16 MFMAs; after MFMA k, fill(k) issues this step's
+        // share of LDS reads and DMAs.  Each step is fenced so the order stays
+        // as written: the LDS reads and DMAs spread between MFMAs, and no read
+        // of a register half moves above the last MFMA that uses its old rows.
+        // fp4 walks the 4 sub-tiles outermost, so consecutive MFMAs never chain
+        // on one accumulator.
+        auto quadrant = [&](int ha, int hb, const int (&sa)[8], const int (&sb)[8],
+                            auto&& fill) __attribute__((always_inline)) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                if constexpr (FP4) {
+                    const int s = k >> 2, bi = (k >> 1) & 1, bj = k & 1;
+                    const int i = 2 * ha + bi, j = 2 * hb + bj;
+                    // scale word and byte of sub-tile s: MX word s/2, byte 2(s%2);
+                    // MXS word s%2, byte 2(s/2)
+                    const int sw = MXS ? (s & 1) : (s >> 1);
+                    if (MXS ? (s >> 1) : (s & 1))
+                        wide::mfma_fp4<true>(acc[i][j], bh[hb][4 * bj + s], ah[ha][4 * bi + s], sb[2 * j + sw],
+                                             sa[2 * i + sw]);
+                    else
+                        wide::mfma_fp4<false>(acc[i][j], bh[hb][4 * bj + s], ah[ha][4 * bi + s], sb[2 * j + sw],
+                                              sa[2 * i + sw]);
+                } else {
+                    const int i = k >> 2, j = k & 3;
+                    wide::mfma_fp8(acc[4 * ha + i][4 * hb + j], bh[hb][j], ah[ha][i], sb[4 * hb + j], sa[4 * ha + i]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                fill(k);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        // One K-tile t in phase P = t % 4 (LDS stage P & 1 holds t and then
+        // t + 2).  sa/sb: this K-tile's scales; san/sbn receive K-tile t + 1's.
+        auto ktile = [&](auto PC, int t, const int (&sa)[8], const int (&sb)[8], int (&san)[8],
+                         int (&sbn)[8]) __attribute__((always_inline)) {
+            constexpr int P = decltype(PC)::value;
+            QG_LDS uint8_t* sA = (P & 1) ? pA1 : pA0;
+            QG_LDS uint8_t* sB = (P & 1) ? pB1 : pB0;
+            QG_LDS uint8_t* nA = (P & 1) ? pA0 : pA1;
+            QG_LDS uint8_t* nB = (P & 1) ? pB0 : pB1;
+            constexpr bool r1a = wide::shared_is_a(P, 1), r2a = wide::shared_is_a(P, 2), r0a = wide::shared_is_a(P, 0);
+            constexpr int r1 = wide::shared_half(P, 1), r2 = wide::shared_half(P, 2), r0 = wide::shared_half(P, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            // quadrant 1: K-tile t's two halves freed at the end of the previous
+            // K-tile, one read unit after each of the first 8 MFMAs
+            quadrant(wide::qa(P), wide::qb(P), sa, sb, [&](int k) __attribute__((always_inline)) {
+                if (k < 4) read_one(r1a, r1, k, sA, sB);
+                else if (k < 8) read_one(r2a, r2, k - 4, sA, sB);
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1: stage P&1 is free
+            // quadrants 2-4: the 16 operand DMAs of K-tile t + 2 (A rows 0-7,
+            // then B rows 0-7, in 8-row groups) into this K-tile's stage, one
+            // after every third MFMA, so the CU's texture path is never asked
+            // for more than it streams (a wave blocks on a DMA it cannot queue);
+            // the scale DMAs go first, so B2's vmcnt covers them
+            const bool more = t + 2 < nk;
+            if constexpr ((P + 2) % SPAN == 0) dma_scales(t + 2, more);
+            const auto rA = rsrc(A + (t + 2) * BKB, more);
+            const auto rB = rsrc(b_ktile(t + 2), more);
+            auto dma_op = [&](int d) __attribute__((always_inline)) {
+                if (d < 8) dma16_buf(rA, sA + (w * 8 + d) * 8 * BKB, aoff[d], 0);
+                else dma16_buf(rB, sB + (w * 8 + d - 8) * 8 * BKB, boff[d - 8], 0);
+            };
+            // quadrant 2: DMAs 0-5
+            quadrant(wide::qa(P + 1), wide::qb(P + 1), sa, sb, [&](int k) __attribute__((always_inline)) {
+                if (k % 3 == 0) dma_op(k / 3);
+            });
+            asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");  // B2: K-tile t + 1 landed
+            // quadrant 3: DMAs 6-10; first half of t + 1
+            quadrant(wide::qa(P + 2), wide::qb(P + 2), sa, sb, [&](int k) __attribute__((always_inline)) {
+                if (k % 3 == 2) dma_op(6 + k / 3);
+                if (k < 8 && (k & 1) == 0) read_one(r0a, r0, k >> 1, nA, nB);
+            });
+            // quadrant 4: DMAs 11-15; second half and scales of t + 1
+            quadrant(wide::qa(P + 3), wide::qb(P + 3), sa, sb, [&](int k) __attribute__((always_inline)) {
+                if (k % 3 == 1) dma_op(11 + k / 3);
+                if (k < 4) read_one(r1a, r1, k, nA, nB);
+                if (k < 8) read_scale(t + 1, k, san, sbn);
+                else finish_scale(k - 8, san, sbn);
+            });
+        };
+
+        // ---- prologue: DMA K-tiles 0 and 1 (scales of 1 first, so vmcnt(16)
+        // leaves only the operand DMAs of K-tile 1 outstanding) ----
+        dma_scales(0, true);
+        dma_a(0, true, pA0);
+        dma_b(0, true, pB0);
+        if constexpr (SPAN == 1) dma_scales(1, nk > 1);
+        dma_a(1, nk > 1, pA1);
+        dma_b(1, nk > 1, pB1);
+        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        // halves and scales used by quadrant 1 of K-tile 0
+        int s0a[8], s0b[8], s1a[8], s1b[8];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            read_one(wide::shared_is_a(0, 3), wide::shared_half(0, 3), x, pA0, pB0);
+            read_one(wide::shared_is_a(0, 0), wide::shared_half(0, 0), x, pA0, pB0);
+        }
+#pragma unroll
+        for (int x = 0; x < 8; ++x) read_scale(0, x, s0a, s0b);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) finish_scale(x, s0a, s0b);
+
+        // the loop runs U K-tiles per iteration: the quadrant rotation repeats
+        // every 4 and the scale-panel DMA every SPAN, both at compile time
+        constexpr int U = SPAN > 4 ? SPAN : 4;
+        auto step = [&](auto PC, int tt) __attribute__((always_inline)) {
+            if constexpr (decltype(PC)::value & 1) ktile(PC, tt, s1a, s1b, s0a, s0b);
+            else ktile(PC, tt, s0a, s0b, s1a, s1b);
+        };
+        int t = 0;
+        for (; t + U <= nk; t += U) wide::static_for<U>([&](auto pc) __attribute__((always_inline)) { step(pc, t + pc.value); });
+        wide::static_for<U - 1>([&](auto pc) __attribute__((always_inline)) {
+            if (t + pc.value < nk) step(pc, t + pc.value);
+        });
+        wait_vmcnt<0>();
+        // the accumulators come from inline-asm MFMAs, which the compiler's hazard
+        // tracking does not see: cover the MFMA-result-to-VALU-read latency
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+        // ---- epilogue ----
+        // Output element (r, c) of the wave's 128 x 128 block for accumulator
+        // element 4*v4 + e of block (i, j):
+        //   fp8: r = 16i + l16, c = 16j + 4q + e            (v4 = 0)
+        //   fp4: r = 32i + l32, c = 32j + 8*v4 + 4g + e     (v4 = 0..3)
+        auto out_row = [&](int i) __attribute__((always_inline)) { return FP4 ? 32 * i + l32 : 16 * i + l16; };
+        auto out_col = [&](int j, int v4) __attribute__((always_inline)) {
+            return FP4 ? 32 * j + 8 * v4 + 4 * g : 16 * j + 4 * q;
+        };
+        constexpr int NV4 = FP4 ? 4 : 1;
+        // 4-element stores need 8- (bf16) or 16-byte (fp32) aligned row starts;
+        // the bf16 whole-tile path stores 16 bytes (8 elements) per lane
+        const bool vec_ok = p.c_vec >= 4;
+        if (p.c_vec >= (BF16 ? 8 : 4) && m0 + BM <= M && n0 + BM <= N) {
+            if constexpr (BF16) {
+                // Whole tile inside C, bf16: the wave's 128 x 128 block goes
+                // through its own 32 KB of LDS (one operand stage, rows of 256 B,
+                // 16-byte chunks XOR-swizzled by row) so that every global store
+                // writes whole 128-byte lines: 16 B per lane, 4 rows of 256 B
+                // per instruction, instead of 16 rows x 32 B.
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                QG_LDS uint8_t* img = w == 0 ? pA0 : w == 1 ? pA1 : w == 2 ? pB0 : pB1;
+#pragma unroll
+                for (int i = 0; i < NBLK; ++i)
+#pragma unroll
+                    for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+                        for (int v4 = 0; v4 < NV4; ++v4) {
+                            const int r = out_row(i), cbyte = 2 * out_col(j, v4);
+                            const int c = (cbyte >> 4) ^ (r & 15);
+                            const Acc& a = acc[i][j];
+                            *(QG_LDS u32x2*)(img + r * 256 + c * 16 + (cbyte & 15)) =
+                                u32x2{pack_bf16x2(a[4 * v4], a[4 * v4 + 1]), pack_bf16x2(a[4 * v4 + 2], a[4 * v4 + 3])};
                         }
-                    } else {
-                        float* crow = (float*)p.c + bz * p.c_batch + (long long)mm * LDC;
-                        if (vec_ok && nn + 3 < N) {
-                            *(f32x4*)(crow + nn) = v;
+                const int rr = L >> 4, cc = L & 15;
+                uint16_t* cbase = (uint16_t*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128 + rr) * LDC +
+                                  n0 + wn * 128 + cc * 8;
+#pragma unroll
+                for (int u = 0; u < 32; ++u) {
+                    const int r = u * 4 + rr;
+                    const i32x4 v = *(const QG_LDS i32x4*)(img + r * 256 + ((cc ^ (r & 15)) << 4));
+                    // non-temporal: the output is not re-read, keep L2 and MALL for A and B
+                    __builtin_nontemporal_store(v, (i32x4*)(cbase + (long long)u * 4 * LDC));
+                }
+            } else {
+                float* cw = (float*)p.c + (long long)bz * p.c_batch + (long long)(m0 + wm * 128) * LDC + n0 + wn * 128;
+#pragma unroll
+                for (int i = 0; i < NBLK; ++i)
+#pragma unroll
+                    for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+                        for (int v4 = 0; v4 < NV4; ++v4) {
+                            const Acc& a = acc[i][j];
+                            *(f32x4*)(cw + (long long)out_row(i) * LDC + out_col(j, v4)) =
+                                f32x4{a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]};
+                        }
+            }
+            continue;
+        }
+        // edge tiles: masked element stores
+#pragma unroll
+        for (int i = 0; i < NBLK; ++i) {
+            const int mm = m0 + wm * 128 + out_row(i);
+            if (mm < M) {
+#pragma unroll
+                for (int j = 0; j < NBLK; ++j)
+#pragma unroll
+                    for (int v4 = 0; v4 < NV4; ++v4) {
+                        const int nn = n0 + wn * 128 + out_col(j, v4);
+                        const Acc& a = acc[i][j];
+                        const f32x4 v = f32x4{a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]};
+                        if constexpr (BF16) {
+                            uint16_t* crow = (uint16_t*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                            if (vec_ok && nn + 3 < N) {
+                                *(u32x2*)(crow + nn) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                            } else {
+                                for (int r = 0; r < 4; ++r)
+                                    if (nn + r < N) crow[nn + r] = bf16_bits(v[r]);
+                            }
                         } else {
-                            for (int r = 0; r < 4; ++r)
-                                if (nn + r < N) crow[nn + r] = v[r];
+                            float* crow = (float*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                            if (vec_ok && nn + 3 < N) {
+                                *(f32x4*)(crow + nn) = v;
+                            } else {
+                                for (int r = 0; r < 4; ++r)
+                                    if (nn + r < N) crow[nn + r] = v[r];
+                            }
                         }
                     }
-                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

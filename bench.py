@@ -54,6 +54,9 @@ WORKLOADS = {
     # name: (family, M, N, K, BASELINE config index)
     "mxfp8_8192": ("mx8", 8192, 8192, 8192, 1),
     "mxfp4_8192": ("mx4", 8192, 8192, 8192, 3),
+    # configs[3] with aiter's gemm_a4w4(bpreshuffle=True) operands: the weight
+    # pre-shuffled once (shuffle_weight(16,16)), scales in e8m0_shuffle order
+    "mxfp4_8192_aiter": ("mx4a", 8192, 8192, 8192, 3),
     "bs_fp32_8192": ("bs", 8192, 8192, 8192, 2),
     "bs_c0": ("bs", 32, 1536, 7168, 0),
     "ldsbypass_c0": ("lbp", 32, 1536, 7168, 0),
@@ -65,6 +68,8 @@ WORKLOADS = {
 
 NAMES = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
          "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
+         "mx4a": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K, aiter gemm_a4w4 bpreshuffle formats "
+                 "(shuffle_weight(16,16) B, e8m0_shuffle scales)",
          "bs": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, K-panel B (bpreshuffle)",
          "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)",
          "bs8": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, shuffle_weight(16,16) B"}
@@ -81,6 +86,8 @@ def parse():
     p.add_argument("--m", type=int, default=None, help="override M (decode sweeps)")
     p.add_argument("--n", type=int, default=None, help="override N")
     p.add_argument("--k", type=int, default=None, help="override K")
+    p.add_argument("--grid-blocks", type=int, default=0,
+                   help="mxfp4_8192_aiter: persistent grid of this many workgroups (0 = one per tile)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-check", action="store_true", help="skip the output check against the oracle")
     p.add_argument("--sfa-km", action="store_true",
@@ -134,7 +141,7 @@ def make_operands(q, fam, M, N, K, dev, sfa_km=False):
         A, SA = q.quant_mxfp8(a)
         B, SB = q.quant_mxfp8(b)
         ops.update(A=A.view(torch.uint8), SA=SA, B=B.view(torch.uint8), SB=SB)
-    elif fam == "mx4":
+    elif fam in ("mx4", "mx4a"):
         A, SA = q.quant_mxfp4(a)
         B, SB = q.quant_mxfp4(b)
         ops.update(A=A, SA=SA, B=B, SB=SB)
@@ -154,13 +161,21 @@ def make_operands(q, fam, M, N, K, dev, sfa_km=False):
         ops["B"] = q.ldsbypass_pack_b(ops["B"])
     elif fam == "bs8":
         ops["B"] = q.shuffle_weight_16x16(ops["B"])
+    elif fam == "mx4a":
+        ops["B"] = q.shuffle_weight_16x16(ops["B"])
+        ops["SA_raw"], ops["SB_raw"] = ops["SA"], ops["SB"]
+        ops["SA"], ops["SB"] = q.e8m0_shuffle(ops["SA"]), q.e8m0_shuffle(ops["SB"])
     torch.cuda.synchronize()
     return ops
 
 
-def kargs_for(q, fam, M, N, K, A, B, C, SA, SB, sfa_km):
+def kargs_for(q, fam, M, N, K, A, B, C, SA, SB, sfa_km, grid_blocks=0):
     kg32, kg128 = K // 32, K // 128
-    kb = K // 2 if fam == "mx4" else K
+    kb = K // 2 if fam in ("mx4", "mx4a") else K
+    if fam == "mx4a":
+        blk = 32 * ((kg32 + 7) // 8 * 8)       # e8m0_shuffle bytes per 32-row block
+        return q.Mxfp4Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, kb, kb, N, M * kb, N * kb, M * N,
+                            SA.data_ptr(), SB.data_ptr(), blk, blk, SA.numel(), SB.numel(), grid_blocks)
     if fam in ("mx8", "mx4"):
         return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, kb, kb, N, M * kb, N * kb, M * N,
                        SA.data_ptr(), SB.data_ptr(), kg32, kg32, M * kg32, N * kg32)
@@ -179,6 +194,8 @@ def entry_for(L, fam):
     """(launch(kargs_ptr, ws_ptr, ws_bytes, stream), workspace query) of a family."""
     if fam == "bs8":
         return (lambda ka, wp, wb, s: L.launch_blockscale_bpreshuffle(ka, 1, 0, s)), (lambda ka: 0)
+    if fam == "mx4a":
+        return (lambda ka, wp, wb, s: L.gemm_a4w4_mxfp4_bpreshuffle(ka, 1, s)), (lambda ka: 0)
     name = {"mx8": "gemm_a8w8_mxfp8", "mx4": "gemm_a4w4_mxfp4", "bs": "gemm_a8w8_blockscale_bpreshuffle",
             "lbp": "gemm_a8w8_blockscale_ldsbypass"}[fam]
     fn = getattr(L, name)
@@ -280,7 +297,7 @@ def check_points(O, fam, M, N, K, host, C, sfa_km):
     A, B, SA, SB = host["A"], host["B_raw"], host["SA"], host["SB"]
     if fam == "mx8":
         ref = O.gemm_mx8_points(A, B, SA, SB, rows, cols)
-    elif fam == "mx4":
+    elif fam in ("mx4", "mx4a"):
         ref = O.gemm_mx4_points(A, B, SA, SB, rows, cols)
     elif fam == "bs8":
         ref = O.gemm_bs_e8m0_points(A, B, SA, SB, rows, cols)     # SA physical [K/128][M]
@@ -295,6 +312,9 @@ def host_copies(fam, ops, sfa_km):
     """Host arrays of the quantized operands in the oracle's layouts."""
     h = {k: ops[k].cpu().numpy() for k in ("A", "B_raw", "SB")}
     sa = ops["SA"]
+    if fam == "mx4a":                                           # the row-major scales
+        h["SB"] = ops["SB_raw"].cpu().numpy()
+        sa = ops["SA_raw"]
     if fam == "bs8":
         h["SA"] = sa.t().contiguous().cpu().numpy()               # physical [K/128][M]
     elif fam in ("bs", "lbp") and sfa_km:
@@ -312,7 +332,7 @@ def cpu_baseline(O, fam, M, N, K, h, sfa_km, seconds):
     if fam == "mx8":
         fn = lambda r: O.gemm_mx8(A[r], B, SA[r], SB)
         which = "MX8 gemm_ref (mxfp8_gemm/gemm_a8w8_mxfp8_host.cc:96-122)"
-    elif fam == "mx4":
+    elif fam in ("mx4", "mx4a"):
         fn = lambda r: O.gemm_mx4(A[r], B, SA[r], SB)
         which = "MX4 gemm_ref_gpu grouped form (gemm_a4w4_mxfp4_4wave_host.cc:66-94)"
     elif fam == "bs8":
@@ -443,7 +463,7 @@ def main():
     SBs = [SB0] + [SB0.clone() for _ in range(copies - 1)]
 
     launch_fn, wq = entry_for(L, fam)
-    calls = [kargs_for(q, fam, M, N, K, A, B, C, SA, SB, args.sfa_km) for B, SB in zip(Bs, SBs)]
+    calls = [kargs_for(q, fam, M, N, K, A, B, C, SA, SB, args.sfa_km, args.grid_blocks) for B, SB in zip(Bs, SBs)]
     ws_bytes = max(1, wq(ctypes.byref(calls[0])))
     ws = torch.zeros((ws_bytes + 255) // 256 * 256, dtype=torch.uint8, device=dev)
     stream = torch.cuda.Stream(dev)
@@ -461,7 +481,7 @@ def main():
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
 
-    kind = "fp4" if fam == "mx4" else "fp8"
+    kind = "fp4" if fam in ("mx4", "mx4a") else "fp8"
     tag = args.workload + (f"_m{M}" if args.m else "") + (f"_n{N}" if args.n else "") + (f"_k{K}" if args.k else "")
     if hbm_bound:
         # algorithmic bytes: A, B and both scale arrays read once, C written once

@@ -170,6 +170,45 @@ hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, voi
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args);
 
+/* MXFP4 with aiter's gemm_a4w4(..., bpreshuffle=True) operands: the
+ * 96-byte block plus grid_blocks (MX4/candidate_m10/
+ * gemm_a4w4_mxfp4_4wave_traits.hpp:9-30). */
+typedef struct opus_gemm_mxfp4_scale_kargs {
+    const void* ptr_a;
+    const void* ptr_b;
+    void* ptr_c;
+    int m;
+    int n;
+    int k;
+    int batch;
+    int stride_a;
+    int stride_b;
+    int stride_c;
+    int stride_a_batch;
+    int stride_b_batch;
+    int stride_c_batch;
+    const void* ptr_sfa;
+    const void* ptr_sfb;
+    int stride_sfa;
+    int stride_sfb;
+    int stride_sfa_batch;
+    int stride_sfb_batch;
+    int grid_blocks;
+} opus_gemm_mxfp4_scale_kargs;
+
+/* Replaces the launch in MX4/candidate_m10/gemm_a4w4_mxfp4_4wave_host.cc:194-250
+ * (kargs filled at host.cc:224-235). A [M,K/2] row-major bytes (stride_a);
+ * B = shuffle_weight(16,16) of [N,K/2]: byte (n,kb) at
+ * (n/16)*16*(K/2) + (kb/16)*256 + (n%16)*16 + kb%16, N a multiple of 16,
+ * stride_b = K/2; SFA / SFB in e8m0_shuffle order (qgemm_e8m0_shuffle),
+ * stride_sfa / stride_sfb = bytes per 32-row block (>= K, a multiple of
+ * 16), stride_sf*_batch >= ceil(rows/32) * stride_sf*. K a multiple of 256,
+ * any M. grid_blocks: 0 = one workgroup per 256x256 tile; > 0 = a persistent
+ * grid of min(grid_blocks, tiles*batch) workgroups walking the tile list.
+ * Needs no workspace. Every shape runs the 256x256 tile kernel (decode
+ * shapes run faster through gemm_a4w4_mxfp4 with row-major operands). */
+hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream);
+
 /* No counterpart in the reference.  gemm_a4w4_mxfp4 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): the same kernels and results,

@@ -87,6 +87,27 @@ def test_mxfp4_bench_kernel_full_size(qgemm, gpu, m, n, k, kernel):
            lambda band: O.gemm_mx4(qa[band], qb, sa[band], sb), m, n, 256, f"mxfp4 {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("grid_blocks,kernel", [
+    (0, "wide_gemm<fp4,MXS,W16,bf16,pb32>"),
+    (256, "wide_gemm<fp4,MXS,W16,bf16,pb32,persist256>"),
+])
+def test_mxfp4_aiter_bench_kernel_full_size(qgemm, gpu, grid_blocks, kernel):
+    """configs[3] in aiter's gemm_a4w4(bpreshuffle=True) formats (bench.py
+    workload mxfp4_8192_aiter): B shuffle_weight(16,16), e8m0_shuffle scales."""
+    m = n = k = 8192
+    a, b = _bench_inputs(m, n, k)
+    qa, sa = O.quant_mx4(a)
+    qb, sb = O.quant_mx4(b)
+    del a, b
+    dev = lambda x: torch.from_numpy(x).to(gpu)
+    y = qgemm.gemm_a4w4(dev(qa), dev(O.shuffle_weight_16x16(qb)), dev(O.e8m0_shuffle(sa)), dev(O.e8m0_shuffle(sb)),
+                        grid_blocks=grid_blocks)
+    assert qgemm.last_launch() == kernel
+    torch.cuda.synchronize()
+    _check(y, lambda r, c: O.gemm_mx4_points(qa, qb, sa, sb, r, c),
+           lambda band: O.gemm_mx4(qa[band], qb, sa[band], sb), m, n, 256, f"mxfp4 aiter {m}x{n}x{k}")
+
+
 def test_blockscale_fp32_bench_kernel_full_size(qgemm, gpu):
     """bench.py --workload bs_fp32_8192: fp32 1x128 / 128x128 scales, K-panel B."""
     m = n = k = 8192
