@@ -15,6 +15,9 @@ and launch on the current stream:
   B') and ``ldsbypass_pack_b`` (CPU, from raw B) to build B'';
 * ``gemm_a8w8_mxfp8`` -- MXFP8 TN GEMM (MX8 host.cc:96-122, 266-296);
 * ``gemm_a4w4_mxfp4`` -- MXFP4 A4W4 GEMM (MX4 host.cc:96-115, 201-216);
+* ``opus`` -- the aiter-facing names (``gemm_a8w8_bpreshuffle_opus`` with
+  the tuned kernel table, ``gemm_a8w8_mxfp8_opus``,
+  ``opus_gemm_mxfp8_{nt,nn,tt,tn}``);
 * ``gemm_a4w4`` -- MXFP4 with aiter's ``gemm_a4w4(..., bpreshuffle=True)``
   operands: B in shuffle_weight(16,16) order, both scales in e8m0_shuffle
   order (MX4 candidate_m10/gemm_a4w4_mxfp4_4wave_host.cc:194-250).
@@ -87,6 +90,16 @@ EXPORTS = {
     "gemm_a8w8_blockscale_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p,
                                                         ctypes.c_size_t, ctypes.c_void_p]),
     "gemm_a8w8_blockscale_bpreshuffle_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
+    "gemm_a8w8_blockscale_layout": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                                   ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a8w8_blockscale_layout_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), ctypes.c_int]),
+    "gemm_a8w8_blockscale_bpreshuffle_kid": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_int,
+                                                            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), ctypes.c_int]),
+    "gemm_a8w8_blockscale_ldsbypass_kid": (ctypes.c_int, [ctypes.POINTER(LdsBypassKargs), ctypes.c_int, ctypes.c_int,
+                                                          ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a8w8_blockscale_ldsbypass_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LdsBypassKargs),
+                                                                             ctypes.c_int]),
     "gemm_a4w4_mxfp4_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_void_p]),
     "gemm_a8w8_mxfp8": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),
@@ -471,5 +484,7 @@ def shuffle_weight_16x16(B):
 
 
 from . import blockscale_bpreshuffle  # noqa: E402  (reference adapter mirror)
+from .opus import (gemm_a8w8_bpreshuffle_opus, gemm_a8w8_mxfp8_opus, opus_gemm_mxfp8_nn,  # noqa: E402,F401
+                   opus_gemm_mxfp8_nt, opus_gemm_mxfp8_tn, opus_gemm_mxfp8_tt)
 from .quant import (e8m0_shuffle, quant_fp8_blockscale, quant_fp8_e8m0_blockscale,  # noqa: E402,F401
                     quant_mxfp4, quant_mxfp8)

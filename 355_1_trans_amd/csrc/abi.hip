@@ -314,11 +314,11 @@ constexpr int kMidBelow = 128;
 constexpr int kMidMinKt = 16;    // 8 measured slower where the split tail dominates (M = 256, N = 4096, K = 7168: 34.4 vs 27.0 us)
 
 // Replaces p with a 128 x 128 plan when M > kMidMinM and the 256 x 256
-// kernel would have fewer than kMidBelow tiles.
-void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus) {
-    if (m <= kMidMinM) return;
+// kernel would have fewer than kMidBelow tiles (always with force).
+void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus, bool force = false) {
+    if (m <= kMidMinM && !force) return;
     const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
-    if (tiles256 >= kMidBelow) return;
+    if (tiles256 >= kMidBelow && !force) return;
     p = Plan{};
     p.mid = true;
     p.kt_per_split = k_tiles;
@@ -372,6 +372,72 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
     Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false, decode_ok, decode_ok);
     plan_mid(p, m, n, k_tiles, batch, cus);
     return p;
+}
+
+// Kernel routes of the fp32 block-scale entries (QGEMM_KID_* in qgemm.h):
+// AUTO resolves to one of the others by the plans above; a forced route
+// runs that kernel with its own plan (tile shape and K split), or fails
+// with hipErrorInvalidValue where the kernel cannot take the shape.  The
+// workspace a route needs is the same with or without one at hand (the
+// query); without one, split plans run unsplit.
+struct BsfRoute {
+    int kid = QGEMM_KID_AUTO;
+    bool ok = false;
+    qg::BurstPlan bp;
+    Plan pl;
+    size_t ws_bytes = 0;
+};
+
+BsfRoute route_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool frag, int kid, bool have_ws) {
+    BsfRoute r;
+    r.kid = kid;
+    if (m <= 0 || n <= 0 || k_tiles <= 0 || batch <= 0) return r;
+    const int cus = device_cus();
+    switch (kid) {
+        case QGEMM_KID_AUTO: {
+            r.bp = plan_bsf32_burst(m, n, k_tiles, batch);
+            if (r.bp.ok) {
+                r.ws_bytes = burst_ws_bytes(r.bp, m, n, batch);
+                if (r.bp.splitk == 1 || have_ws) {
+                    r.kid = QGEMM_KID_BURST;
+                    r.ok = true;
+                    return r;
+                }
+            }
+            r.pl = plan_bsf32(m, n, k_tiles, batch, b_bytes, !frag);
+            if (!r.bp.ok) r.ws_bytes = r.pl.ws_bytes;
+            r.kid = r.pl.mid ? QGEMM_KID_MID
+                             : r.pl.skinny ? (r.pl.decode ? QGEMM_KID_DECODE : QGEMM_KID_SKINNY) : QGEMM_KID_TILE256;
+            r.ok = true;
+            return r;
+        }
+        case QGEMM_KID_TILE256:
+            r.ok = true;
+            return r;
+        case QGEMM_KID_MID:
+            plan_mid(r.pl, m, n, k_tiles, batch, cus, true);
+            break;
+        case QGEMM_KID_SKINNY:
+            r.pl = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, true, false);
+            break;
+        case QGEMM_KID_DECODE:
+            if (m > 64 || frag) return r;    // the decode kernel stages K-panel B' only
+            r.pl.skinny = true;
+            plan_decode(r.pl, m, n, k_tiles, batch, b_bytes, cus);
+            break;
+        case QGEMM_KID_BURST:
+            r.bp = qg::burst_plan(m, n, k_tiles, batch, cus, kMaxCounters, false);
+            if (!r.bp.ok) return r;
+            r.ws_bytes = burst_ws_bytes(r.bp, m, n, batch);
+            if (r.bp.splitk > 1 && !have_ws) r.bp = qg::burst_plan(m, n, k_tiles, batch, cus, kMaxCounters, false, 1);
+            r.ok = r.bp.ok;
+            return r;
+        default:
+            return r;
+    }
+    r.ws_bytes = r.pl.ws_bytes;
+    r.ok = true;
+    return r;
 }
 
 // MX: the same 128 x 128 rule (row-major B, E8M0 scales applied by the MFMA)
@@ -584,6 +650,25 @@ hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bo
                         (pl.splitk == 1 || pl.kt_per_split % (16 / kt_bytes) == 0);
     }
     return qg::launch_skinny(kind, s, pl.mb, pl.nb, batch, bf16, stream);
+}
+
+hipError_t run_bsf32(const BsfRoute& r, const TileArgs& t, int batch, bool frag, long long b_bytes, bool bf16,
+                     void* ws, size_t ws_bytes, int k_tiles, hipStream_t stream) {
+    switch (r.kid) {
+        case QGEMM_KID_BURST:
+            return run_burst(t, batch, r.bp, frag, b_bytes, bf16, ws, stream);
+        case QGEMM_KID_MID:
+            return run_mid(t, batch, r.pl, bf16, frag ? qg::MidKind::BS_FRAG : qg::MidKind::BS_KPANEL, ws, ws_bytes,
+                           k_tiles, stream);
+        case QGEMM_KID_SKINNY:
+        case QGEMM_KID_DECODE:
+            return run_skinny(frag ? SkinnyKind::BSF32_FRAG : SkinnyKind::BSF32_KPANEL, t, batch, r.pl, bf16, ws,
+                              ws_bytes, k_tiles, stream);
+        default:
+            // the eight-wave kernel with VGPR accumulators and a VALU rescale
+            // per K-tile (bsf32_gemm.hpp)
+            return qg::launch_bsf32(t, batch, bf16, frag, stream);
+    }
 }
 
 // Byte ranges of a call's operands (C first), for the overlap checks of the
@@ -964,9 +1049,82 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
     return qg::launch_wide_bs8_w16(t, a.batch, output_bf16 == 1, stream);
 }
 
+// ------------------------------------------------ E8M0 block scales, NN / TT / TN
+// Each M- or N-contiguous operand is first brought into the NT kernel's
+// operand layout (A [M][K]; B shuffle_weight(16,16) of [N][K]) in the
+// workspace by one transpose pass, and the NT mainloop runs unchanged
+// (TT keeps its row-major [N][K] B and reads it as is).
+size_t gemm_a8w8_blockscale_layout_workspace_bytes(const opus_gemm_scale_kargs* args, int layout) {
+    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->batch <= 0 || layout < 0 || layout > 3)
+        return 0;
+    const bool at = layout == QGEMM_LAYOUT_TT || layout == QGEMM_LAYOUT_TN;
+    const bool bn = layout == QGEMM_LAYOUT_NN || layout == QGEMM_LAYOUT_TN;
+    const size_t per_a = (size_t)args->m * args->k, per_b = (size_t)args->n * args->k;
+    return (at ? round256(per_a * args->batch) : 0) + (bn ? round256(per_b * args->batch) : 0);
+}
+
+hipError_t gemm_a8w8_blockscale_layout(const opus_gemm_scale_kargs* args, int layout, int output_bf16,
+                                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (layout == QGEMM_LAYOUT_NT) return launch_blockscale_bpreshuffle(args, output_bf16, 0, stream);
+    qg::trace_reset();
+    if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
+        !flag01(output_bf16) || layout < 0 || layout > 3)
+        return hipErrorInvalidValue;
+    const auto& a = *args;
+    const bool at = layout == QGEMM_LAYOUT_TT || layout == QGEMM_LAYOUT_TN;
+    const bool bn = layout == QGEMM_LAYOUT_NN || layout == QGEMM_LAYOUT_TN;
+    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.m % 256 || a.n % 256 || a.k % 128 ||
+        !bounded_count(a.m, a.k, a.batch, 1) || !bounded_count(a.n, a.k, a.batch, 1) ||
+        !bounded_count(a.m, a.n, a.batch, output_bf16 ? 2 : 4) || !bounded_count(a.m, a.k / 128, a.batch, 1) ||
+        !bounded_count(a.n / 128, a.k / 128, a.batch, 1))
+        return hipErrorInvalidValue;
+    if (a.stride_a != (at ? a.m : a.k) || a.stride_b != (bn ? a.n : a.k) || a.stride_c != a.n ||
+        a.stride_a_batch != a.m * a.k || a.stride_b_batch != a.n * a.k || a.stride_c_batch != a.m * a.n ||
+        a.stride_sfa != a.m || a.stride_sfb != a.k / 128 || a.stride_sfa_batch != a.m * (a.k / 128) ||
+        a.stride_sfb_batch != (a.n / 128) * (a.k / 128))
+        return hipErrorInvalidValue;
+    if (!dma_aligned(a, false) || !aligned(a.ptr_c, output_bf16 ? 2 : 4)) return hipErrorInvalidValue;
+    Spans sp;
+    sp.add(a.ptr_c, uint64_t(a.m) * a.n * a.batch * (output_bf16 ? 2 : 4));
+    sp.add(a.ptr_a, uint64_t(a.stride_a_batch) * a.batch);
+    sp.add(a.ptr_b, uint64_t(a.stride_b_batch) * a.batch);
+    sp.add(a.ptr_sfa, uint64_t(a.stride_sfa_batch) * a.batch);
+    sp.add(a.ptr_sfb, uint64_t(a.stride_sfb_batch) * a.batch);
+    if (sp.overlap_any(sp.p[0], sp.bytes[0], 1)) return hipErrorInvalidValue;
+    // the canonical copies need the workspace: NULL is an error here
+    const size_t need = gemm_a8w8_blockscale_layout_workspace_bytes(args, layout);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256) || sp.overlap_any(workspace, need, 0))
+        return hipErrorInvalidValue;
+    hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    opus_gemm_scale_kargs c = a;    // the NT view
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (at) {
+        st = qg::launch_transpose(false, static_cast<const uint8_t*>(a.ptr_a), ws, a.m, a.k, a.m, a.batch,
+                                  (long long)a.m * a.k, (long long)a.m * a.k, stream);
+        if (st != hipSuccess) return st;
+        c.ptr_a = ws;
+        c.stride_a = a.k;
+        ws += round256((size_t)a.batch * a.m * a.k);
+    }
+    if (bn) {
+        st = qg::launch_transpose(true, static_cast<const uint8_t*>(a.ptr_b), ws, a.n, a.k, a.n, a.batch,
+                                  (long long)a.n * a.k, (long long)a.n * a.k, stream);
+        if (st != hipSuccess) return st;
+        c.ptr_b = ws;
+        c.stride_b = a.k;
+    }
+    TileArgs t{};
+    fill_common(t, c, a.k, output_bf16 ? 2 : 4);
+    t.sfa_sk = a.stride_sfa;
+    t.sfb_sn = a.stride_sfb;
+    return bn ? qg::launch_wide_bs8_w16(t, a.batch, output_bf16 == 1, stream)
+              : qg::launch_wide_bs8_raw(t, a.batch, output_bf16 == 1, stream);
+}
+
 // ------------------------------------------------ block-scale FP8, fp32 scales
-hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
-                                            size_t workspace_bytes, hipStream_t stream) {
+hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
+                                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
     qg::trace_reset();
     if (!args) return hipErrorInvalidValue;
     const auto& a = *args;
@@ -980,7 +1138,9 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
     if (a.batch > 1 && ((long long)a.stride_b_batch < bk || a.stride_b_batch % 16)) return hipErrorInvalidValue;
     sp.add(a.ptr_b, span(a.batch, a.stride_b_batch, 1, 0, bk, 1));
     if (sp.overlap_any(sp.p[0], sp.bytes[0], sp.n - 1)) return hipErrorInvalidValue;
-    st = check_workspace(workspace, workspace_bytes, gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(args), sp);
+    const BsfRoute r = route_bsf32(a.m, a.n, a.k / 128, a.batch, bk, false, kernel_id, workspace != nullptr);
+    if (!r.ok) return hipErrorInvalidValue;
+    st = check_workspace(workspace, workspace_bytes, r.ws_bytes, sp);
     if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
@@ -989,31 +1149,29 @@ hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
-    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const qg::BurstPlan bp = plan_bsf32_burst(a.m, a.n, a.k / 128, a.batch);
-    // (a split plan needs the workspace; without one the kernels below run unsplit)
-    if (bp.ok && (bp.splitk == 1 || workspace)) return run_burst(t, a.batch, bp, false, bk, bf16, workspace, stream);
-    const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bk, true);
-    if (pl.mid)
-        return run_mid(t, a.batch, pl, bf16, qg::MidKind::BS_KPANEL, workspace, workspace_bytes, a.k / 128, stream);
-    if (pl.skinny)
-        return run_skinny(SkinnyKind::BSF32_KPANEL, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128,
-                          stream);
-    // fp32 block scales: the eight-wave kernel with VGPR accumulators and a
-    // VALU rescale per K-tile (bsf32_gemm.hpp)
-    return qg::launch_bsf32(t, a.batch, bf16, false, stream);
+    return run_bsf32(r, t, a.batch, false, bk, out_dtype == QGEMM_OUT_BF16, workspace, workspace_bytes, a.k / 128,
+                     stream);
+}
+
+size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id) {
+    if (!args || args->k <= 0 || args->k % 128) return 0;
+    const BsfRoute r = route_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false,
+                                   kernel_id, true);
+    return r.ok ? r.ws_bytes : 0;
+}
+
+hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
+                                            size_t workspace_bytes, hipStream_t stream) {
+    return gemm_a8w8_blockscale_bpreshuffle_kid(args, out_dtype, QGEMM_KID_AUTO, workspace, workspace_bytes, stream);
 }
 
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args) {
-    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    const qg::BurstPlan bp = plan_bsf32_burst(args->m, args->n, args->k / 128, args->batch);
-    if (bp.ok) return burst_ws_bytes(bp, args->m, args->n, args->batch);
-    return plan_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, true).ws_bytes;
+    return gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(args, QGEMM_KID_AUTO);
 }
 
 // ------------------------------------------------ LDS-bypass block-scale FP8
-hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args, int out_dtype, void* workspace,
-                                          size_t workspace_bytes, hipStream_t stream) {
+hipError_t gemm_a8w8_blockscale_ldsbypass_kid(const opus_gemm_ldsbypass_kargs* args, int out_dtype, int kernel_id,
+                                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
     qg::trace_reset();
     if (!args) return hipErrorInvalidValue;
     const opus_gemm_scale_kargs a = from_ldsbypass(*args);
@@ -1026,7 +1184,12 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
         return hipErrorInvalidValue;
     sp.add(args->ptr_b_pp, span(a.batch, args->stride_b_pp_batch, 1, 0, bpp, 1));
     if (sp.overlap_any(sp.p[0], sp.bytes[0], sp.n - 1)) return hipErrorInvalidValue;
-    st = check_workspace(workspace, workspace_bytes, gemm_a8w8_blockscale_ldsbypass_workspace_bytes(args), sp);
+    // decode shapes: the burst kernel (B'' fragments straight into
+    // registers); other small M: the skinny kernel streams B'' into
+    // registers; large M: the tile kernels stage B'' blocks through LDS
+    const BsfRoute r = route_bsf32(a.m, a.n, a.k / 128, a.batch, bpp, true, kernel_id, workspace != nullptr);
+    if (!r.ok) return hipErrorInvalidValue;
+    st = check_workspace(workspace, workspace_bytes, r.ws_bytes, sp);
     if (st != hipSuccess) return st;
     st = check_arch();
     if (st != hipSuccess) return st;
@@ -1035,27 +1198,24 @@ hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args,
     t.sfa_sm = sfa_sm;
     t.sfa_sk = sfa_sk;
     t.sfb_sn = a.stride_sfb;
-    // decode shapes: the burst kernel (B'' fragments straight into
-    // registers); other small M: the skinny kernel streams B'' into
-    // registers; large M: the tile kernels stage B'' blocks through LDS
-    const qg::BurstPlan bp = plan_bsf32_burst(a.m, a.n, a.k / 128, a.batch);
-    if (bp.ok && (bp.splitk == 1 || workspace))
-        return run_burst(t, a.batch, bp, true, bpp, out_dtype == QGEMM_OUT_BF16, workspace, stream);
-    const Plan pl = plan_bsf32(a.m, a.n, a.k / 128, a.batch, bpp, false);
-    if (pl.mid)
-        return run_mid(t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, qg::MidKind::BS_FRAG, workspace,
-                       workspace_bytes, a.k / 128, stream);
-    if (!pl.skinny) return qg::launch_bsf32(t, a.batch, out_dtype == QGEMM_OUT_BF16, true, stream);
-    return run_skinny(SkinnyKind::BSF32_FRAG, t, a.batch, pl, out_dtype == QGEMM_OUT_BF16, workspace,
-                      workspace_bytes, a.k / 128, stream);
+    return run_bsf32(r, t, a.batch, true, bpp, out_dtype == QGEMM_OUT_BF16, workspace, workspace_bytes, a.k / 128,
+                     stream);
+}
+
+size_t gemm_a8w8_blockscale_ldsbypass_kid_workspace_bytes(const opus_gemm_ldsbypass_kargs* args, int kernel_id) {
+    if (!args || args->k <= 0 || args->k % 128 || args->n <= 0) return 0;
+    const BsfRoute r = route_bsf32(args->m, args->n, args->k / 128, args->batch,
+                                   (long long)frag_bytes(args->n, args->k), true, kernel_id, true);
+    return r.ok ? r.ws_bytes : 0;
+}
+
+hipError_t gemm_a8w8_blockscale_ldsbypass(const opus_gemm_ldsbypass_kargs* args, int out_dtype, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+    return gemm_a8w8_blockscale_ldsbypass_kid(args, out_dtype, QGEMM_KID_AUTO, workspace, workspace_bytes, stream);
 }
 
 size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_kargs* args) {
-    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    const qg::BurstPlan bp = plan_bsf32_burst(args->m, args->n, args->k / 128, args->batch);
-    if (bp.ok) return burst_ws_bytes(bp, args->m, args->n, args->batch);
-    return plan_bsf32(args->m, args->n, args->k / 128, args->batch, (long long)frag_bytes(args->n, args->k), false)
-        .ws_bytes;
+    return gemm_a8w8_blockscale_ldsbypass_kid_workspace_bytes(args, QGEMM_KID_AUTO);
 }
 
 // B' (K-panel, ptr_b, stride_b = 128) -> B'' (ptr_b_pp) on the GPU.

@@ -77,13 +77,16 @@ struct BurstPlan {
     double cost_us = 1e30;
 };
 
-inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long long max_counters) {
+// gate: apply the measured acceptance rule below (off when a caller forces
+// the burst kernel); max_split: largest K split considered
+inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long long max_counters, bool gate = true,
+                            int max_split = 16) {
     BurstPlan best;
     if (m < 1 || m > 64 || k_tiles < 1 || k_tiles > 64 || n < 1 || batch < 1 || cus < 1) return best;
     const int mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     for (int nb : {2, 1}) {
         const long long tiles = (long long)((n + 16 * nb - 1) / (16 * nb)) * batch;
-        for (int s = 1; s <= 16; ++s) {
+        for (int s = 1; s <= max_split; ++s) {
             const int kt_per = (k_tiles + s - 1) / s;
             const int split = (k_tiles + kt_per - 1) / kt_per;
             if (split != s) continue;
@@ -113,7 +116,7 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
     // burst kernel wins or ties for M <= 32 (M = 1-16: 1.05-1.35x); for
     // M = 33-64 only when one round of workgroups covers the plan and K is
     // split at most 5 ways (more rounds re-read the 64 rows of A per tile)
-    if (best.ok && best.mb == 4 &&
+    if (gate && best.ok && best.mb == 4 &&
         ((long long)best.n_tiles * batch * best.splitk > cus || best.splitk > 5))
         best.ok = false;
     return best;

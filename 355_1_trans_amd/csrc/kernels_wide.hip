@@ -53,6 +53,9 @@ hipError_t launch_wide_mx4_w16s(const TileArgs& a, int batch, bool bf16, int pan
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::W16>(a, batch, bf16, s);
 }
+hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
+    return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::RAW>(a, batch, bf16, s);
+}
 
 // E8M0 scales [rows][ngroups] (row pitch ld) -> panel-major [ngroups/pb][rows][pb]
 // for both operands (grid.z), one 16-byte piece per thread: consecutive

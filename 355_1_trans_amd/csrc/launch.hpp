@@ -27,6 +27,8 @@ hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int pane
 hipError_t launch_wide_mx4_w16s(const TileArgs& a, int batch, bool bf16, int panel_bytes, int persist_blocks,
                                 hipStream_t s);
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+// E8M0 block scales with row-major [N][K] B
+hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // E8M0 scales of A and B into the wide kernel's panel-major layout
 // [ngroups/pb][rows][pb] (pb = 16 or 32 bytes, ngroups % pb == 0)
 struct ScalePanelArgs {
@@ -81,6 +83,10 @@ hipError_t launch_quant_wgt_blocks(int fmt, bool bf16in, const void* w, long lon
 hipError_t launch_relayout(int layout, const uint8_t* src, uint8_t* dst, int n, int kbytes, long long ld,
                            hipStream_t st);
 hipError_t launch_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int kg, long long ld, hipStream_t st);
+// MN-major [K][X] bytes (pitch ld) -> [X][K] row-major, or shuffle_weight(16,16)
+// order with w16; X and K multiples of 64
+hipError_t launch_transpose(bool w16, const uint8_t* src, uint8_t* dst, int x_len, int k_len, long long ld,
+                            int batch, long long src_batch, long long dst_batch, hipStream_t st);
 
 // probe.hip
 hipError_t launch_probe(int32_t* dev_out, hipStream_t s);

@@ -110,6 +110,26 @@ typedef struct opus_gemm_ldsbypass_kargs {
 hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int output_bf16, int tiles,
                                   hipStream_t stream);
 
+/* Physical layouts of C[M,N] = A[M,K] x B[K,N] with the E8M0 block scales
+ * above: aiter's opus_gemm_mxfp8_{nn,tn,tt} (reference runner
+ * opus_mxfp8_layouts_trace_8192_20261027T005846Z/capture.py:42-62).
+ *   NT  A [M,K]; B shuffle_weight(16,16) of [N,K]  (= launch_blockscale_bpreshuffle)
+ *   NN  A [M,K]; B [K,N] N-contiguous             (stride_b = N)
+ *   TT  A [K,M] M-contiguous (stride_a = M); B [N,K] row-major (stride_b = K)
+ *   TN  A [K,M]; B [K,N]
+ * Scales, C, shape and density rules as launch_blockscale_bpreshuffle
+ * (stride_a_batch = M*K, stride_b_batch = N*K). NN / TT / TN bring each
+ * M- or N-contiguous operand into the NT operand layout inside `workspace`
+ * (gemm_a8w8_blockscale_layout_workspace_bytes; required, 256-byte aligned,
+ * no overlap) and run the NT kernel. */
+#define QGEMM_LAYOUT_NT 0
+#define QGEMM_LAYOUT_NN 1
+#define QGEMM_LAYOUT_TT 2
+#define QGEMM_LAYOUT_TN 3
+hipError_t gemm_a8w8_blockscale_layout(const opus_gemm_scale_kargs* args, int layout, int output_bf16,
+                                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_blockscale_layout_workspace_bytes(const opus_gemm_scale_kargs* args, int layout);
+
 /* ------------------------------------------------------------------ */
 /* Block-scale FP8, fp32 scales (1x128 activation, 128x128 weight).     */
 /* ------------------------------------------------------------------ */
@@ -139,6 +159,27 @@ size_t gemm_a8w8_blockscale_ldsbypass_workspace_bytes(const opus_gemm_ldsbypass_
 /* GPU repack B' (K-panel, ptr_b) -> B'' (ptr_b_pp); the reference's
  * gemm_a8w8_blockscale_ldsbypass_repack_kernel (LBP host.cc:289-294). */
 hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs* args, hipStream_t stream);
+
+/* Kernel selection for the two fp32 block-scale entries: the kernelId of
+ * the reference's tuned dispatch (opus_a8w8_bpreshuffle_integration_and_
+ * benchmark.md section 3-4: an explicit id skips the tuned-table lookup).
+ * AUTO is the library's own plan (what the entries above run); the others
+ * force one kernel family with that family's tile and K-split plan, and
+ * return hipErrorInvalidValue for shapes the family cannot take (DECODE:
+ * M <= 64 and the K-panel B' only; BURST: M <= 64, K <= 8192).  Workspace
+ * contract as above, queried per id. */
+#define QGEMM_KID_AUTO    0  /* library plan */
+#define QGEMM_KID_TILE256 1  /* eight-wave 256x256 tiles */
+#define QGEMM_KID_MID     2  /* four-wave 128x128 tiles, split-K */
+#define QGEMM_KID_SKINNY  3  /* skinny-M tiles (16-64 rows), split-K */
+#define QGEMM_KID_DECODE  4  /* decode kernel: waves split N, A shared through LDS */
+#define QGEMM_KID_BURST   5  /* burst kernel: every load issued up front */
+hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
+                                                void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);
+hipError_t gemm_a8w8_blockscale_ldsbypass_kid(const opus_gemm_ldsbypass_kargs* args, int out_dtype, int kernel_id,
+                                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_blockscale_ldsbypass_kid_workspace_bytes(const opus_gemm_ldsbypass_kargs* args, int kernel_id);
 
 /* ------------------------------------------------------------------ */
 /* MXFP8: e4m3 x e4m3 with one E8M0 scale per 32 K elements.            */
