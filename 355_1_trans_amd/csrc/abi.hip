@@ -370,7 +370,22 @@ hipError_t run_burst(const TileArgs& t, int batch, const qg::BurstPlan& pl, bool
 Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool decode_ok) {
     const int cus = device_cus();
     Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false, decode_ok, decode_ok);
-    plan_mid(p, m, n, k_tiles, batch, cus);
+    // 64 < M <= 128: half of every 256-row tile would be padding, so the
+    // 128 x 128 kernel even with many tiles (M = 128, N = 65536, K = 1536:
+    // 30.2 -> 25.7 us)
+    plan_mid(p, m, n, k_tiles, batch, cus, m > kMidMinM && m <= 128);
+    if (p.mid && m <= 320) {
+        // one round of skinny workgroups (3/4 to all of the CUs, no K split),
+        // each streaming <= 768 KB of A and B, beats the 128 x 128 kernel's
+        // K split (traced dsv4 shapes, N = 1536 / 2048, K = 7168, M = 66-312:
+        // 1.2-1.4x; N = 7168, K = 3072, M = 128: 21.9 -> 17.7 us); more bytes
+        // per workgroup (N = 6144, K = 7168) or a second round (M = 192,
+        // N = 1536) stay on the 128 x 128 kernel
+        const Plan s = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, true, false);
+        const long long wgs = (long long)s.n_tiles * s.m_tiles * batch;
+        const long long wg_bytes = 16LL * (s.mb + s.nb) * k_tiles * 128;
+        if (s.splitk == 1 && wgs <= cus && 4 * wgs >= 3LL * cus && wg_bytes <= 768 * 1024) p = s;
+    }
     return p;
 }
 

@@ -94,9 +94,10 @@ def parse():
                    help="block-scale fp32 workloads: pass A's scales column-major [K/128][M] (the reference's "
                         "layout) instead of BASELINE's row-major [M][K/128]")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--sweep", action="store_true",
-                   help="BASELINE configs[2]: time the block-scale shape sweep (bpreshuffle and ldsbypass), "
-                        "one JSON line per shape")
+    p.add_argument("--sweep", nargs="?", const="configs2", default=None, choices=["configs2", "dsv4"],
+                   help="time a block-scale shape sweep (bpreshuffle and ldsbypass), one JSON line per shape: "
+                        "configs2 = BASELINE configs[2] (default), dsv4 = the 125 traced DeepSeek-V4 a8w8 shapes "
+                        "(355_1_trans_amd/configs/dsv4_a8w8_shapes.csv)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run only a plain 256 MiB device copy 5 times (PMC byte-counter calibration)")
     return p.parse_args()
@@ -366,8 +367,21 @@ SWEEP_M = (1, 16, 64, 256, 1024, 4096, 16384)
 SWEEP_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168))
 
 
+def sweep_shapes(which):
+    """{(N, K): [M, ...]} of a sweep, in file / table order."""
+    import csv
+    if which == "configs2":
+        return {(n, k): list(SWEEP_M) for n, k in SWEEP_NK}
+    groups = {}
+    with open(ROOT / "355_1_trans_amd" / "configs" / "dsv4_a8w8_shapes.csv", newline="") as fh:
+        for r in csv.DictReader(fh):
+            groups.setdefault((int(r["N"]), int(r["K"])), []).append(int(r["M"]))
+    return groups
+
+
 def sweep(args):
-    """M x (N, K) for both block-scale entry points.
+    """Block-scale shape sweep for both entry points (library plan, bf16
+    out): BASELINE configs[2] (M x (N, K)) or the traced dsv4 shapes.
     HBM-bound shapes (M <= 256) replay a graph over rotating weight copies
     (> 512 MB, beyond the last-level cache); the others launch back to back."""
     import torch
@@ -376,12 +390,12 @@ def sweep(args):
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(dev)
-    for n, k in SWEEP_NK:
+    for (n, k), ms in sweep_shapes(args.sweep).items():
         qb, sb = q.quant_fp8_blockscale(randn((n, k), 1, dev), "128x128")
         bk = q.shuffle_b_kpanel(qb.view(torch.uint8))
         bpp = q.ldsbypass_pack_b(qb.view(torch.uint8))
         kg = k // 128
-        for m in SWEEP_M:
+        for m in ms:
             qa, sa = q.quant_fp8_blockscale(randn((m, k), 0, dev), "1x128")
             qa = qa.view(torch.uint8)
             C = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
@@ -397,6 +411,7 @@ def sweep(args):
                 wsb = max(1, wq(ctypes.byref(calls[0])))
                 ws = torch.zeros((wsb + 255) // 256 * 256, dtype=torch.uint8, device=dev)
                 sptr = ctypes.c_void_p(stream.cuda_stream)
+                torch.cuda.synchronize()    # inputs made on the default stream; launches on `stream`
 
                 def launch(i):
                     st = launch_fn(ctypes.byref(calls[i % len(calls)]), ws.data_ptr(), ws.numel(), sptr)
@@ -409,7 +424,7 @@ def sweep(args):
                 alg = m * k + sa.numel() * 4 + b_bytes + m * n * 2
                 tf = flops / (ms * 1e-3) / 1e12
                 gbps = alg / (ms * 1e-3) / 1e9
-                print(json.dumps({"sweep": "configs[2]", "variant": variant, "M": m, "N": n, "K": k,
+                print(json.dumps({"sweep": args.sweep, "variant": variant, "M": m, "N": n, "K": k,
                                   "us": round(ms * 1e3, 2), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / 5000.0, 4),
                                   "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_GBPS, 4),
                                   "bound": "hbm" if hbm else "mfma", "kernel": q.last_launch()}), flush=True)
