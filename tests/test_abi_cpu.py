@@ -154,6 +154,16 @@ def test_ldsbypass_host_pack_matches_permutation(qgemm, n, k):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 512), (256, 1024)])
+def test_ldsbypass_b_is_shuffle_weight_16x16(qgemm, n, k):
+    """For N % 16 == 0 the LDS-bypass B'' is byte for byte aiter's
+    shuffle_weight(16,16) of B (the 16x16x128 fragment order): aiter-shuffled
+    weights feed gemm_a8w8_blockscale_ldsbypass as they are."""
+    b = np.random.default_rng(n + k).integers(0, 256, (n, k), dtype=np.uint8)
+    assert np.array_equal(qgemm.ldsbypass_pack_b(torch.from_numpy(b)).numpy().reshape(-1),
+                          O.shuffle_weight_16x16(b).reshape(-1))
+
+
 def test_python_layout_helpers(qgemm):
     b = torch.from_numpy(np.random.default_rng(22).integers(0, 256, (32, 256), dtype=np.uint8))
     assert np.array_equal(qgemm.shuffle_b_kpanel(b).numpy(), O.shuffle_b_kpanel(b.numpy()))

@@ -146,14 +146,16 @@ def test_blockscale_e8m0_bench_kernel_full_size(qgemm, gpu):
 
 
 SWEEP_NK = [(24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168)]
+SWEEP_M = [1, 16, 64, 256, 1024, 4096, 16384]
 
 
+@pytest.mark.parametrize("m", SWEEP_M)
 @pytest.mark.parametrize("n,k", SWEEP_NK)
 @pytest.mark.parametrize("variant", ["bpreshuffle", "ldsbypass"])
-def test_blockscale_sweep_large_m(qgemm, gpu, n, k, variant):
-    """configs[2] cells at M = 4096 (the tile kernels the sweep times for
-    M >= 1024), both B layouts, at 4096 sampled points."""
-    m = 4096
+def test_blockscale_sweep_cell(qgemm, gpu, m, n, k, variant):
+    """Every configs[2] cell (bench.py --sweep), both B layouts, through the
+    entry and plan the sweep times, with its workspace: 4096 sampled points
+    (every output when M*N is smaller) against the oracle."""
     a, b = O.randn((m, k), 2, 0), O.randn((n, k), 2, 1)
     qa, sa = O.quant_bs_act(a)
     qb, sb = O.quant_bs_wgt(b)
@@ -165,7 +167,11 @@ def test_blockscale_sweep_large_m(qgemm, gpu, n, k, variant):
         y = qgemm.gemm_a8w8_bpreshuffle(A, bk.view(torch.float8_e4m3fn), dev(sa), dev(sb), dtype=torch.bfloat16)
     else:
         y = qgemm.gemm_a8w8_ldsbypass(A, qgemm.ldsbypass_repack(bk), dev(sa), dev(sb), n, dtype=torch.bfloat16)
+    kernel = qgemm.last_launch()
     torch.cuda.synchronize()
-    rows, cols = _points(m, n, 3)
+    if m * n <= N_POINTS:
+        rows, cols = (x.reshape(-1).astype(np.int32) for x in np.meshgrid(np.arange(m), np.arange(n), indexing="ij"))
+    else:
+        rows, cols = _points(m, n, 3)
     ref = O.gemm_bs_fp32_points(qa, qb, sa, sb, rows, cols)
-    assert_close(ref, y.float().cpu().numpy()[rows, cols], f"bs {variant} {m}x{n}x{k}")
+    assert_close(ref, y.float().cpu().numpy()[rows, cols], f"bs {variant} {m}x{n}x{k} ({kernel})")
