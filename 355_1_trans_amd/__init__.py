@@ -100,6 +100,12 @@ EXPORTS = {
                                                           ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "gemm_a8w8_blockscale_ldsbypass_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LdsBypassKargs),
                                                                              ctypes.c_int]),
+    "gemm_a8w8_mxfp8_kid": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a8w8_mxfp8_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), ctypes.c_int]),
+    "gemm_a4w4_mxfp4_kid": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a4w4_mxfp4_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), ctypes.c_int]),
     "gemm_a4w4_mxfp4_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_void_p]),
     "gemm_a8w8_mxfp8": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),

@@ -686,6 +686,139 @@ hipError_t run_bsf32(const BsfRoute& r, const TileArgs& t, int batch, bool frag,
     }
 }
 
+// Kernel routes of the MX entries (QGEMM_KID_*): AUTO follows the plans
+// above (row-streaming kernel for M <= 8, burst kernel where its gate
+// accepts, skinny / decode, 128 x 128, 256 x 256 tiles); a forced id runs
+// that family with its own plan or fails for shapes it cannot take.
+struct MxRoute {
+    int kid = QGEMM_KID_AUTO;
+    bool ok = false;
+    Plan pl;
+    StreamPlan sp;
+    qg::BurstPlan bp;
+    size_t ws_bytes = 0;
+};
+
+// Burst plan for MX row-major B: the fp32-block-scale gate, and only up to
+// 32 K-tiles (4 KB of K per row) and past M = kStreamMaxM.  Measured
+// (graph-replayed, MXFP4 / MXFP8 us): short K gains 1.1-1.5x over the skinny
+// kernel (fp4 M = 32: N = 24576, K = 1536 12.4 -> 9.4; N = 7168, K = 2048
+// 8.1 -> 5.6; fp8 M = 16, N = 24576, K = 1536 15.6 -> 10.7), long K loses
+// (fp4 configs[4] K = 16384, M = 16 / 32: 15.8 / 19.2 on the skinny kernel,
+// 17.7 / 29.2 as a burst); M <= 8 stays on the row-streaming kernel, whose
+// contiguous row runs 16-row fragments cannot match (M = 1: 12.8 vs 17.5)
+qg::BurstPlan plan_mx_burst(int m, int n, int k_tiles, int batch, bool gate) {
+    if (gate && (m <= kStreamMaxM || k_tiles > 32)) return qg::BurstPlan{};
+    return qg::burst_plan(m, n, k_tiles, batch, device_cus(), kMaxCounters, gate, 16, true);
+}
+
+MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws) {
+    MxRoute r;
+    r.kid = kid;
+    if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % (fp4 ? 256 : 128)) return r;
+    const int kt = a.k / (fp4 ? 256 : 128);
+    const long long bb = (long long)a.n * (fp4 ? a.k / 2 : a.k);
+    const int cus = device_cus();
+    switch (kid) {
+        case QGEMM_KID_AUTO: {
+            r.pl = plan_mx(a.m, a.n, kt, a.batch, bb, fp4);
+            r.sp = plan_stream(a.m, a.n, a.k, a.batch, fp4);
+            r.bp = plan_mx_burst(a.m, a.n, kt, a.batch, true);
+            r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
+                                   r.pl.skinny || r.pl.mid ? 0 : scale_panel_bytes(a)});
+            r.ok = true;
+            if (stream_ok(a, fp4)) {
+                // without the K split's workspace: the skinny kernel, unsplit
+                r.kid = r.sp.splitk == 1 || have_ws ? QGEMM_KID_STREAM : QGEMM_KID_SKINNY;
+                if (r.kid == QGEMM_KID_SKINNY && !r.pl.skinny) r.pl = plan_gemm(a.m, a.n, kt, a.batch, bb, cus, true, false);
+                return r;
+            }
+            if (r.bp.ok && (r.bp.splitk == 1 || have_ws)) {
+                r.kid = QGEMM_KID_BURST;
+                return r;
+            }
+            r.kid = r.pl.mid ? QGEMM_KID_MID
+                             : r.pl.skinny ? (r.pl.decode ? QGEMM_KID_DECODE : QGEMM_KID_SKINNY) : QGEMM_KID_TILE256;
+            return r;
+        }
+        case QGEMM_KID_TILE256:
+            r.ws_bytes = scale_panel_bytes(a);
+            break;
+        case QGEMM_KID_MID:
+            plan_mid(r.pl, a.m, a.n, kt, a.batch, cus, true);
+            r.ws_bytes = r.pl.ws_bytes;
+            break;
+        case QGEMM_KID_SKINNY:
+            r.pl = plan_gemm(a.m, a.n, kt, a.batch, bb, cus, true, false);
+            r.ws_bytes = r.pl.ws_bytes;
+            break;
+        case QGEMM_KID_DECODE:
+            if (a.m > 64) return r;
+            r.pl.skinny = true;
+            plan_decode(r.pl, a.m, a.n, kt, a.batch, bb, cus);
+            r.ws_bytes = r.pl.ws_bytes;
+            break;
+        case QGEMM_KID_BURST:
+            r.bp = plan_mx_burst(a.m, a.n, kt, a.batch, false);
+            if (!r.bp.ok) return r;
+            r.ws_bytes = burst_ws_bytes(r.bp, a.m, a.n, a.batch);
+            if (r.bp.splitk > 1 && !have_ws)
+                r.bp = qg::burst_plan(a.m, a.n, kt, a.batch, cus, kMaxCounters, false, 1, true);
+            if (!r.bp.ok) return r;
+            break;
+        case QGEMM_KID_STREAM:
+            if (!stream_ok(a, fp4)) return r;
+            r.sp = plan_stream(a.m, a.n, a.k, a.batch, fp4);
+            r.ws_bytes = r.sp.ws_bytes;
+            if (r.sp.splitk > 1 && !have_ws) return r;    // the row-streaming kernel needs its split
+            break;
+        default:
+            return r;
+    }
+    r.ok = true;
+    return r;
+}
+
+hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, bool bf16, void* ws,
+                  size_t ws_bytes, hipStream_t stream) {
+    const int kt = a.k / (fp4 ? 256 : 128);
+    const SkinnyKind sk = fp4 ? SkinnyKind::MX4_RAW : SkinnyKind::MX8_RAW;
+    switch (r.kid) {
+        case QGEMM_KID_STREAM: {
+            hipError_t st = hipSuccess;
+            if (!run_stream(t, a.k, a.batch, fp4, bf16, ws, ws_bytes, stream, &st)) return hipErrorInvalidValue;
+            return st;
+        }
+        case QGEMM_KID_BURST: {
+            qg::BurstArgs b{};
+            b.t = t;
+            b.splitk = r.bp.splitk;
+            b.kt_per_split = r.bp.kt_per_split;
+            b.n_tiles = r.bp.n_tiles;
+            b.b_bytes = (long long)(a.n - 1) * a.stride_b + (fp4 ? a.k / 2 : a.k);
+            if (r.bp.splitk > 1) {
+                b.counters = static_cast<unsigned*>(ws);
+                b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+            }
+            return qg::launch_burst_mx(b, fp4, r.bp.mb, r.bp.nb, r.bp.waves, a.batch, bf16, stream);
+        }
+        case QGEMM_KID_SKINNY:
+        case QGEMM_KID_DECODE:
+            return run_skinny(sk, t, a.batch, r.pl, bf16, ws, ws_bytes, kt, stream);
+        case QGEMM_KID_MID:
+            t.sfa_sk = t.sfb_sk = fp4 ? 8 : 4;
+            return run_mid(t, a.batch, r.pl, bf16, fp4 ? qg::MidKind::MX4 : qg::MidKind::MX8, ws, ws_bytes, kt,
+                           stream);
+        default: {
+            // fp8: 16-byte panels (32-byte ones cover 8 K-tiles and measured 1%
+            // slower); fp4: 32-byte panels (4 K-tiles, two DMA lanes per scale
+            // row) need whole panels, K % 1024 == 0
+            const int pb = fp4 ? (mx_wide_panels(a) ? (a.k % 1024 == 0 ? 32 : 16) : 8) : (mx_wide_panels(a) ? 16 : 4);
+            return run_wide_mx(t, a, fp4, pb, bf16, ws, ws_bytes, stream);
+        }
+    }
+}
+
 // Byte ranges of a call's operands (C first), for the overlap checks of the
 // output and of the workspace.
 struct Spans {
@@ -823,87 +956,61 @@ opus_gemm_scale_kargs from_ldsbypass(const opus_gemm_ldsbypass_kargs& l) {
 
 extern "C" {
 
-// ---------------------------------------------------------------- MXFP8
+// ---------------------------------------------------------------- MXFP8 / MXFP4
+static hipError_t mx_entry(const opus_gemm_scale_kargs* args, bool fp4, int out_dtype, int kernel_id,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    qg::trace_reset();
+    Spans sp;
+    hipError_t st = validate_mx(args, out_dtype, args ? (fp4 ? args->k / 2 : args->k) : 0, fp4 ? 256 : 128, &sp);
+    if (st != hipSuccess) return st;
+    const auto& a = *args;
+    const MxRoute r = route_mx(a, fp4, kernel_id, workspace != nullptr);
+    if (!r.ok) return hipErrorInvalidValue;
+    st = check_workspace(workspace, workspace_bytes, r.ws_bytes, sp);
+    if (st != hipSuccess) return st;
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    TileArgs t{};
+    fill_common(t, a, fp4 ? a.k / 2 : a.k, out_dtype ? 2 : 4);
+    t.sfa_sm = a.stride_sfa;
+    t.sfb_sn = a.stride_sfb;
+    return run_mx(r, t, a, fp4, out_dtype == QGEMM_OUT_BF16, workspace, workspace_bytes, stream);
+}
+
+static size_t mx_workspace(const opus_gemm_scale_kargs* args, bool fp4, int kernel_id) {
+    if (!args) return 0;
+    const MxRoute r = route_mx(*args, fp4, kernel_id, true);
+    return r.ok ? r.ws_bytes : 0;
+}
+
 hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-    qg::trace_reset();
-    Spans sp;
-    hipError_t st = validate_mx(args, out_dtype, args ? args->k : 0, 128, &sp);
-    if (st != hipSuccess) return st;
-    st = check_workspace(workspace, workspace_bytes, gemm_a8w8_mxfp8_workspace_bytes(args), sp);
-    if (st != hipSuccess) return st;
-    st = check_arch();
-    if (st != hipSuccess) return st;
-    const auto& a = *args;
-    TileArgs t{};
-    fill_common(t, a, a.k, out_dtype ? 2 : 4);
-    t.sfa_sm = a.stride_sfa;
-    t.sfb_sn = a.stride_sfb;
-    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_mx(a.m, a.n, a.k / 128, a.batch, (long long)a.n * a.k, false);
-    if (stream_ok(a, false)) {
-        if (run_stream(t, a.k, a.batch, false, bf16, workspace, workspace_bytes, stream, &st)) return st;
-        // the K split's workspace is missing: the skinny kernel, without a split
-        return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, nullptr, 0, a.k / 128, stream);
-    }
-    if (pl.skinny)
-        return run_skinny(SkinnyKind::MX8_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 128, stream);
-    if (pl.mid) {
-        t.sfa_sk = t.sfb_sk = 4;
-        return run_mid(t, a.batch, pl, bf16, qg::MidKind::MX8, workspace, workspace_bytes, a.k / 128, stream);
-    }
-    // (32-byte panels would cover 8 K-tiles; the loop then unrolls by 8, and
-    // measured 1% slower than 16-byte panels for fp8)
-    return run_wide_mx(t, a, false, mx_wide_panels(a) ? 16 : 4, bf16, workspace, workspace_bytes, stream);
+    return mx_entry(args, false, out_dtype, QGEMM_KID_AUTO, workspace, workspace_bytes, stream);
 }
-
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args) {
-    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 128 || args->batch <= 0) return 0;
-    const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, false);
-    const Plan pl = plan_mx(args->m, args->n, args->k / 128, args->batch, (long long)args->n * args->k, false);
-    return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny || pl.mid ? 0 : scale_panel_bytes(*args)});
+    return mx_workspace(args, false, QGEMM_KID_AUTO);
+}
+hipError_t gemm_a8w8_mxfp8_kid(const opus_gemm_scale_kargs* args, int out_dtype, int kernel_id, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
+    return mx_entry(args, false, out_dtype, kernel_id, workspace, workspace_bytes, stream);
+}
+size_t gemm_a8w8_mxfp8_kid_workspace_bytes(const opus_gemm_scale_kargs* args, int kernel_id) {
+    return mx_workspace(args, false, kernel_id);
 }
 
-// ---------------------------------------------------------------- MXFP4
 hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
-    qg::trace_reset();
-    Spans sp;
-    hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256, &sp);
-    if (st != hipSuccess) return st;
-    st = check_workspace(workspace, workspace_bytes, gemm_a4w4_mxfp4_workspace_bytes(args), sp);
-    if (st != hipSuccess) return st;
-    st = check_arch();
-    if (st != hipSuccess) return st;
-    const auto& a = *args;
-    TileArgs t{};
-    fill_common(t, a, a.k / 2, out_dtype ? 2 : 4);
-    t.sfa_sm = a.stride_sfa;
-    t.sfb_sn = a.stride_sfb;
-    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const Plan pl = plan_mx(a.m, a.n, a.k / 256, a.batch, (long long)a.n * a.k / 2, true);
-    if (stream_ok(a, true)) {
-        if (run_stream(t, a.k, a.batch, true, bf16, workspace, workspace_bytes, stream, &st)) return st;
-        // the K split's workspace is missing: the skinny kernel, without a split
-        return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, nullptr, 0, a.k / 256, stream);
-    }
-    if (pl.skinny)
-        return run_skinny(SkinnyKind::MX4_RAW, t, a.batch, pl, bf16, workspace, workspace_bytes, a.k / 256, stream);
-    if (pl.mid) {
-        t.sfa_sk = t.sfb_sk = 8;
-        return run_mid(t, a.batch, pl, bf16, qg::MidKind::MX4, workspace, workspace_bytes, a.k / 256, stream);
-    }
-    // 32-byte panels (4 K-tiles, two DMA lanes per scale row) need whole
-    // panels: K % 1024 == 0
-    const int pb = mx_wide_panels(a) ? (a.k % 1024 == 0 ? 32 : 16) : 8;
-    return run_wide_mx(t, a, true, pb, bf16, workspace, workspace_bytes, stream);
+    return mx_entry(args, true, out_dtype, QGEMM_KID_AUTO, workspace, workspace_bytes, stream);
 }
-
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args) {
-    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
-    const StreamPlan sp = plan_stream(args->m, args->n, args->k, args->batch, true);
-    const Plan pl = plan_mx(args->m, args->n, args->k / 256, args->batch, (long long)args->n * args->k / 2, true);
-    return std::max({sp.ok ? sp.ws_bytes : 0, pl.ws_bytes, pl.skinny || pl.mid ? 0 : scale_panel_bytes(*args)});
+    return mx_workspace(args, true, QGEMM_KID_AUTO);
+}
+hipError_t gemm_a4w4_mxfp4_kid(const opus_gemm_scale_kargs* args, int out_dtype, int kernel_id, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
+    return mx_entry(args, true, out_dtype, kernel_id, workspace, workspace_bytes, stream);
+}
+size_t gemm_a4w4_mxfp4_kid_workspace_bytes(const opus_gemm_scale_kargs* args, int kernel_id) {
+    return mx_workspace(args, true, kernel_id);
 }
 
 // ------------------------------------------------ MXFP4, aiter bpreshuffle operands

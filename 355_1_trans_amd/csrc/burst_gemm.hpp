@@ -1,5 +1,7 @@
-// Burst GEMM for fp8 decode shapes with fp32 block scales (M <= 64) on
-// gfx950: every global load of a workgroup's K slice is issued in one burst.
+// Burst GEMM for decode shapes (M <= 64) on gfx950: every global load of a
+// workgroup's K slice is issued in one burst.  fp8 with fp32 block scales
+// (K-panel B' or fragment-order B''), or MXFP8 / MXFP4 with row-major B and
+// row-major E8M0 scales.
 //
 // A decode GEMM streams B once; at configs[0] size (11 MB) the whole launch
 // lasts a few microseconds, so what bounds it is how many bytes are in flight
@@ -22,11 +24,14 @@
 //    fragment-order B'', the two 1 KB halves that already are the MFMA
 //    operands), A's rows (whole lines, from L2: every N tile re-reads A) and
 //    the fp32 block scales -- into registers;
-//  * per K-tile the wave writes its A (and B') lines into its own LDS slot,
-//    XOR-swizzled, and reads them back as 16x16x128 fragments (the LDS unit
-//    executes one wave's accesses in order, so one slot serves every K-tile
-//    with no barrier); unscaled MFMA partials are rescaled in VALU,
-//    acc += part * (sa * sb), the reference's scale-then-sum order;
+//  * per K-tile the wave writes its A (and B' or row-major B) lines into its
+//    own LDS slot, XOR-swizzled, and reads them back as 16x16x128 fragments
+//    (the LDS unit executes one wave's accesses in order, so one slot serves
+//    every K-tile with no barrier); fp32 block scales: unscaled MFMA partials
+//    rescaled in VALU, acc += part * (sa * sb), the reference's
+//    scale-then-sum order; MX: the E8M0 bytes ride on the scaled MFMA (fp8:
+//    one instruction per K-tile, the lane group's byte of the row's 4; fp4:
+//    two, chunks q and q + 4, bytes q and q + 4 of the row's 8);
 //  * the waves' partial tiles meet in LDS and are summed in wave order;
 //  * K is split over workgroups (grid.x = n_tiles * splitk): fp32 partial
 //    tiles with device-coherent stores, one relaxed counter atomic per
@@ -37,6 +42,8 @@
 // L = 16q + r holds row r, fp8 16-byte chunks q and q+4; srcA = B,
 // srcB = A; accumulator of lane L holds C[m = r][n = 4q .. 4q+3].
 #pragma once
+#include <type_traits>
+
 #include "skinny_gemm.hpp"
 
 namespace qg {
@@ -53,8 +60,10 @@ struct BurstArgs {
 // workgroup (16 waves leave 128 VGPRs per wave); the kernel is instantiated
 // for 1, 2, 4 and 8 (up to this) K-tiles per wave and launched with the
 // smallest that covers the slice.
-__host__ __device__ constexpr int burst_max_kpw(int mb, int nb, int waves) {
-    return waves == 16 ? (mb <= 2 ? 4 : 0) : (mb * nb <= 2 ? 8 : 4);
+// MX keeps the rows' E8M0 bytes of every K-tile in registers as well (fp4:
+// 8 bytes per row), which leaves 16-wave 32 x 32 tiles room for 2.
+__host__ __device__ constexpr int burst_max_kpw(int mb, int nb, int waves, bool mx = false) {
+    return waves == 16 ? (mb <= 2 ? (mx && mb * nb > 2 ? 2 : 4) : 0) : (mb * nb <= 2 ? 8 : 4);
 }
 constexpr int kBurstLdsMax = 159 * 1024;    // 160 KB per CU, less the kernel's few scalar LDS words
 // LDS of one workgroup: a slot of (MB + NB) 2 KB blocks per wave (B'' needs
@@ -80,7 +89,7 @@ struct BurstPlan {
 // gate: apply the measured acceptance rule below (off when a caller forces
 // the burst kernel); max_split: largest K split considered
 inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long long max_counters, bool gate = true,
-                            int max_split = 16) {
+                            int max_split = 16, bool mx = false) {
     BurstPlan best;
     if (m < 1 || m > 64 || k_tiles < 1 || k_tiles > 64 || n < 1 || batch < 1 || cus < 1) return best;
     const int mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
@@ -92,7 +101,7 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
             if (split != s) continue;
             int waves = 0;
             for (int w : {8, 16})
-                if (!waves && (kt_per + w - 1) / w <= burst_max_kpw(mb, nb, w) &&
+                if (!waves && (kt_per + w - 1) / w <= burst_max_kpw(mb, nb, w, mx) &&
                     burst_lds_bytes(mb, nb, w, true) <= kBurstLdsMax)
                     waves = w;
             if (!waves) continue;
@@ -122,13 +131,19 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
     return best;
 }
 
-template <BLay BL, int MB, int NB, int WAVES, int KPW, bool BF16>
+template <int FMT, BLay BL, int MB, int NB, int WAVES, int KPW, bool BF16>
 __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs bp) {
     constexpr int kBurstWaves = WAVES;
-    static_assert(BL == BLay::KPANEL || BL == BLay::FRAG, "K-panel B' or fragment-order B''");
+    // RAW: MXFP8 / MXFP4 with row-major B and E8M0 scales; else fp8 with
+    // fp32 block scales on B' (K-panel) or B'' (fragment order)
+    constexpr bool MX = BL == BLay::RAW;
+    constexpr bool FP4 = FMT == kFmtFp4;
+    static_assert(BL == BLay::KPANEL || BL == BLay::FRAG || BL == BLay::RAW, "B layout");
+    static_assert(MX || !FP4, "fp4 comes with E8M0 scales");
     static_assert((MB == 1 || MB == 2 || MB == 4) && (NB == 1 || NB == 2), "tile shape");
     constexpr int BKB = 128;
-    constexpr bool STAGE_B = BL == BLay::KPANEL;          // B' goes through LDS; B'' already is fragment order
+    constexpr int KT_SC = FP4 ? 8 : 4;                    // MX: scale bytes per row and K-tile
+    constexpr bool STAGE_B = BL != BLay::FRAG;            // B' / row-major B go through LDS; B'' already is fragment order
     constexpr int SLOT = (MB + (STAGE_B ? NB : 0)) * 2048; // one K-tile of the wave's A (and B') lines
     constexpr int LDS_BYTES = burst_lds_bytes(MB, NB, WAVES, STAGE_B);
     static_assert(LDS_BYTES <= kBurstLdsMax, "LDS");
@@ -139,7 +154,7 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
     QG_LDS uint8_t* const lds = (QG_LDS uint8_t*)lds_mem;
 
     const TileArgs& p = bp.t;
-    const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDC = p.ldc;
+    const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
     const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
     const int nk = KB / BKB;
     const int nt = blockIdx.x % bp.n_tiles, sk = blockIdx.x / bp.n_tiles, bz = blockIdx.y;
@@ -147,6 +162,7 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
     const int kt_begin = sk * bp.kt_per_split;
     const int kt_end = min(nk, kt_begin + bp.kt_per_split);
     const int per_wave = (bp.kt_per_split + kBurstWaves - 1) / kBurstWaves;    // <= KPW (host plan)
+    static_assert(KPW <= burst_max_kpw(MB, NB, WAVES, MX), "registers");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
     const int q = L >> 4, l16 = L & 15;
     const int kw0 = kt_begin + w * per_wave;
@@ -154,8 +170,9 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
 
     const uint8_t* A = p.a + bz * p.a_batch;
     const uint8_t* B = p.b + bz * p.b_batch;
-    const float* SFA = (const float*)p.sfa + bz * p.sfa_batch;
-    const float* SFB = (const float*)p.sfb + bz * p.sfb_batch;
+    // scale bases: fp32 elements (block scales) or E8M0 bytes (MX)
+    const void* SFA = MX ? (const void*)(p.sfa + bz * p.sfa_batch) : (const void*)((const float*)p.sfa + bz * p.sfa_batch);
+    const void* SFB = MX ? (const void*)(p.sfb + bz * p.sfb_batch) : (const void*)((const float*)p.sfb + bz * p.sfb_batch);
     auto rsrc = [](const void* base, int bytes) __attribute__((always_inline)) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
     };
@@ -166,14 +183,23 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
     // lane L taking row 8h + L/8, 16-byte chunk L%8
     i32x4 av[KPW][MB][2], bv[KPW][NB][2];
     float sa[KPW][MB], sb[KPW];
-    int a_off[MB][2];
+    // MX: the row's scale bytes of the K-tile (fp8 one dword, fp4 two)
+    using SX = std::conditional_t<FP4, u32x2, uint32_t>;
+    SX xa[KPW][MB], xb[KPW][NB];
+    int a_off[MB][2], b_off[NB][2];
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h) a_off[i][h] = min(16 * i + 8 * h + (L >> 3), M - 1) * LDA + (L & 7) * 16;
-    int sa_off[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i) sa_off[i] = min(16 * i + l16, M - 1) * SFA_SM * 4;
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) b_off[b][h] = min(n0 + 16 * b + 8 * h + (L >> 3), N - 1) * LDB + (L & 7) * 16;
+    int sa_off[MB], xb_off[NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) sa_off[i] = min(16 * i + l16, M - 1) * SFA_SM * (MX ? 1 : 4);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) xb_off[b] = min(n0 + 16 * b + l16, N - 1) * SFB_SN;
     const int sb_off = ((min(n0, N - 1) >> 7) * SFB_SN) * 4;
 #pragma unroll
     for (int j = 0; j < KPW; ++j) {
@@ -185,12 +211,17 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
         for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                int soff;
-                if constexpr (BL == BLay::KPANEL) soff = (kt * N + n0 + 16 * b) * BKB;        // [K/128][N][128]
-                else soff = (((n0 / 16 + b) * nk + kt) * 2) * 1024;                          // [N/16][K/128][2][1 KB]
                 // each B byte is read once: nontemporal
-                bv[j][b][h] = __builtin_bit_cast(
-                    i32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, h * 1024 + L * 16, soff, 2));
+                if constexpr (BL == BLay::RAW) {                                            // [N][K] rows
+                    bv[j][b][h] = __builtin_bit_cast(
+                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, b_off[b][h], kt * BKB, 2));
+                } else {
+                    int soff;
+                    if constexpr (BL == BLay::KPANEL) soff = (kt * N + n0 + 16 * b) * BKB;    // [K/128][N][128]
+                    else soff = (((n0 / 16 + b) * nk + kt) * 2) * 1024;                      // [N/16][K/128][2][1 KB]
+                    bv[j][b][h] = __builtin_bit_cast(
+                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, h * 1024 + L * 16, soff, 2));
+                }
             }
 #pragma unroll
         for (int i = 0; i < MB; ++i)
@@ -198,11 +229,25 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
             for (int h = 0; h < 2; ++h)
                 av[j][i][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i][h],
                                                                                               kt * BKB, 0));
+        if constexpr (MX) {
+            // lane (q, r): the KT_SC scale bytes of its row for this K-tile
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
-            sa[j][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSA, sa_off[i],
-                                                                                      kt * SFA_SK * 4, 0));
-        sb[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSB, sb_off, kt * 4, 0));
+            for (int i = 0; i < MB; ++i) {
+                if constexpr (FP4) xa[j][i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rSA, sa_off[i], kt * KT_SC, 0));
+                else xa[j][i] = __builtin_amdgcn_raw_buffer_load_b32(rSA, sa_off[i], kt * KT_SC, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if constexpr (FP4) xb[j][b] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rSB, xb_off[b], kt * KT_SC, 0));
+                else xb[j][b] = __builtin_amdgcn_raw_buffer_load_b32(rSB, xb_off[b], kt * KT_SC, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                sa[j][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSA, sa_off[i],
+                                                                                          kt * SFA_SK * 4, 0));
+            sb[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rSB, sb_off, kt * 4, 0));
+        }
     }
 
     // keep the whole burst ahead of the first use (the scheduler otherwise
@@ -255,17 +300,58 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
                 bf[b] = cat8(bv[j][b][0], bv[j][b][1]);
             }
         }
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-            const QG_LDS uint8_t* as = slot + i * 2048;
-            const i32x8 af = cat8(*(const QG_LDS i32x4*)(as + frag0), *(const QG_LDS i32x4*)(as + frag1));
-            const float s = sa[j][i] * sb[j];
+        if constexpr (MX) {
+            // the lane group's scale byte in byte 0: fp8 byte q of the
+            // row's 4; fp4 bytes q (chunk q) and q + 4 (chunk q + 4)
+            int sxb[NB][2];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    bf[b], af, f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, unit, 0, unit);
+                if constexpr (FP4) {
+                    sxb[b][0] = (int)(xb[j][b][0] >> (8 * q));
+                    sxb[b][1] = (int)(xb[j][b][1] >> (8 * q));
+                } else {
+                    sxb[b][0] = (int)(xb[j][b] >> (8 * q));
+                }
+            }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[i][b][r] = __builtin_fmaf(part[r], s, acc[i][b][r]);
+            for (int i = 0; i < MB; ++i) {
+                const QG_LDS uint8_t* as = slot + i * 2048;
+                const i32x4 a0 = *(const QG_LDS i32x4*)(as + frag0), a1 = *(const QG_LDS i32x4*)(as + frag1);
+                if constexpr (FP4) {
+                    const int s0 = (int)(xa[j][i][0] >> (8 * q)), s1 = (int)(xa[j][i][1] >> (8 * q));
+                    const i32x8 a0w = i32x8{a0[0], a0[1], a0[2], a0[3], 0, 0, 0, 0};
+                    const i32x8 a1w = i32x8{a1[0], a1[1], a1[2], a1[3], 0, 0, 0, 0};
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const i32x8 b0w = i32x8{bf[b][0], bf[b][1], bf[b][2], bf[b][3], 0, 0, 0, 0};
+                        const i32x8 b1w = i32x8{bf[b][4], bf[b][5], bf[b][6], bf[b][7], 0, 0, 0, 0};
+                        acc[i][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b0w, a0w, acc[i][b], kFmtFp4,
+                                                                                     kFmtFp4, 0, sxb[b][0], 0, s0);
+                        acc[i][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b1w, a1w, acc[i][b], kFmtFp4,
+                                                                                     kFmtFp4, 0, sxb[b][1], 0, s1);
+                    }
+                } else {
+                    const int s0 = (int)(xa[j][i] >> (8 * q));
+                    const i32x8 af = cat8(a0, a1);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        acc[i][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[b], af, acc[i][b], kFmtFp8,
+                                                                                     kFmtFp8, 0, sxb[b][0], 0, s0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const QG_LDS uint8_t* as = slot + i * 2048;
+                const i32x8 af = cat8(*(const QG_LDS i32x4*)(as + frag0), *(const QG_LDS i32x4*)(as + frag1));
+                const float s = sa[j][i] * sb[j];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const f32x4 part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        bf[b], af, f32x4{0.f, 0.f, 0.f, 0.f}, kFmtFp8, kFmtFp8, 0, unit, 0, unit);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][b][r] = __builtin_fmaf(part[r], s, acc[i][b][r]);
+                }
             }
         }
     }

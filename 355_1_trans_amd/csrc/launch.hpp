@@ -65,6 +65,9 @@ hipError_t launch_stream(const StreamArgs& a, bool fp4, int wr, int mb, int batc
 struct BurstArgs;
 hipError_t launch_burst(const BurstArgs& a, bool frag, int mb, int nb, int waves, int batch, bool bf16,
                         hipStream_t s);
+// kernels_burst_mx.hip: the same for MXFP8 / MXFP4 (fp4) with row-major B and E8M0 scales
+hipError_t launch_burst_mx(const BurstArgs& a, bool fp4, int mb, int nb, int waves, int batch, bool bf16,
+                           hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);

@@ -174,6 +174,7 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
 #define QGEMM_KID_SKINNY  3  /* skinny-M tiles (16-64 rows), split-K */
 #define QGEMM_KID_DECODE  4  /* decode kernel: waves split N, A shared through LDS */
 #define QGEMM_KID_BURST   5  /* burst kernel: every load issued up front */
+#define QGEMM_KID_STREAM  6  /* MX only: row-streaming kernel (M <= 8, N >= 256) */
 hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
                                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);
@@ -195,6 +196,12 @@ size_t gemm_a8w8_blockscale_ldsbypass_kid_workspace_bytes(const opus_gemm_ldsbyp
 hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
+/* The same with a kernel id (QGEMM_KID_*, as for the fp32 block-scale entries;
+ * DECODE and BURST take M <= 64, STREAM M <= 8 with N >= 256 and needs the
+ * workspace when its plan splits K). */
+hipError_t gemm_a8w8_mxfp8_kid(const opus_gemm_scale_kargs* args, int out_dtype, int kernel_id, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_mxfp8_kid_workspace_bytes(const opus_gemm_scale_kargs* args, int kernel_id);
 
 /* ------------------------------------------------------------------ */
 /* MXFP4 A4W4: packed e2m1 x e2m1, E8M0 per 32 K elements.             */
@@ -210,6 +217,10 @@ size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
 hipError_t gemm_a4w4_mxfp4(const opus_gemm_scale_kargs* args, int out_dtype, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a4w4_mxfp4_workspace_bytes(const opus_gemm_scale_kargs* args);
+/* The same with a kernel id (as gemm_a8w8_mxfp8_kid). */
+hipError_t gemm_a4w4_mxfp4_kid(const opus_gemm_scale_kargs* args, int out_dtype, int kernel_id, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a4w4_mxfp4_kid_workspace_bytes(const opus_gemm_scale_kargs* args, int kernel_id);
 
 /* MXFP4 with aiter's gemm_a4w4(..., bpreshuffle=True) operands: the
  * 96-byte block plus grid_blocks (MX4/candidate_m10/

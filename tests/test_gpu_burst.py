@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close, make_bs, out_to_f32, to_dev
+from helpers import assert_close, make_bs, make_mx4, make_mx8, out_to_f32, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -81,3 +81,78 @@ def test_burst_batched_c_abi(qgemm, gpu, m, n, k):
     for i, d in enumerate(data):
         assert_close(O.gemm_bs_fp32(*d), C[i].float().cpu().numpy(), f"batch {i}")
     assert int(ws[:2048].to(torch.int32).sum()) == 0, "split-K counters not re-armed"
+
+
+# ----------------------------------------------------------------- MX burst
+MX_KIDS = {"auto": 0, "tile256": 1, "mid128": 2, "skinny": 3, "decode": 4, "burst": 5, "stream": 6}
+
+
+def _mx_call(qgemm, gpu, fp4, qa, qb, ea, eb, kid, out_dtype=torch.bfloat16, batch_data=None):
+    m, n = qa.shape[0], qb.shape[0]
+    kb = qa.shape[1]
+    k = 2 * kb if fp4 else kb
+    A, B = to_dev(qa, None, gpu), to_dev(qb, None, gpu)
+    SA, SB = to_dev(ea, None, gpu), to_dev(eb, None, gpu)
+    C = torch.empty(m, n, dtype=out_dtype, device=gpu)
+    args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
+                       SA.data_ptr(), SB.data_ptr(), k // 32, k // 32, m * (k // 32), n * (k // 32))
+    L = qgemm.lib()
+    name = "gemm_a4w4_mxfp4_kid" if fp4 else "gemm_a8w8_mxfp8_kid"
+    need = getattr(L, name + "_workspace_bytes")(ctypes.byref(args), kid)
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=gpu)
+    st = getattr(L, name)(ctypes.byref(args), 1 if out_dtype == torch.bfloat16 else 0, kid,
+                          ws.data_ptr() if need else None, need,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    kern = qgemm.last_launch()
+    torch.cuda.synchronize()
+    if need:
+        assert int(ws[:2048].sum()) == 0, "split-K counters not re-armed"
+    return st, C, kern
+
+
+# (M, N, K): tile shapes 16/32/64 rows x 16/32 columns, M and N tails, K
+# split over workgroups and not, configs[4] M = 32 (N = 7168, K = 16384)
+MX_BURST_SHAPES = [(1, 1000, 2048), (9, 2112, 7168), (17, 520, 4096), (32, 7168, 16384), (33, 1536, 2048),
+                   (48, 300, 1024), (64, 4096, 7168), (24, 7168, 16384)]
+
+
+@pytest.mark.parametrize("m,n,k", MX_BURST_SHAPES)
+@pytest.mark.parametrize("fp4", [False, True])
+def test_mx_burst(qgemm, gpu, m, n, k, fp4):
+    if fp4:
+        qa, qb, ea, eb = make_mx4(m, n, k, seed=3 * m + n)
+        ref = O.gemm_mx4(qa, qb, ea, eb)
+    else:
+        qa, qb, ea, eb = make_mx8(m, n, k, seed=3 * m + n)
+        ref = O.gemm_mx8(qa, qb, ea, eb)
+    for dtype in (torch.bfloat16, torch.float32):
+        st, C, kern = _mx_call(qgemm, gpu, fp4, qa, qb, ea, eb, MX_KIDS["burst"], dtype)
+        if k // (256 if fp4 else 128) > 64:      # more K-tiles than the burst plan takes
+            assert st == 1
+            return
+        assert st == 0
+        assert kern.startswith(f"burst_gemm<{'fp4' if fp4 else 'fp8'},MX,RAW,"), kern
+        assert_close(ref, out_to_f32(C), f"mx burst {m}x{n}x{k} {dtype} ({kern})")
+
+
+@pytest.mark.parametrize("m,n,k", [(4, 2112, 7168), (24, 1536, 4096), (100, 1024, 2048)])
+@pytest.mark.parametrize("fp4", [False, True])
+@pytest.mark.parametrize("kid", list(MX_KIDS))
+def test_mx_kernel_ids(qgemm, gpu, m, n, k, fp4, kid):
+    """Every kernel id of the MX entries against the oracle, or a clean
+    rejection where the family cannot take the shape."""
+    if fp4:
+        qa, qb, ea, eb = make_mx4(m, n, k, seed=m + n)
+        ref = O.gemm_mx4(qa, qb, ea, eb)
+    else:
+        qa, qb, ea, eb = make_mx8(m, n, k, seed=m + n)
+        ref = O.gemm_mx8(qa, qb, ea, eb)
+    st, C, kern = _mx_call(qgemm, gpu, fp4, qa, qb, ea, eb, MX_KIDS[kid])
+    if (kid in ("decode", "burst") and m > 64) or (kid == "stream" and m > 8):
+        assert st == 1
+        return
+    assert st == 0
+    want = {"tile256": "wide_gemm", "mid128": "mid_gemm", "skinny": "skinny_gemm", "decode": "decode_gemm",
+            "burst": "burst_gemm", "stream": "stream_gemm"}.get(kid)
+    assert want is None or want in kern, kern
+    assert_close(ref, out_to_f32(C), f"mx kid {kid} {m}x{n}x{k} ({kern})")
