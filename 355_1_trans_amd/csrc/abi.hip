@@ -313,6 +313,21 @@ constexpr int kMidMinM = 64;
 constexpr int kMidBelow = 128;
 constexpr int kMidMinKt = 16;    // 8 measured slower where the split tail dominates (M = 256, N = 4096, K = 7168: 34.4 vs 27.0 us)
 
+// M <= 256 with at least kMidBelow 256 x 256 tiles (N > 32512 at batch 1):
+// the planners below replace the 256 x 256 plan of small M there, and the
+// burst kernel stays out for M > 16 (N = 32768 - 129280, M = 17-32: the
+// 128 x 128 kernel 1.05-1.4x faster)
+bool wide_region(int n, int batch) { return (long long)ceil_div(n, 256) * batch >= kMidBelow; }
+
+// A 256 x 256 plan the small-M rule replaces: M <= 128, or M <= 192 with
+// K <= 2048 and fewer 256 x 256 tiles than CUs (measured, N = 32768 -
+// 129280: the 128 x 128 kernel 1.1-1.7x faster for M <= 128; for M = 192
+// only while the 256 x 256 tiles leave CUs idle, 0.8-0.9x past that)
+bool small_m_wide(int m, int n, int batch, long long k, int cus) {
+    const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    return m <= 128 || (m <= 192 && k <= 2048 && tiles256 < cus);
+}
+
 // Replaces p with a 128 x 128 plan when M > kMidMinM and the 256 x 256
 // kernel would have fewer than kMidBelow tiles (always with force).
 void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus, bool force = false) {
@@ -345,6 +360,7 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus, bool force
 // cost-model plan when that plan is accepted; workspace = counters +
 // splitk * batch * M * N fp32 partials when K is split.
 qg::BurstPlan plan_bsf32_burst(int m, int n, int k_tiles, int batch) {
+    if (m > 16 && wide_region(n, batch)) return qg::BurstPlan{};
     return qg::burst_plan(m, n, k_tiles, batch, device_cus(), kMaxCounters);
 }
 
@@ -385,6 +401,16 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
         const long long wgs = (long long)s.n_tiles * s.m_tiles * batch;
         const long long wg_bytes = 16LL * (s.mb + s.nb) * k_tiles * 128;
         if (s.splitk == 1 && wgs <= cus && 4 * wgs >= 3LL * cus && wg_bytes <= 768 * 1024) p = s;
+    }
+    // M <= 64 and >= 128 256 x 256 tiles (N > 32512): the 256-row tiles
+    // would be mostly padding -- the 128 x 128 kernel (N = 32768 - 129280,
+    // M = 33-64: 1.3-1.6x; also M = 192 with K <= 2048 and fewer 256 x 256
+    // tiles than CUs: N = 32768, K = 1536 1.08x), or for M <= 32 with
+    // K > 2048 the skinny kernel unsplit (N = 32768 - 129280, K = 7168:
+    // within 5% of the fastest id, 1.35-1.7x over the 256 x 256 tiles)
+    if (!p.skinny && !p.mid && small_m_wide(m, n, batch, (long long)k_tiles * 128, cus)) {
+        if (m <= 32 && k_tiles > 16) p = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, true, decode_ok, decode_ok);
+        else plan_mid(p, m, n, k_tiles, batch, cus, true);
     }
     return p;
 }
@@ -455,12 +481,23 @@ BsfRoute route_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bo
     return r;
 }
 
-// MX: the same 128 x 128 rule (row-major B, E8M0 scales applied by the MFMA)
+// MX: the same 128 x 128 rule (row-major B, E8M0 scales applied by the
+// MFMA); small M on >= 128 256 x 256 tiles runs the 128 x 128 kernel
+// (N = 32768 - 129280, MXFP4 / MXFP8 M = 24-128: 1.1-1.7x over the
+// 256 x 256 tiles), M <= 16 the skinny kernel unsplit (MXFP8 K = 7168,
+// M = 16: 85.3 -> 49.4 us at N = 32768)
 Plan plan_mx(int m, int n, int k_tiles, int batch, long long b_bytes, bool fp4) {
     const int cus = device_cus();
-    Plan p = fp4 ? plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false, false, false, true)
-                 : plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false);
+    auto skinny = [&](bool force) {
+        return fp4 ? plan_gemm(m, n, k_tiles, batch, b_bytes, cus, force, false, false, true)
+                   : plan_gemm(m, n, k_tiles, batch, b_bytes, cus, force);
+    };
+    Plan p = skinny(false);
     plan_mid(p, m, n, k_tiles, batch, cus);
+    if (!p.skinny && !p.mid && small_m_wide(m, n, batch, (long long)k_tiles * (fp4 ? 256 : 128), cus)) {
+        if (m <= 16) p = skinny(true);
+        else plan_mid(p, m, n, k_tiles, batch, cus, true);
+    }
     return p;
 }
 
@@ -501,7 +538,13 @@ StreamPlan plan_stream(int m, int n, int k, int batch, bool fp4) {
     const long long nblk_target = std::max<long long>(1, device_cus() / ((long long)p.splitk * batch));
     long long rows = (n + nblk_target - 1) / nblk_target;
     const int wsp = 1 << qg::stream_ws_log2(p.seg_per_split * 64 / p.wr);
-    rows = std::min<long long>(rows, std::min(qg::stream_max_rows(p.wr), qg::kStreamWsBytes / wsp));
+    const long long rcap = std::min(qg::stream_max_rows(p.wr), qg::kStreamWsBytes / wsp);
+    if (rows > rcap) {
+        // more than one round: the rows spread evenly over whole rounds (at
+        // the cap, N = 16384 would be 293 blocks -- a second round of 37)
+        const long long rounds = ((n + rcap - 1) / rcap + nblk_target - 1) / nblk_target;
+        rows = (n + rounds * nblk_target - 1) / (rounds * nblk_target);
+    }
     p.rows = (int)std::max<long long>(rows, 1);
     if (p.splitk > 1) {
         const long long blocks = (long long)ceil_div(n, p.rows) * batch;
@@ -706,9 +749,14 @@ struct MxRoute {
 // 8.1 -> 5.6; fp8 M = 16, N = 24576, K = 1536 15.6 -> 10.7), long K loses
 // (fp4 configs[4] K = 16384, M = 16 / 32: 15.8 / 19.2 on the skinny kernel,
 // 17.7 / 29.2 as a burst); M <= 8 stays on the row-streaming kernel, whose
-// contiguous row runs 16-row fragments cannot match (M = 1: 12.8 vs 17.5)
+// contiguous row runs 16-row fragments cannot match (M = 1: 12.8 vs 17.5),
+// up to N = kStreamBurstN: past it the burst kernel's many short workgroups
+// win (N = 16384 - 129280, K = 1536 / 7168: 1.0-1.5x, one shape 4% slower)
+constexpr int kStreamBurstN = 16384;
+
 qg::BurstPlan plan_mx_burst(int m, int n, int k_tiles, int batch, bool gate) {
-    if (gate && (m <= kStreamMaxM || k_tiles > 32)) return qg::BurstPlan{};
+    if (gate && ((m <= kStreamMaxM && n < kStreamBurstN) || k_tiles > 32 || (m > 16 && wide_region(n, batch))))
+        return qg::BurstPlan{};
     return qg::burst_plan(m, n, k_tiles, batch, device_cus(), kMaxCounters, gate, 16, true);
 }
 
@@ -727,14 +775,14 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
                                    r.pl.skinny || r.pl.mid ? 0 : scale_panel_bytes(a)});
             r.ok = true;
-            if (stream_ok(a, fp4)) {
-                // without the K split's workspace: the skinny kernel, unsplit
-                r.kid = r.sp.splitk == 1 || have_ws ? QGEMM_KID_STREAM : QGEMM_KID_SKINNY;
-                if (r.kid == QGEMM_KID_SKINNY && !r.pl.skinny) r.pl = plan_gemm(a.m, a.n, kt, a.batch, bb, cus, true, false);
-                return r;
-            }
             if (r.bp.ok && (r.bp.splitk == 1 || have_ws)) {
                 r.kid = QGEMM_KID_BURST;
+                return r;
+            }
+            if (stream_ok(a, fp4)) {
+                // without the K split's workspace: the skinny kernel (plan_mx
+                // plans it for every M <= 16)
+                r.kid = r.sp.splitk == 1 || have_ws ? QGEMM_KID_STREAM : QGEMM_KID_SKINNY;
                 return r;
             }
             r.kid = r.pl.mid ? QGEMM_KID_MID

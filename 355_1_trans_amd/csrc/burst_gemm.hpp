@@ -107,6 +107,13 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
             if (!waves) continue;
             if (split > 1 && (tiles > max_counters || (long long)m * n >= (1LL << 29))) continue;
             const long long wgs = tiles * split;
+            // past one round of workgroups (N > 8192): 16-wave plans lose
+            // 2.2-2.4x (fp32 scales, M = 17-32, K = 7168, N = 16384 - 129280:
+            // N = 32768, M = 32 100.4 us vs 41.2 on the decode kernel), and
+            // with fp32 scales so does K past 16 K-tiles (M <= 16, K = 7168:
+            // 1.1-1.25x slower than skinny / decode); 8-wave plans over short
+            // K keep it (K = 1536, N = 12288 - 129280: best or within 8%)
+            if (gate && wgs > cus && (waves == 16 || (!mx && k_tiles > 16))) continue;
             const double kb = (16.0 * nb + m) * kt_per * 128 / 1024.0;
             const double cost = 2.5 + 0.025 * kb * (double)((wgs + cus - 1) / cus) + (split > 1 ? 3.4 : 0.0);
             if (cost < best.cost_us) {

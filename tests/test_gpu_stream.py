@@ -218,3 +218,34 @@ def test_stream_routing_boundaries(qgemm, gpu, m, n):
     y = qgemm.gemm_a8w8_mxfp8(_fp8(qa, gpu), _fp8(qb, gpu), to_dev(ea, None, gpu), to_dev(eb, None, gpu),
                               dtype=torch.float32)
     assert_close(O.gemm_mx8(qa, qb, ea, eb), out_to_f32(y), f"mxfp8 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,workspace,expect", [
+    (4, 7168, None, "stream_gemm<fp4,wr4,mb4,fp32,splitk2>"),
+    (4, 7168, False, "skinny_gemm<fp4"),
+    (4, 32768, None, "skinny_gemm<fp4"),
+    (16, 32768, None, "skinny_gemm<fp4"),
+])
+def test_long_k_routes(qgemm, gpu, m, n, workspace, expect):
+    """K = 16640: 65 fp4 K-tiles (past the burst kernel's 32) and 8320 bytes
+    per row (past the 8 KB of a row the row-streaming kernel's LDS holds).
+    M = 4, N = 7168: the row-streaming kernel splits K in two with a
+    workspace, and without one the skinny kernel runs unsplit.  N = 32768
+    (128 tiles of 256 x 256): the streaming split would need more counters
+    than it has, and M <= 16 runs the skinny kernel, not 256-row tiles.
+    Random fp4 codes and E8M0 bytes keep the host arrays small; 4096
+    sampled outputs against the oracle."""
+    k = 16640
+    rng = np.random.default_rng(5 + m + n)
+    qa = rng.integers(0, 256, (m, k // 2), dtype=np.uint8)
+    qb = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    ea = rng.integers(120, 135, (m, k // 32), dtype=np.uint8)
+    eb = rng.integers(120, 135, (n, k // 32), dtype=np.uint8)
+    dev = lambda x: torch.from_numpy(x).to(gpu)
+    y = qgemm.gemm_a4w4_mxfp4(dev(qa), dev(qb), dev(ea), dev(eb), dtype=torch.float32, workspace=workspace)
+    assert qgemm.last_launch().startswith(expect), qgemm.last_launch()
+    torch.cuda.synchronize()
+    rows = rng.integers(0, m, 4096).astype(np.int32)
+    cols = rng.integers(0, n, 4096).astype(np.int32)
+    ref = O.gemm_mx4_points(qa, qb, ea, eb, rows, cols)
+    assert_close(ref, y.cpu().numpy()[rows, cols], f"M={m} N={n} K={k} workspace={workspace}")
