@@ -16,6 +16,7 @@
 
 #include "launch.hpp"
 #include "qgemm.h"
+#include "bsf32_gemm.hpp"
 #include "burst_gemm.hpp"
 #include "decode_gemm.hpp"
 #include "mid_gemm.hpp"
@@ -415,6 +416,59 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
     return p;
 }
 
+// Tail split of the 256 x 256 fp32-scale kernel (bsf32_gemm.hpp): one
+// workgroup per CU, so batch x tiles beyond whole rounds of `cus` leave a
+// partial last round; its tiles may be cut into S K-slices (one workgroup
+// each, fp32 partial images summed by the last slice).  Cost model in
+// microseconds, fitted to the dsv4 sweep run both ways (bsf32 kernel, 27
+// shapes with a tail): a K-tile takes kTailKtFreeUs on a CU while few CUs
+// run and kTailKtFullUs when the chip is at its power limit, so the tail
+// costs max(its longest workgroup, its total work at the full-load rate);
+// a split adds its partial images, written and read back at
+// kTailPartialBytesPerUs (256 KB each way per slice), and kTailFixUs.  The
+// split is taken when it saves at least 5%: K >= 16384 with a tail of
+// 80-108 tiles gains 5-12% (M = 3072, N = 7168, K = 16384: 347 -> 311 us);
+// larger tails lose to the chip's power limit (M = 2048, N = 7168,
+// K = 16384 split 8 ways: 195 -> 611 us) and short K to the partial traffic.
+// Workspace = counters + the tail's partial images.
+struct TailPlan {
+    int dp = 0, split = 1, kps = 0;
+    size_t ws_bytes = 0;
+};
+constexpr double kTailKtFreeUs = 1.27, kTailKtFullUs = 1.5, kTailFixUs = 3.4, kTailPartialBytesPerUs = 2.0e6;
+constexpr int kTailMaxSplit = 8, kTailMinKt = 4;
+
+TailPlan plan_tail(int m, int n, int k_tiles, int batch, int cus) {
+    TailPlan tp;
+    const long long items = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    tp.dp = (int)std::min<long long>(items, 1LL << 30);
+    tp.kps = k_tiles;
+    const long long tail = items % cus;
+    if (tail == 0 || items >= (1LL << 30) || tail > kMaxCounters) return tp;
+    const double power = (double)tail * k_tiles / cus * kTailKtFullUs;
+    const double unsplit = std::max((double)k_tiles * kTailKtFreeUs, power);
+    double best = unsplit;
+    int bs = 1;
+    for (int sp = 2; sp <= kTailMaxSplit; ++sp) {
+        const int kps = ceil_div(k_tiles, sp);
+        if (kps < kTailMinKt) break;
+        if (ceil_div(k_tiles, kps) != sp) continue;
+        const double path = (double)((tail * sp + cus - 1) / cus) * kps * kTailKtFreeUs;
+        const double c = std::max(path, power) + (double)tail * sp * 2 * 256 * 256 * 4 / kTailPartialBytesPerUs +
+                         kTailFixUs;
+        if (c < 0.95 * unsplit && c < best) {
+            best = c;
+            bs = sp;
+        }
+    }
+    if (bs == 1) return tp;
+    tp.dp = (int)(items - tail);
+    tp.split = bs;
+    tp.kps = ceil_div(k_tiles, bs);
+    tp.ws_bytes = kCounterBytes + (size_t)tail * bs * 256 * 256 * sizeof(float);
+    return tp;
+}
+
 // Kernel routes of the fp32 block-scale entries (QGEMM_KID_* in qgemm.h):
 // AUTO resolves to one of the others by the plans above; a forced route
 // runs that kernel with its own plan (tile shape and K split), or fails
@@ -426,6 +480,7 @@ struct BsfRoute {
     bool ok = false;
     qg::BurstPlan bp;
     Plan pl;
+    TailPlan tp;
     size_t ws_bytes = 0;
 };
 
@@ -446,13 +501,16 @@ BsfRoute route_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bo
                 }
             }
             r.pl = plan_bsf32(m, n, k_tiles, batch, b_bytes, !frag);
-            if (!r.bp.ok) r.ws_bytes = r.pl.ws_bytes;
             r.kid = r.pl.mid ? QGEMM_KID_MID
                              : r.pl.skinny ? (r.pl.decode ? QGEMM_KID_DECODE : QGEMM_KID_SKINNY) : QGEMM_KID_TILE256;
+            if (r.kid == QGEMM_KID_TILE256) r.tp = plan_tail(m, n, k_tiles, batch, cus);
+            if (!r.bp.ok) r.ws_bytes = r.kid == QGEMM_KID_TILE256 ? r.tp.ws_bytes : r.pl.ws_bytes;
             r.ok = true;
             return r;
         }
         case QGEMM_KID_TILE256:
+            r.tp = plan_tail(m, n, k_tiles, batch, cus);
+            r.ws_bytes = r.tp.ws_bytes;
             r.ok = true;
             return r;
         case QGEMM_KID_MID:
@@ -722,10 +780,24 @@ hipError_t run_bsf32(const BsfRoute& r, const TileArgs& t, int batch, bool frag,
         case QGEMM_KID_DECODE:
             return run_skinny(frag ? SkinnyKind::BSF32_FRAG : SkinnyKind::BSF32_KPANEL, t, batch, r.pl, bf16, ws,
                               ws_bytes, k_tiles, stream);
-        default:
+        default: {
             // the eight-wave kernel with VGPR accumulators and a VALU rescale
-            // per K-tile (bsf32_gemm.hpp)
-            return qg::launch_bsf32(t, batch, bf16, frag, stream);
+            // per K-tile (bsf32_gemm.hpp); the tail split only with the
+            // workspace at hand
+            qg::Bsf32Args a{};
+            a.t = t;
+            a.dp_tiles = t.tiles_m * t.tiles_n * batch;
+            a.tail_split = 1;
+            a.kt_per_split = k_tiles;
+            if (r.tp.split > 1 && ws && ws_bytes >= r.tp.ws_bytes) {
+                a.dp_tiles = r.tp.dp;
+                a.tail_split = r.tp.split;
+                a.kt_per_split = r.tp.kps;
+                a.counters = static_cast<unsigned*>(ws);
+                a.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+            }
+            return qg::launch_bsf32(a, batch, bf16, frag, stream);
+        }
     }
 }
 

@@ -43,10 +43,31 @@
 //
 // LDS rows are 128 bytes with 16-byte chunks XOR-swizzled by row & 7 (DMA
 // writes and fragment reads are conflict free).
+//
+// Tail split (the data-parallel + split-K form of stream-K).  One workgroup
+// fills a CU, so batch x tiles = R rounds of `cus` tiles plus a tail of
+// fewer; unsplit, the last round leaves CUs idle (M = 3072, N = 7168: 336
+// tiles = one round and 80 tiles).  The host may run the first dp_tiles
+// (whole rounds) as they are and cut each tail tile's K into tail_split
+// slices of kt_per_split K-tiles, one workgroup each, so the last round is
+// full.  A slice stores its fp32 partial tile (a flat 256 x 256 image,
+// device-coherent) into the workspace, then one relaxed counter atomic per
+// workgroup; the last slice of a tile to arrive sums the slices' images in
+// slice order (deterministic whichever arrives last) with all 512 threads
+// reading whole lines, rounds and stores C, and re-arms the counter.
 #pragma once
 #include "tile_args.hpp"
 
 namespace qg {
+
+struct Bsf32Args {
+    TileArgs t;
+    float* ws;            // tail_split > 1: fp32 partial images [tail][tail_split][256 * 256]
+    unsigned* counters;   // tail_split > 1: one per tail tile, zero between launches
+    int dp_tiles;         // batch x tiles run whole (the rest is the tail)
+    int tail_split;       // K slices per tail tile (1: no tail split)
+    int kt_per_split;     // K-tiles per slice
+};
 
 namespace bsf {
 template <int V>
@@ -64,7 +85,8 @@ __device__ __forceinline__ f32x4 mfma_part(const i32x8& b, const i32x8& a) {
 }  // namespace bsf
 
 template <bool BF16, BLay BL>
-__global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
+__global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const Bsf32Args ba) {
+    const TileArgs& p = ba.t;
     static_assert(BL == BLay::KPANEL || BL == BLay::FRAG, "K-panel B' or fragment-order B''");
     constexpr bool FRAG = (BL == BLay::FRAG);
     constexpr int BKB = 128, BM = 256;
@@ -81,9 +103,19 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lB2[BHALF];
     __shared__ __attribute__((aligned(1024))) uint8_t lB3[BHALF];
 
-    // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
+    __shared__ int last_flag;
+
+    // ---- work item: tile v of the batch x tiles list (workgroups past
+    // dp_tiles: slice sk of tail tile dp_tiles + (b - dp_tiles) / S) ----
     const int T = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
+    const int S = ba.tail_split;
+    const int b = blockIdx.x;
+    const bool slice = b >= ba.dp_tiles && S > 1;
+    const int v = slice ? ba.dp_tiles + (b - ba.dp_tiles) / S : b;
+    const int sk = slice ? (b - ba.dp_tiles) % S : 0;
+    const int bz = v / T;
+    // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
+    int bid = v - bz * T;
     if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
     const int gfull = p.group_m * p.tiles_n;
     const int gi = bid / gfull;
@@ -92,7 +124,6 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     const int within = bid - gi * gfull;
     const int tm = first_m + within % gm;
     const int tn = within / gm;
-    const int bz = blockIdx.z;
     const int m0 = tm * BM, n0 = tn * BM;
 
     // kernel arguments copied into locals once (the loop must not reload the
@@ -105,11 +136,16 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     const int wm = w >> 1, wn = w & 1;
     const int q = L >> 4, l16 = L & 15;
 
-    const int nk = KB / BKB;
-    const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
+    // NKT K-tiles per row; this work item runs K-tiles [kt0, kt0 + nk)
+    const int NKT = KB / BKB;
+    const int kt0 = sk * ba.kt_per_split;
+    const int nk = slice ? min(NKT, kt0 + ba.kt_per_split) - kt0 : NKT;
+    const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA + (long long)kt0 * BKB;
     // B' (K-panel): K-tile kt is [N][128 B] at kt * N * 128.  B'' (FRAG):
-    // block nb of 16 rows, K-tile kt at (nb * nk + kt) * 2048
-    const uint8_t* B = p.b + bz * p.b_batch + (FRAG ? (long long)(n0 >> 4) * nk * 2048 : (long long)n0 * BKB);
+    // block nb of 16 rows, K-tile kt at (nb * NKT + kt) * 2048
+    const uint8_t* B = p.b + bz * p.b_batch +
+                       (FRAG ? (long long)(n0 >> 4) * NKT * 2048 + (long long)kt0 * 2048
+                             : (long long)n0 * BKB + (long long)kt0 * N * BKB);
     const uint8_t* SFA = p.sfa + 4ll * bz * p.sfa_batch;
     const uint8_t* SFB = p.sfb + 4ll * bz * p.sfb_batch;
 
@@ -142,7 +178,7 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
             if constexpr (FRAG) {
                 const int tb = (w >> 2) * 8 + jh * 4 + (w & 3);    // 16-column block of the tile
                 const int nb = min((n0 >> 4) + tb, ((N + 15) >> 4) - 1) - (n0 >> 4);
-                boff[jh][u] = nb * nk * 2048 + u * 1024 + L * 16;
+                boff[jh][u] = nb * NKT * 2048 + u * 1024 + L * 16;
             } else {
                 const int s = (2 * w + u) * 8 + (L >> 3);
                 const int n = (s >> 6) * 128 + jh * 64 + (s & 63);
@@ -154,8 +190,8 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     // (lane L: row 64w + L); wave 4 + j the weight scale of the tile's
     // 128-column block j & 1 (every lane the same dword)
     const bool sc_is_a = w < 4;
-    const uint8_t* sc_base = sc_is_a ? SFA + 4ll * m0 * SFA_SM
-                                     : SFB + 4ll * min((n0 >> 7) + (w & 1), (N - 1) >> 7) * SFB_SN;
+    const uint8_t* sc_base = sc_is_a ? SFA + 4ll * m0 * SFA_SM + 4ll * kt0 * SFA_SK
+                                     : SFB + 4ll * min((n0 >> 7) + (w & 1), (N - 1) >> 7) * SFB_SN + 4ll * kt0;
     const int sc_voff = sc_is_a ? 4 * (min(m0 + 64 * w + L, M - 1) - m0) * SFA_SM : 0;
     const long long sc_kstride = sc_is_a ? 4ll * SFA_SK : 4ll;
     const int sc_dst = sc_is_a ? SA_OFF + 256 * w : SB_OFF + 256 * (w - 4);
@@ -346,6 +382,79 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const TileArgs p) {
     drain();
     wait_vmcnt<0>();
     (void)SFB_SN;
+
+    if (slice) {
+        // ---- tail slice: the partial image, the counter, and for the last
+        // slice to arrive the sum of the slices in slice order ----
+        const int r = v - ba.dp_tiles;
+        float* const img0 = ba.ws + (long long)r * S * (BM * BM);
+        {
+            const auto out = partial_rsrc(img0 + (long long)sk * (BM * BM));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+                    store_partial4(out, (wm * 64 + 16 * i + l16) * BM + wn * 128 + 16 * jj + 4 * q, acc[i][jj]);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (tid == 0)
+            last_flag = __hip_atomic_fetch_add(ba.counters + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        (unsigned)(S - 1);
+        __syncthreads();
+        if (!last_flag) return;
+        // thread tid sums 4 consecutive columns of rows tid / 64 + 8u
+        // (u = 0..31): 8 rows per group of loads, every slice's loads of a
+        // group issued before the first add
+        const auto src = partial_rsrc(img0);
+        const int col = 4 * (tid & 63), row0 = tid >> 6;
+        const bool vec_ok = p.c_vec >= 4;
+        for (int ug = 0; ug < 32; ug += 8) {
+            f32x4 sum[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sum[u] = load_partial4(src, (row0 + 8 * (ug + u)) * BM + col);
+            for (int s2 = 1; s2 < S; s2 += 2) {
+                f32x4 x0[8], x1[8];
+                const bool two = s2 + 1 < S;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int e = (row0 + 8 * (ug + u)) * BM + col;
+                    x0[u] = load_partial4(src, s2 * (BM * BM) + e);
+                    if (two) x1[u] = load_partial4(src, (s2 + 1) * (BM * BM) + e);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    sum[u] += x0[u];
+                    if (two) sum[u] += x1[u];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int mm = m0 + row0 + 8 * (ug + u), nn = n0 + col;
+                if (mm >= M) continue;
+                const f32x4 sv = sum[u];
+                if constexpr (BF16) {
+                    uint16_t* crow = (uint16_t*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                    if (vec_ok && nn + 3 < N) {
+                        *(u32x2*)(crow + nn) = u32x2{pack_bf16x2(sv[0], sv[1]), pack_bf16x2(sv[2], sv[3])};
+                    } else {
+                        for (int e = 0; e < 4; ++e)
+                            if (nn + e < N) crow[nn + e] = bf16_bits(sv[e]);
+                    }
+                } else {
+                    float* crow = (float*)p.c + bz * p.c_batch + (long long)mm * LDC;
+                    if (vec_ok && nn + 3 < N) {
+                        *(f32x4*)(crow + nn) = sv;
+                    } else {
+                        for (int e = 0; e < 4; ++e)
+                            if (nn + e < N) crow[nn + e] = sv[e];
+                    }
+                }
+            }
+        }
+        if (tid == 0) __hip_atomic_store(ba.counters + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
 
     // ---- epilogue: lane holds C[16i + l16][16jj + 4q + 0..3] of the wave's
     // 64 x 128 block ----

@@ -4,8 +4,10 @@
 
 namespace qg {
 
-hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipStream_t s) {
-    const dim3 grid(a.tiles_m * a.tiles_n, 1, batch);
+hipError_t launch_bsf32(const Bsf32Args& a, int batch, bool bf16, bool frag, hipStream_t s) {
+    const long long items = (long long)a.t.tiles_m * a.t.tiles_n * batch;
+    const long long tail = items - a.dp_tiles;
+    const dim3 grid((unsigned)(a.tail_split > 1 ? a.dp_tiles + tail * a.tail_split : items), 1, 1);
     if (frag) {
         if (bf16) bsf32_gemm_kernel<true, BLay::FRAG><<<grid, 512, 0, s>>>(a);
         else bsf32_gemm_kernel<false, BLay::FRAG><<<grid, 512, 0, s>>>(a);
@@ -13,7 +15,11 @@ hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipS
         if (bf16) bsf32_gemm_kernel<true, BLay::KPANEL><<<grid, 512, 0, s>>>(a);
         else bsf32_gemm_kernel<false, BLay::KPANEL><<<grid, 512, 0, s>>>(a);
     }
-    trace_launch("bsf32_gemm<fp8,BSF32,%s,%s>", frag ? "FRAG" : "KPANEL", bf16 ? "bf16" : "fp32");
+    if (a.tail_split > 1)
+        trace_launch("bsf32_gemm<fp8,BSF32,%s,%s,tail%lldx%d>", frag ? "FRAG" : "KPANEL", bf16 ? "bf16" : "fp32", tail,
+                     a.tail_split);
+    else
+        trace_launch("bsf32_gemm<fp8,BSF32,%s,%s>", frag ? "FRAG" : "KPANEL", bf16 ? "bf16" : "fp32");
     return hipGetLastError();
 }
 

@@ -15,7 +15,8 @@ void trace_launch(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
 // kernels_bsf32.hip: eight-wave 256 x 256 tiles, fp32 block scales; B' (K-panel) or,
 // with frag, B'' (the LDS-bypass entry's fragment order)
-hipError_t launch_bsf32(const TileArgs& a, int batch, bool bf16, bool frag, hipStream_t s);
+struct Bsf32Args;
+hipError_t launch_bsf32(const Bsf32Args& a, int batch, bool bf16, bool frag, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
 // panel_bytes: MX8 scale panel width, 16 or 4 bytes per row
 hipError_t launch_wide_mx8_raw(const TileArgs& a, int batch, bool bf16, int panel_bytes, hipStream_t s);
