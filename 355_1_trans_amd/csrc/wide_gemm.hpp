@@ -144,8 +144,12 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     const int total = PERSIST ? T * p.batch : 1;
     for (int it = PERSIST ? (int)blockIdx.x : 0; it < total; it += PERSIST ? (int)gridDim.x : 1) {
         // the previous tile's epilogue read its C image from the operand
-        // stages and left stores in flight: drain both before the DMAs
-        if (PERSIST && it != (int)blockIdx.x) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // stages: every wave's LDS reads finish before the DMAs overwrite
+        // them.  Its global stores may still be in flight: the prologue's
+        // vmcnt wait counts them as well (vector loads complete in issue
+        // order, so that wait still means K-tile 0 has landed), and the
+        // stores drain under the first DMAs' latency
+        if (PERSIST && it != (int)blockIdx.x) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const int bz = PERSIST ? it / T : (int)blockIdx.z;
         int bid = PERSIST ? it - bz * T : (int)blockIdx.x;
         if ((T & 7) == 0) bid = (bid & 7) * (T >> 3) + (bid >> 3);
