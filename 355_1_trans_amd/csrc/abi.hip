@@ -16,6 +16,7 @@
 
 #include "launch.hpp"
 #include "qgemm.h"
+#include "band_gemm.hpp"
 #include "bsf32_gemm.hpp"
 #include "burst_gemm.hpp"
 #include "decode_gemm.hpp"
@@ -619,6 +620,70 @@ bool stream_ok(const opus_gemm_scale_kargs& a, bool fp4) {
     return a.batch == 1 || a.stride_sfa_batch % 4 == 0;
 }
 
+// Band kernel (band_gemm.hpp): M <= 64 with row-major MX B.  A workgroup
+// owns 128 * cb columns and a K slice of at most band_kt_max(mb) K-tiles
+// (its A in LDS); the plan takes the (cb, split) whose workgroups fill the
+// most CUs in one round, the smaller split on a tie, and no plan when even
+// the smallest split needs more than one round.
+struct BandPlan {
+    bool ok = false;
+    int mb = 1, cb = 1, splitk = 1, kps = 1, bands = 1;
+    size_t ws_bytes = 0;
+};
+
+BandPlan plan_band(int m, int n, int k_tiles, int batch) {
+    BandPlan best;
+    if (m < 1 || m > 64 || n < 1 || k_tiles < 1 || batch < 1) return best;
+    const int cus = device_cus();
+    const int mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    const int ktm = qg::band_kt_max(mb);
+    long long best_wgs = 0;
+    for (int cb : {1, 2}) {
+        if (mb == 2 && cb == 2) continue;    // no LDS room for a ring
+        const int bands = ceil_div(n, qg::band_cols(cb));
+        for (int sk = ceil_div(k_tiles, ktm); sk <= k_tiles; ++sk) {
+            const int kps = ceil_div(k_tiles, sk);
+            const int sp = ceil_div(k_tiles, kps);
+            if (sp != sk) continue;
+            const long long wgs = (long long)bands * sp * batch;
+            if (wgs > cus) break;
+            if (sp > 1 && ((long long)bands * batch > kMaxCounters || (long long)m * n >= (1LL << 29))) break;
+            if (wgs > best_wgs) {
+                best_wgs = wgs;
+                best.ok = true;
+                best.mb = mb;
+                best.cb = cb;
+                best.splitk = sp;
+                best.kps = kps;
+                best.bands = bands;
+                best.ws_bytes = sp > 1 ? kCounterBytes + (size_t)sp * batch * m * n * 4 : 0;
+            }
+        }
+    }
+    return best;
+}
+
+// operands the band kernel's DMAs take: 16-byte rows of A and B, dword
+// scale rows of both operands
+bool band_ok(const opus_gemm_scale_kargs& a) {
+    if (!dma_aligned(a, true) || a.stride_b % 16 || a.stride_sfa % 4 || a.stride_sfb % 4) return false;
+    return a.batch == 1 || (a.stride_sfa_batch % 4 == 0 && a.stride_sfb_batch % 4 == 0);
+}
+
+hipError_t run_band(const BandPlan& bp, const TileArgs& t, int batch, bool fp4, bool bf16, void* ws,
+                    hipStream_t stream) {
+    qg::BandArgs b{};
+    b.t = t;
+    b.splitk = bp.splitk;
+    b.kt_per_split = bp.kps;
+    b.bands = bp.bands;
+    if (bp.splitk > 1) {    // the caller brought the workspace (checked before routing)
+        b.counters = static_cast<unsigned*>(ws);
+        b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+    }
+    return qg::launch_band(b, fp4, bp.mb, bp.cb, batch, bf16, stream);
+}
+
 // Launches the stream kernel; false when its K split needs a workspace the
 // call did not bring (the caller then runs the skinny kernel).
 bool run_stream(const TileArgs& t, int k, int batch, bool fp4, bool bf16, void* ws, size_t ws_bytes,
@@ -811,6 +876,7 @@ struct MxRoute {
     Plan pl;
     StreamPlan sp;
     qg::BurstPlan bp;
+    BandPlan bd;
     size_t ws_bytes = 0;
 };
 
@@ -847,6 +913,20 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
                                    r.pl.skinny || r.pl.mid ? 0 : scale_panel_bytes(a)});
             r.ok = true;
+            if (a.m > 16 && band_ok(a)) {
+                // the band kernel when one unsplit round of bands covers
+                // three quarters of the CUs: it reads each B row once with
+                // A's slice in LDS and no partials (MXFP4 / MXFP8, N =
+                // 24576-32768, K <= 4096, M = 24-64: 1.05-2.1x over the
+                // burst / decode / 128 x 128 plans); its split plans lose
+                // to them (up to 1.75x slower at N = 8192)
+                const BandPlan bd = plan_band(a.m, a.n, kt, a.batch);
+                if (bd.ok && bd.splitk == 1 && 4LL * bd.bands * a.batch >= 3LL * cus) {
+                    r.bd = bd;
+                    r.kid = QGEMM_KID_BAND;
+                    return r;
+                }
+            }
             if (r.bp.ok && (r.bp.splitk == 1 || have_ws)) {
                 r.kid = QGEMM_KID_BURST;
                 return r;
@@ -892,6 +972,13 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = r.sp.ws_bytes;
             if (r.sp.splitk > 1 && !have_ws) return r;    // the row-streaming kernel needs its split
             break;
+        case QGEMM_KID_BAND:
+            if (!band_ok(a)) return r;
+            r.bd = plan_band(a.m, a.n, kt, a.batch);
+            if (!r.bd.ok) return r;
+            r.ws_bytes = r.bd.ws_bytes;
+            if (r.bd.splitk > 1 && !have_ws) return r;    // its K slices need the workspace
+            break;
         default:
             return r;
     }
@@ -925,6 +1012,8 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
         case QGEMM_KID_SKINNY:
         case QGEMM_KID_DECODE:
             return run_skinny(sk, t, a.batch, r.pl, bf16, ws, ws_bytes, kt, stream);
+        case QGEMM_KID_BAND:
+            return run_band(r.bd, t, a.batch, fp4, bf16, ws, stream);
         case QGEMM_KID_MID:
             t.sfa_sk = t.sfb_sk = fp4 ? 8 : 4;
             return run_mid(t, a.batch, r.pl, bf16, fp4 ? qg::MidKind::MX4 : qg::MidKind::MX8, ws, ws_bytes, kt,

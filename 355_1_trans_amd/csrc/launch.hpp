@@ -16,6 +16,11 @@ void trace_launch(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 // kernels_bsf32.hip: eight-wave 256 x 256 tiles, fp32 block scales; B' (K-panel) or,
 // with frag, B'' (the LDS-bypass entry's fragment order)
 struct Bsf32Args;
+// kernels_band.hip: band kernel (MX, row-major B, M <= 64): a workgroup owns
+// 128 * cb columns and a K slice with A's slice in LDS; (mb, cb) in {(1,1),
+// (1,2), (2,1), (4,1), (4,2)}
+struct BandArgs;
+hipError_t launch_band(const BandArgs& a, bool fp4, int mb, int cb, int batch, bool bf16, hipStream_t s);
 hipError_t launch_bsf32(const Bsf32Args& a, int batch, bool bf16, bool frag, hipStream_t s);
 // kernels_wide.hip: four-wave 256 x 256 tiles, accumulators in AGPRs
 // panel_bytes: MX8 scale panel width, 16 or 4 bytes per row

@@ -175,6 +175,7 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
 #define QGEMM_KID_DECODE  4  /* decode kernel: waves split N, A shared through LDS */
 #define QGEMM_KID_BURST   5  /* burst kernel: every load issued up front */
 #define QGEMM_KID_STREAM  6  /* MX only: row-streaming kernel (M <= 8, N >= 256) */
+#define QGEMM_KID_BAND    7  /* MX only: band kernel (M <= 64): 128-256 columns x a K slice, A in LDS */
 hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
                                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);
@@ -198,7 +199,8 @@ hipError_t gemm_a8w8_mxfp8(const opus_gemm_scale_kargs* args, int out_dtype, voi
 size_t gemm_a8w8_mxfp8_workspace_bytes(const opus_gemm_scale_kargs* args);
 /* The same with a kernel id (QGEMM_KID_*, as for the fp32 block-scale entries;
  * DECODE and BURST take M <= 64, STREAM M <= 8 with N >= 256 and needs the
- * workspace when its plan splits K). */
+ * workspace when its plan splits K; BAND M <= 64 with dword-aligned scale
+ * rows, and the workspace when its plan splits K). */
 hipError_t gemm_a8w8_mxfp8_kid(const opus_gemm_scale_kargs* args, int out_dtype, int kernel_id, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_mxfp8_kid_workspace_bytes(const opus_gemm_scale_kargs* args, int kernel_id);

@@ -84,7 +84,7 @@ def test_burst_batched_c_abi(qgemm, gpu, m, n, k):
 
 
 # ----------------------------------------------------------------- MX burst
-MX_KIDS = {"auto": 0, "tile256": 1, "mid128": 2, "skinny": 3, "decode": 4, "burst": 5, "stream": 6}
+MX_KIDS = {"auto": 0, "tile256": 1, "mid128": 2, "skinny": 3, "decode": 4, "burst": 5, "stream": 6, "band": 7}
 
 
 def _mx_call(qgemm, gpu, fp4, qa, qb, ea, eb, kid, out_dtype=torch.bfloat16, batch_data=None):
@@ -148,11 +148,11 @@ def test_mx_kernel_ids(qgemm, gpu, m, n, k, fp4, kid):
         qa, qb, ea, eb = make_mx8(m, n, k, seed=m + n)
         ref = O.gemm_mx8(qa, qb, ea, eb)
     st, C, kern = _mx_call(qgemm, gpu, fp4, qa, qb, ea, eb, MX_KIDS[kid])
-    if (kid in ("decode", "burst") and m > 64) or (kid == "stream" and m > 8):
+    if (kid in ("decode", "burst", "band") and m > 64) or (kid == "stream" and m > 8):
         assert st == 1
         return
     assert st == 0
     want = {"tile256": "wide_gemm", "mid128": "mid_gemm", "skinny": "skinny_gemm", "decode": "decode_gemm",
-            "burst": "burst_gemm", "stream": "stream_gemm"}.get(kid)
+            "burst": "burst_gemm", "stream": "stream_gemm", "band": "band_gemm"}.get(kid)
     assert want is None or want in kern, kern
     assert_close(ref, out_to_f32(C), f"mx kid {kid} {m}x{n}x{k} ({kern})")
