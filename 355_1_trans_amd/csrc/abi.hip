@@ -404,6 +404,10 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
         const long long wg_bytes = 16LL * (s.mb + s.nb) * k_tiles * 128;
         if (s.splitk == 1 && wgs <= cus && 4 * wgs >= 3LL * cus && wg_bytes <= 768 * 1024) p = s;
     }
+    // long K (>= 128 K-tiles) where the 128 x 128 plan would run unsplit:
+    // the 256 x 256 kernel, whose tail split (plan_tail) fills the CUs
+    // (dsv4, N = 7168, K = 16384 / 21504, M = 768 / 1024: 1.13-1.25x)
+    if (p.mid && p.splitk == 1 && k_tiles >= 128 && m > 512) p = Plan{};
     // M <= 64 and >= 128 256 x 256 tiles (N > 32512): the 256-row tiles
     // would be mostly padding -- the 128 x 128 kernel (N = 32768 - 129280,
     // M = 33-64: 1.3-1.6x; also M = 192 with K <= 2048 and fewer 256 x 256
