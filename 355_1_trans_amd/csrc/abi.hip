@@ -259,7 +259,8 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
 // M >= 16 with up to 2 * kSplitBelow skinny tiles and >= 32 K-tiles: A is
 // shared by the workgroup's waves instead of re-read by every 16-column
 // skinny tile (BS fp32 M = 64: N = 2112, K = 7168 17.8 -> 14.8 us; N = 7168,
-// K = 16384 39.7 -> 33.0 us; M = 1 or short K stay faster on the skinny
+// K = 16384 39.7 -> 33.0 us; N = 8192, K = 7168, M = 48 / 64: 19.0 / 21.1 ->
+// 17.6 / 19.3 us; M = 1 or short K stay faster on the skinny
 // kernel, and row-major B (MXFP8) on the skinny kernel at any M).  Short K
 // (<= 16 K-tiles) with many skinny tiles goes to the decode kernel for
 // either layout: the skinny kernel's 8 waves would share too few K-tiles
@@ -286,7 +287,7 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, int cus,
     const long long base = (long long)p.n_tiles * p.m_tiles * batch;
     const bool short_k = k_tiles <= 16 && base >= 2 * kSplitBelow;
     if (m <= 64 && ((decode_ok && (base < kSplitBelow || short_k ||
-                                   (decode_wide && m >= 16 && base < 2 * kSplitBelow && k_tiles >= 32))) ||
+                                   (decode_wide && m >= 16 && base <= 2 * kSplitBelow && k_tiles >= 32))) ||
                     (decode_short && short_k))) {
         plan_decode(p, m, n, k_tiles, batch, b_bytes, cus);
         return p;
@@ -417,6 +418,22 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
     if (!p.skinny && !p.mid && small_m_wide(m, n, batch, (long long)k_tiles * 128, cus)) {
         if (m <= 32 && k_tiles > 16) p = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, true, decode_ok, decode_ok);
         else plan_mid(p, m, n, k_tiles, batch, cus, true);
+    }
+    // M = 17-64 whose 128 x 128 tiles alone fill 3/4 of the CUs (N >= 24576
+    // at batch 1): M = 33-64 the 128 x 128 kernel, which reads B once at full
+    // occupancy (N = 24576, K = 1024 - 7168: 1.2-1.4x over the decode and
+    // skinny kernels); M = 17-32 on K-panel B the decode kernel, whose waves
+    // share A (N = 24576 - 32768, K = 2048 - 7168: 1.05-1.25x over the skinny
+    // and 128 x 128 kernels)
+    const long long tiles128 = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
+    if (m > 16 && m <= kMidMinM && 4 * tiles128 >= 3LL * cus) {
+        if (m > 32) {
+            if (!p.mid) plan_mid(p, m, n, k_tiles, batch, cus, true);
+        } else if (decode_ok && k_tiles > 8) {
+            p = Plan{};
+            p.skinny = true;
+            plan_decode(p, m, n, k_tiles, batch, b_bytes, cus);
+        }
     }
     return p;
 }
@@ -561,6 +578,12 @@ Plan plan_mx(int m, int n, int k_tiles, int batch, long long b_bytes, bool fp4) 
         if (m <= 16) p = skinny(true);
         else plan_mid(p, m, n, k_tiles, batch, cus, true);
     }
+    // M = 33-64 whose 128 x 128 tiles alone fill 3/4 of the CUs: the
+    // 128 x 128 kernel reads B once at full occupancy where the decode and
+    // skinny kernels re-stream it per row group (N = 24576, M = 64, K =
+    // 1024-4096, MXFP4 / MXFP8: 1.3-1.6x over them)
+    const long long tiles128 = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
+    if (p.skinny && m > 32 && m <= kMidMinM && 4 * tiles128 >= 3LL * cus) plan_mid(p, m, n, k_tiles, batch, cus, true);
     return p;
 }
 

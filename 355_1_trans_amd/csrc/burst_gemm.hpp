@@ -114,6 +114,11 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
             // 1.1-1.25x slower than skinny / decode); 8-wave plans over short
             // K keep it (K = 1536, N = 12288 - 129280: best or within 8%)
             if (gate && wgs > cus && (waves == 16 || (!mx && k_tiles > 16))) continue;
+            // fp32 scales, M = 17-32: a 16-wave plan over more than half a
+            // round re-reads A's rows per 32-column tile as often as B's
+            // (N = 8192, K = 7168: 26.4 us vs 15.8 on the skinny / decode
+            // kernels)
+            if (gate && !mx && waves == 16 && m > 16 && 2 * wgs > cus) continue;
             const double kb = (16.0 * nb + m) * kt_per * 128 / 1024.0;
             const double cost = 2.5 + 0.025 * kb * (double)((wgs + cus - 1) / cus) + (split > 1 ? 3.4 : 0.0);
             if (cost < best.cost_us) {
