@@ -427,7 +427,8 @@ def sweep(args):
                 print(json.dumps({"sweep": args.sweep, "variant": variant, "M": m, "N": n, "K": k,
                                   "us": round(ms * 1e3, 2), "TFLOPS": round(tf, 1), "mfma_frac": round(tf / 5000.0, 4),
                                   "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_GBPS, 4),
-                                  "bound": "hbm" if hbm else "mfma", "kernel": q.last_launch()}), flush=True)
+                                  "bound": "hbm" if hbm else "mfma", "kernel": q.last_launch(),
+                                  "spread_us": timing.get("replay_us") or timing.get("launch_us")}), flush=True)
                 del Bs, SBs, calls, ws
             del qa, sa, C
         del qb, sb, bk, bpp
