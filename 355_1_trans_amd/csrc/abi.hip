@@ -122,7 +122,8 @@ uint64_t span(long long batch, long long batch_stride, long long rows, long long
     return (uint64_t)(((batch - 1) * batch_stride + (rows - 1) * pitch + last_row_len) * elem);
 }
 
-int ceil_div(int a, int b) { return (a + b - 1) / b; }
+// a >= 0, b > 0; no intermediate past a (a + b - 1 overflows near INT_MAX)
+int ceil_div(int a, int b) { return a / b + (a % b != 0); }
 
 // Elements per aligned vector store of C: the largest power of two (at
 // most 16 bytes) whose byte size divides ptr_c, the row pitch and, for
@@ -1621,16 +1622,16 @@ int qgemm_shuffle_weight_16x16(const uint8_t* src, uint8_t* dst, int n, int k_by
 
 size_t qgemm_e8m0_shuffle_bytes(int rows, int groups_k) {
     if (rows <= 0 || groups_k <= 0) return 0;
-    return (size_t)((rows + 31) / 32 * 32) * (size_t)((groups_k + 7) / 8 * 8);
+    return ((size_t)rows + 31) / 32 * 32 * (((size_t)groups_k + 7) / 8 * 8);
 }
 
 int qgemm_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int groups_k) {
     if (!src || !dst || rows <= 0 || groups_k <= 0) return (int)hipErrorInvalidValue;
-    const int kg8 = (groups_k + 7) / 8 * 8;
+    const size_t kb8 = ((size_t)groups_k + 7) / 8;    // 8-group blocks per 32-row block
     std::memset(dst, 0x7F, qgemm_e8m0_shuffle_bytes(rows, groups_k));
     for (int r = 0; r < rows; ++r)
         for (int g = 0; g < groups_k; ++g) {
-            const size_t o = ((size_t)(r / 32) * (kg8 / 8) + g / 8) * 256 + (size_t)(g % 4) * 64 +
+            const size_t o = ((size_t)(r / 32) * kb8 + g / 8) * 256 + (size_t)(g % 4) * 64 +
                              (size_t)(r % 16) * 4 + (size_t)((g % 8) / 4) * 2 + (size_t)((r % 32) / 16);
             dst[o] = src[(size_t)r * groups_k + g];
         }

@@ -94,7 +94,7 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
     if (m < 1 || m > 64 || k_tiles < 1 || k_tiles > 64 || n < 1 || batch < 1 || cus < 1) return best;
     const int mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     for (int nb : {2, 1}) {
-        const long long tiles = (long long)((n + 16 * nb - 1) / (16 * nb)) * batch;
+        const long long tiles = (((long long)n + 16 * nb - 1) / (16 * nb)) * batch;
         for (int s = 1; s <= max_split; ++s) {
             const int kt_per = (k_tiles + s - 1) / s;
             const int split = (k_tiles + kt_per - 1) / kt_per;

@@ -282,3 +282,24 @@ def test_quantizers_reject_bad_arguments(qgemm):
     assert lay(x, q, 40, 256, 256, None) == HIP_INVALID_VALUE                            # N % 16
     assert L.qgemm_shuffle_b_kpanel_device(x, q, 40, 200, 208, None) == HIP_INVALID_VALUE   # K % 128
     assert L.qgemm_shuffle_b_kpanel_device(x, x + 256, 40, 256, 256, None) == HIP_INVALID_VALUE  # overlap
+
+
+def test_extreme_dimensions_do_not_overflow(qgemm):
+    """Dimensions near INT_MAX through the workspace queries, the entries and
+    the host layout helpers (found with a host AddressSanitizer /
+    UndefinedBehaviorSanitizer build: rounding-up helpers overflowed int):
+    queries stay defined, entries reject, sizes are computed in 64 bits."""
+    L = qgemm.lib()
+    big = (1 << 31) - 1
+    for m, n in [(1, big), (big, 1), (64, big - 15), (big, big)]:
+        a = _kargs(qgemm, m=m, n=n)
+        for kid in range(-1, 9):
+            L.gemm_a8w8_mxfp8_kid_workspace_bytes(ctypes.byref(a), kid)
+            L.gemm_a4w4_mxfp4_kid_workspace_bytes(ctypes.byref(a), kid)
+            L.gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(ctypes.byref(a), kid)
+        assert L.gemm_a8w8_mxfp8(ctypes.byref(a), 1, None, 0, None) == HIP_INVALID_VALUE
+        assert L.gemm_a8w8_blockscale_bpreshuffle(ctypes.byref(a), 1, None, 0, None) == HIP_INVALID_VALUE
+    # e8m0_shuffle image: rows to 32, groups to 8, in 64 bits
+    assert L.qgemm_e8m0_shuffle_bytes(big, 8) == (big + 31) // 32 * 32 * 8
+    assert L.qgemm_e8m0_shuffle_bytes(32, big) == 32 * ((big + 7) // 8 * 8)
+    assert L.qgemm_ldsbypass_b_bytes(big, 128) == (big + 15) // 16 * 16 * 128
