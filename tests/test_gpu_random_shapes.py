@@ -1,5 +1,5 @@
 """Seeded random shapes through every kernel id of the MXFP8, MXFP4 and
-fp32-block-scale (bpreshuffle) entries, against the oracle.
+fp32-block-scale (bpreshuffle and LDS-bypass) entries, against the oracle.
 
 The hand-picked shape lists of the other GPU tests follow the planner's
 regions; these draws (M 1-200 weighted to decode sizes, N 1-1100 with any
@@ -99,4 +99,29 @@ def test_bs_random_shapes(qgemm, gpu, case):
         launched += 1
         for i in range(batch):
             assert_close(refs[i], out_to_f32(C[i]), f"bs {m}x{n}x{k} b{i} kid {kid} ({trace})")
+    assert launched >= 2
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_ldsbypass_random_shapes(qgemm, gpu, case):
+    """The LDS-bypass entry (B'' packed on the GPU from B) over the same kind
+    of draws."""
+    m, n, k, batch, bf16 = _draws("bs", 24, 3000)[case]
+    data = [make_bs(m, n, k, seed=case * 3 + i) for i in range(batch)]
+    refs = [O.gemm_bs_fp32(*d) for d in data]
+    kg, nbk = k // 128, (n + 127) // 128
+    A = torch.stack([torch.from_numpy(d[0]) for d in data]).to(gpu)
+    SA = torch.stack([torch.from_numpy(d[2]) for d in data]).to(gpu)
+    SB = torch.stack([torch.from_numpy(d[3]) for d in data]).to(gpu)
+    Bp = torch.stack([qgemm.ldsbypass_pack_b(torch.from_numpy(d[1]).to(gpu)) for d in data])
+    args = qgemm.LdsBypassKargs(A.data_ptr(), None, Bp.data_ptr(), 0, m, n, k, batch, k, 128, n, m * k,
+                                Bp[0].numel(), m * n, SA.data_ptr(), SB.data_ptr(), 1, kg, m * kg, nbk * kg,
+                                Bp[0].numel())
+    dt = torch.bfloat16 if bf16 else torch.float32
+    launched = 0
+    for kid, C, trace in _run_ids(qgemm, gpu, "gemm_a8w8_blockscale_ldsbypass_kid", args, range(6), dt, m, n,
+                                  batch):
+        launched += 1
+        for i in range(batch):
+            assert_close(refs[i], out_to_f32(C[i]), f"ldsbypass {m}x{n}x{k} b{i} kid {kid} ({trace})")
     assert launched >= 2
