@@ -312,10 +312,13 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, int cus,
 // runs the 256 x 256 kernel once it has at least kMidBelow tiles, else the
 // 128 x 128 kernel, with K split until about 2 * cus workgroups (two per
 // CU) are in flight -- cus (one per CU) when the tiles alone split K at
-// least in two -- with >= kMidMinKt K-tiles per slice.
+// least in two -- with >= kMidMinKt K-tiles per slice; where K has >= 24
+// K-tiles or the tiles are one M tile, slices down to kMidMinKtDeep while
+// one round of workgroups (one per CU) holds them.
 constexpr int kMidMinM = 64;
 constexpr int kMidBelow = 128;
-constexpr int kMidMinKt = 16;    // 8 measured slower where the split tail dominates (M = 256, N = 4096, K = 7168: 34.4 vs 27.0 us)
+constexpr int kMidMinKt = 16;
+constexpr int kMidMinKtDeep = 8;
 
 // M <= 256 with at least kMidBelow 256 x 256 tiles (N > 32512 at batch 1):
 // the planners below replace the 256 x 256 plan of small M there, and the
@@ -343,7 +346,7 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus, bool force
     p.kt_per_split = k_tiles;
     const long long tiles = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
     const long long target = 2LL * cus;    // two workgroups per CU
-    if (tiles >= target / 2 || tiles > kMaxCounters || (long long)m * n >= (1LL << 29))    // 32-bit partial offsets
+    if (tiles >= target / 2 || (long long)m * n >= (1LL << 29))    // 32-bit partial offsets
         return;
     long long split = std::min<long long>(target / tiles, k_tiles / kMidMinKt);
     // up to cus / 2 tiles: at most one workgroup per CU (four LDS stages,
@@ -351,11 +354,18 @@ void plan_mid(Plan& p, int m, int n, int k_tiles, int batch, int cus, bool force
     // 75.0 -> 61.9 us, BS fp32 M = 128 64.9 -> 47.0, M = 256 76.5 -> 64.0,
     // MXFP4 M = 256 54.7 -> 50.7; shapes with less K unchanged
     if (cus / tiles >= 2) split = std::min<long long>(split, cus / tiles);
+    // 8-K-tile slices (the slices summed by splitk_reduce_kernel): BS fp32
+    // M = 128, N = 2112, K = 7168 22.4 -> 17.7 us, MXFP4 M = 128 - 512,
+    // K = 7168 (28 K-tiles, unsplit before) 1.2-1.75x, MXFP8 M = 128,
+    // K = 2048 1.15-1.3x; K = 2048 at M >= 256, or a second round of
+    // workgroups, up to 1.6x slower
+    if (k_tiles >= 24 || ceil_div(m, 128) == 1)
+        split = std::max<long long>(split, std::min<long long>(cus / tiles, k_tiles / kMidMinKtDeep));
     if (split <= 1) return;
     p.kt_per_split = ceil_div(k_tiles, (int)split);
     p.splitk = ceil_div(k_tiles, p.kt_per_split);
     if (p.splitk > 1) {
-        p.ctr_bytes = kCounterBytes;
+        p.ctr_bytes = kCounterBytes;    // unused by this kernel: keeps the partials past the counter block
         p.ws_bytes = p.ctr_bytes + (size_t)p.splitk * batch * m * n * 4;
     }
 }
@@ -794,7 +804,6 @@ hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, qg::MidKind kind, 
     a.t = t;
     if (pl.splitk > 1 && ws) {
         if (ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return hipErrorInvalidValue;
-        a.counters = static_cast<unsigned*>(ws);
         a.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl.ctr_bytes);
         a.splitk = pl.splitk;
         a.kt_per_split = pl.kt_per_split;

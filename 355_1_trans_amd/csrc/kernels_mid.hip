@@ -1,5 +1,7 @@
 // Instantiations and launcher of the four-wave 128 x 128 kernel: fp8 with fp32
 // block scales (K-panel B' or fragment-order B''), MXFP8 and MXFP4 (row-major B).
+#include <climits>
+
 #include "launch.hpp"
 #include "mid_gemm.hpp"
 
@@ -33,12 +35,43 @@ static void mid_kind(const MidArgs& a, const dim3& grid, bool bf16, MidKind kind
     }
 }
 
+// The slice sum after a split-K launch: one thread per 4 elements (N % 4
+// == 0) or per element, over batch x M x N.
+static hipError_t launch_splitk_reduce(const SplitReduceArgs& r, bool bf16, hipStream_t s) {
+    const bool vec = r.n % 4 == 0;
+    const long long total = (long long)r.m * r.n * r.batch;
+    const long long blocks = ((vec ? total / 4 : total) + 255) / 256;
+    if (blocks <= 0 || blocks > INT_MAX) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks);
+    if (bf16) {
+        if (vec) splitk_reduce_kernel<true, true><<<grid, 256, 0, s>>>(r);
+        else splitk_reduce_kernel<true, false><<<grid, 256, 0, s>>>(r);
+    } else {
+        if (vec) splitk_reduce_kernel<false, true><<<grid, 256, 0, s>>>(r);
+        else splitk_reduce_kernel<false, false><<<grid, 256, 0, s>>>(r);
+    }
+    trace_launch("splitk_reduce<%s,%s,splitk%d>", bf16 ? "bf16" : "fp32", vec ? "x4" : "x1", r.splitk);
+    return hipGetLastError();
+}
+
 hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, MidKind kind, int stages, hipStream_t s) {
     const dim3 grid(a.t.tiles_m * a.t.tiles_n, a.splitk, batch);
     if (stages == 2) mid_kind<2>(a, grid, bf16, kind, s);
     else if (stages == 4) mid_kind<4>(a, grid, bf16, kind, s);
     else return hipErrorInvalidValue;
-    return hipGetLastError();
+    const hipError_t st = hipGetLastError();
+    if (st != hipSuccess || a.splitk == 1) return st;
+    SplitReduceArgs r{};
+    r.ws = a.ws;
+    r.c = a.t.c;
+    r.m = a.t.m;
+    r.n = a.t.n;
+    r.ldc = a.t.ldc;
+    r.c_vec = a.t.c_vec;
+    r.splitk = a.splitk;
+    r.batch = batch;
+    r.c_batch = a.t.c_batch;
+    return launch_splitk_reduce(r, bf16, s);
 }
 
 }  // namespace qg

@@ -28,10 +28,13 @@
 //    rescale).  fp8: lane (q, r) holds chunks q and q + 4 of row r with
 //    scale byte q; fp4: two MFMAs per K-tile, chunks 2q and 2q + 1 with
 //    scale bytes 2q and 2q + 1 (op_sel 0 and 1 of one 16-bit read);
-//  * split-K: each workgroup stores its fp32 partial tile device-coherently,
-//    then one relaxed counter atomic per workgroup (common.hpp); the last
-//    workgroup of a tile adds the slices in slice order (deterministic),
-//    rounds, stores and re-arms the counter.
+//  * split-K: every workgroup stores its fp32 partial tile and returns;
+//    splitk_reduce_kernel, launched next on the stream, adds the slices in
+//    slice order (deterministic) over the whole chip.  A last-arriving
+//    workgroup summing its tile instead streams all slices back through one
+//    CU at the end of the launch: 5-10 us of a 20-60 us kernel (M = 256,
+//    N = 2112, K = 7168: 26.5 us vs 22.4 us with the separate reduce), and
+//    it capped how deep K could split.
 //
 // LDS rows are 128 bytes, 16-byte chunks XOR-swizzled by row & 7.
 #pragma once
@@ -43,9 +46,74 @@ namespace qg {
 struct MidArgs {
     TileArgs t;            // tiles_m / tiles_n count 128 x 128 tiles
     float* ws;             // fp32 partials [splitk][batch][M][N] (splitk > 1)
-    unsigned* counters;    // [batch][tiles], zero between launches
     int splitk, kt_per_split;
 };
+
+// Sums the fp32 partials [splitk][batch][M][N] in slice order into C (row
+// pitch ldc elements, batch stride c_batch); c_vec as in TileArgs.
+struct SplitReduceArgs {
+    const float* ws;
+    void* c;
+    int m, n, ldc, c_vec, splitk, batch;
+    long long c_batch;
+};
+
+// One thread per 4 consecutive elements of a row (VEC: N % 4 == 0) or per
+// element; v = ((0 + p0) + p1) + ... (slice order: the same bits on every
+// run).
+template <bool BF16, bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const SplitReduceArgs r) {
+    constexpr int E = VEC ? 4 : 1;
+    const long long plane = (long long)r.m * r.n, total = plane * r.batch;
+    const long long e = ((long long)blockIdx.x * 256 + threadIdx.x) * E;
+    if (e >= total) return;
+    const int bz = (int)(e / plane);
+    const long long x = e - bz * plane;
+    const int m = (int)(x / r.n), n = (int)(x - (long long)m * r.n);
+    float v[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = 0.f;
+    // four slices' loads in flight before their adds (order kept)
+    for (int s0 = 0; s0 < r.splitk; s0 += 4) {
+        float u[4][E];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            if (s0 + d >= r.splitk) break;
+            const float* src = r.ws + (long long)(s0 + d) * total + e;
+            if constexpr (VEC) {
+                const f32x4 w = *(const f32x4*)src;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) u[d][i] = w[i];
+            } else {
+                u[d][0] = *src;
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            if (s0 + d >= r.splitk) break;
+#pragma unroll
+            for (int i = 0; i < E; ++i) v[i] += u[d][i];
+        }
+    }
+    const long long co = (long long)bz * r.c_batch + (long long)m * r.ldc + n;
+    if constexpr (BF16) {
+        uint16_t* c = (uint16_t*)r.c + co;
+        if (VEC && r.c_vec >= 4) {
+            *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        } else {
+#pragma unroll
+            for (int i = 0; i < E; ++i) c[i] = bf16_bits(v[i]);
+        }
+    } else {
+        float* c = (float*)r.c + co;
+        if (VEC && r.c_vec >= 4) {
+            if constexpr (VEC) *(f32x4*)c = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < E; ++i) c[i] = v[i];
+        }
+    }
+}
 
 namespace mid {
 template <int V>
@@ -88,7 +156,6 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
     __shared__ __attribute__((aligned(1024))) uint8_t st1[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t st2[STAGES > 2 ? STAGE : 1];
     __shared__ __attribute__((aligned(1024))) uint8_t st3[STAGES > 2 ? STAGE : 1];
-    __shared__ int last_flag;
 
     const TileArgs& p = mp.t;
     // ---- tile coordinates: XCD-contiguous remap, then grouped raster ----
@@ -354,73 +421,26 @@ __global__ __launch_bounds__(256, STAGES == 2 ? 2 : 1) void mid_gemm_kernel(cons
         return;
     }
 
-    // split-K: this slice's partial tile, device-coherent; then the counter
+    // split-K: this slice's partial tile (the kernel boundary orders these
+    // stores before splitk_reduce_kernel's loads)
     const long long plane = (long long)M * N;
-    const int batch = gridDim.z;
-    const long long split_stride = (long long)batch * plane;
-    const float* ws0 = mp.ws + (long long)bz * plane;
+    const long long split_stride = (long long)gridDim.z * plane;
+    float* const slice = mp.ws + sk * split_stride + (long long)bz * plane;
     const bool nvec = (N & 3) == 0;
-    {
-        const auto part_out = partial_rsrc(ws0 + sk * split_stride);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int m = mw + 16 * i, n = nw0 + 16 * j;
-                if (m >= M) continue;
-                const int x = m * N + n;
-                if (nvec && n + 3 < N) {
-                    store_partial4(part_out, x, acc[i][j]);
-                } else {
-                    for (int r = 0; r < 4; ++r)
-                        if (n + r < N) store_partial1(part_out, x + r, acc[i][j][r]);
-                }
-            }
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    unsigned* ctr = mp.counters + (long long)bz * T + tile;
-    if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(mp.splitk - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    // slices in order 0 .. splitk-1 (this workgroup's own from registers);
-    // each slice's 16 loads are issued together
-    f32x4 v[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < mp.splitk; ++s) {
-        f32x4 u[4][4];
-        const auto src = partial_rsrc(ws0 + s * split_stride);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int m = min(mw + 16 * i, M - 1), n = nw0 + 16 * j;
-                const int x = m * N + n;
-                if (s == sk) {
-                    u[i][j] = acc[i][j];
-                } else if (nvec && n + 3 < N) {
-                    u[i][j] = load_partial4(src, x);
-                } else {
-                    for (int r = 0; r < 4; ++r) u[i][j][r] = n + r < N ? load_partial1(src, x + r) : 0.f;
-                }
+        for (int j = 0; j < 4; ++j) {
+            const int m = mw + 16 * i, n = nw0 + 16 * j;
+            if (m >= M) continue;
+            float* dst = slice + m * N + n;
+            if (nvec && n + 3 < N) {
+                *(f32x4*)dst = acc[i][j];
+            } else {
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < N) dst[r] = acc[i][j][r];
             }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v[i][j][r] += u[i][j][r];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) store_c(mw + 16 * i, nw0 + 16 * j, v[i][j]);
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
 }
 
 }  // namespace qg

@@ -102,10 +102,11 @@ def test_workspace_queries(qgemm):
         assert ws >= 2048 + 2 * m * n * 4 and (ws - 2048) % (m * n * 4) == 0, (m, n, k, ws)
     # enough N tiles for the skinny kernel -> no split
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1, n=7168, k=16384))) == 0
-    # M > 64 with few 256 x 256 tiles: the 128 x 128 kernel, 64 tiles, K
-    # split in two (16 K-tiles per slice at least)
+    # M > 64 with few 256 x 256 tiles: the 128 x 128 kernel, 64 tiles; K of
+    # 32 K-tiles split in four (8-K-tile slices while one workgroup per CU
+    # holds them: 256 / 64 = 4)
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=4096))) == \
-        2048 + 2 * 128 * 8192 * 4
+        2048 + 4 * 128 * 8192 * 4
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=8192, k=1024))) == 0
     # 56 tiles of 128 x 128 at N = 7168: split capped at kCUs / tiles = 4
     # (one workgroup per CU), not 512 / 56 = 9; MXFP4 K-tiles are 256 deep
