@@ -589,12 +589,19 @@ Plan plan_mx(int m, int n, int k_tiles, int batch, long long b_bytes, bool fp4) 
         if (m <= 16) p = skinny(true);
         else plan_mid(p, m, n, k_tiles, batch, cus, true);
     }
-    // M = 33-64 whose 128 x 128 tiles alone fill 3/4 of the CUs: the
+    // M = 33-64 whose 128 x 128 tiles alone fill 3/8 of the CUs: the
     // 128 x 128 kernel reads B once at full occupancy where the decode and
     // skinny kernels re-stream it per row group (N = 24576, M = 64, K =
-    // 1024-4096, MXFP4 / MXFP8: 1.3-1.6x over them)
+    // 1024-4096, MXFP4 / MXFP8: 1.3-1.6x over them; N = 12288 - 16384,
+    // M = 48 / 64, K = 7168 / 16384: MXFP8 1.05-1.17x, MXFP4 1.02-1.14x).
+    // M = 17-32 where the skinny plan spills into a second round and the
+    // 128 x 128 tiles fill half of the CUs (N = 20480, K = 7168 / 16384:
+    // 1.4-1.6x; one round at N = 16384 stays skinny)
     const long long tiles128 = (long long)ceil_div(m, 128) * ceil_div(n, 128) * batch;
-    if (p.skinny && m > 32 && m <= kMidMinM && 4 * tiles128 >= 3LL * cus) plan_mid(p, m, n, k_tiles, batch, cus, true);
+    const long long skinny_wgs = (long long)p.n_tiles * p.m_tiles * batch * p.splitk;
+    if (p.skinny && m > 32 && m <= kMidMinM && 8 * tiles128 >= 3LL * cus) plan_mid(p, m, n, k_tiles, batch, cus, true);
+    else if (p.skinny && m > 16 && m <= 32 && skinny_wgs > cus && 2 * tiles128 >= cus)
+        plan_mid(p, m, n, k_tiles, batch, cus, true);
     return p;
 }
 
@@ -956,11 +963,20 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
                 // A's slice in LDS and no partials (MXFP4 / MXFP8, N =
                 // 24576-32768, K <= 4096, M = 24-64: 1.05-2.1x over the
                 // burst / decode / 128 x 128 plans); its split plans lose
-                // to them (up to 1.75x slower at N = 8192)
+                // to them where N is narrow (up to 1.75x slower at N =
+                // 8192) and win while N's 128-column strips cover 3/8 to
+                // 3/4 of the CUs (N = 12288 - 20480, K = 4096 / 7168,
+                // M = 32-64: up to 1.34x, a few shapes within 8% of the
+                // best id; wider N keeps the 128 x 128 kernel, the best id
+                // measured at N = 24576 / 32768)
                 const BandPlan bd = plan_band(a.m, a.n, kt, a.batch);
-                if (bd.ok && bd.splitk == 1 && 4LL * bd.bands * a.batch >= 3LL * cus) {
+                const long long bands = (long long)bd.bands * a.batch;
+                const long long strips = (long long)ceil_div(a.n, 128) * a.batch;
+                if (bd.ok && ((bd.splitk == 1 && 4 * bands >= 3LL * cus) || (bd.splitk > 1 && 8 * strips >= 3LL * cus && 4 * strips < 3LL * cus)) &&
+                    (bd.splitk == 1 || have_ws)) {
                     r.bd = bd;
                     r.kid = QGEMM_KID_BAND;
+                    r.ws_bytes = std::max(r.ws_bytes, bd.ws_bytes);
                     return r;
                 }
             }
