@@ -446,6 +446,15 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
             plan_decode(p, m, n, k_tiles, batch, b_bytes, cus);
         }
     }
+    // M = 17-64 whose skinny plan spills a little past one round (1 to 1.5
+    // rounds) while the 128 x 128 tiles fill half of the CUs: the 128 x 128
+    // kernel (N = 20480, K = 4096-16384: 1.07-1.74x; M = 32, K = 4096 the
+    // decode kernel is another 9% faster). Two full rounds stay skinny
+    // (ldsbypass M = 32, N = 32768, K = 7168: the fastest id)
+    const long long skinny_wgs = (long long)p.n_tiles * p.m_tiles * batch * p.splitk;
+    if (p.skinny && !p.decode && m > 16 && m <= kMidMinM && 2 * tiles128 >= cus && skinny_wgs > cus &&
+        2 * skinny_wgs < 3LL * cus)
+        plan_mid(p, m, n, k_tiles, batch, cus, true);
     return p;
 }
 
