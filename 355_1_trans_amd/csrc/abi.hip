@@ -402,19 +402,26 @@ Plan plan_bsf32(int m, int n, int k_tiles, int batch, long long b_bytes, bool de
     Plan p = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, false, decode_ok, decode_ok);
     // 64 < M <= 128: half of every 256-row tile would be padding, so the
     // 128 x 128 kernel even with many tiles (M = 128, N = 65536, K = 1536:
-    // 30.2 -> 25.7 us)
-    plan_mid(p, m, n, k_tiles, batch, cus, m > kMidMinM && m <= 128);
+    // 30.2 -> 25.7 us); also at exactly kMidBelow 256 x 256 tiles, half a
+    // round, with >= 12 K-tiles (M = 4096, N = 2048, K = 7168: 70.3 -> 65.0
+    // us; M = 1024, N = 8192, K = 1536: 20.5 -> 18.3 us; M = 256,
+    // N = 32768, K = 512 stays on 256 x 256 tiles, 11.7 vs 13.3 us; from
+    // 168 tiles the 256 x 256 kernel is 1.3-1.45x faster)
+    const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    plan_mid(p, m, n, k_tiles, batch, cus,
+             m > kMidMinM && (m <= 128 || (tiles256 == kMidBelow && k_tiles >= 12)));
     if (p.mid && m <= 320) {
         // one round of skinny workgroups (3/4 to all of the CUs, no K split),
-        // each streaming <= 768 KB of A and B, beats the 128 x 128 kernel's
-        // K split (traced dsv4 shapes, N = 1536 / 2048, K = 7168, M = 66-312:
-        // 1.2-1.4x; N = 7168, K = 3072, M = 128: 21.9 -> 17.7 us); more bytes
-        // per workgroup (N = 6144, K = 7168) or a second round (M = 192,
-        // N = 1536) stay on the 128 x 128 kernel
+        // each streaming <= 512 KB of A and B, beats the 128 x 128 kernel's
+        // K split (N = 7168, K = 3072, M = 128: 21.9 -> 17.7 us; N = 8192,
+        // K = 1536, M = 128); at 570-690 KB per workgroup (N = 1536 / 2048,
+        // K = 7168, M = 66-312) the 128 x 128 kernel with its separately
+        // reduced deep split is 1.05-1.4x faster, and more bytes or a
+        // second round of skinny workgroups favour it further
         const Plan s = plan_gemm(m, n, k_tiles, batch, b_bytes, cus, true, false);
         const long long wgs = (long long)s.n_tiles * s.m_tiles * batch;
         const long long wg_bytes = 16LL * (s.mb + s.nb) * k_tiles * 128;
-        if (s.splitk == 1 && wgs <= cus && 4 * wgs >= 3LL * cus && wg_bytes <= 768 * 1024) p = s;
+        if (s.splitk == 1 && wgs <= cus && 4 * wgs >= 3LL * cus && wg_bytes <= 512 * 1024) p = s;
     }
     // long K (>= 128 K-tiles) where the 128 x 128 plan would run unsplit:
     // the 256 x 256 kernel, whose tail split (plan_tail) fills the CUs
