@@ -600,7 +600,16 @@ Plan plan_mx(int m, int n, int k_tiles, int batch, long long b_bytes, bool fp4) 
                    : plan_gemm(m, n, k_tiles, batch, b_bytes, cus, force);
     };
     Plan p = skinny(false);
-    plan_mid(p, m, n, k_tiles, batch, cus);
+    // M > 256: the 128 x 128 kernel below 96 256 x 256 tiles, and up to
+    // kMidBelow (inclusive) only with short K (<= 16 K-tiles fp8, <= 12
+    // fp4); longer K from 96 tiles runs the 256 x 256 kernel (M = 512-1024,
+    // N = 6144-12288, K = 2048-7168: 128 x 128 1.03-1.2x slower there,
+    // 1.1-1.3x faster with short K; N = 8192, M = 1024, K = 1536 MXFP4
+    // 18.6 -> 14.0 us)
+    const long long tiles256 = (long long)ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    const bool short_k = k_tiles <= (fp4 ? 12 : 16);
+    if (m <= 256 || tiles256 < 96 || (tiles256 <= kMidBelow && short_k))
+        plan_mid(p, m, n, k_tiles, batch, cus, m > 256 && tiles256 == kMidBelow);
     if (!p.skinny && !p.mid && small_m_wide(m, n, batch, (long long)k_tiles * (fp4 ? 256 : 128), cus)) {
         if (m <= 16) p = skinny(true);
         else plan_mid(p, m, n, k_tiles, batch, cus, true);
