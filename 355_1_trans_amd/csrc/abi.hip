@@ -827,6 +827,42 @@ hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int
                : qg::launch_wide_mx8_raw(t, a.batch, bf16, pb, stream);
 }
 
+// The four-wave MX kernel split into s equal K slices (plan_wide_split):
+// slice z of the launch's batch reads A / B row bytes [z * slice, (z + 1) *
+// slice) and the row-major scales of those groups, and writes fp32 plane z
+// of the workspace (after the counter block); splitk_reduce_kernel then
+// sums the planes in slice order into C.
+hipError_t run_wide_split(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int s, bool bf16, void* ws,
+                          hipStream_t stream) {
+    const int slice = a.k / s;                          // K elements per slice
+    const int slice_bytes = fp4 ? slice / 2 : slice;    // multiple of 128 (>= kWideSplitMinKt K-tiles)
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+    TileArgs w = t;
+    w.kbytes = slice_bytes;
+    w.a_batch = slice_bytes;
+    w.b_batch = slice_bytes;
+    w.sfa_sk = w.sfb_sk = fp4 ? 8 : 4;    // row-major scales: one K-tile's bytes
+    w.sfa_batch = w.sfb_batch = slice / 32;
+    w.c = part;
+    w.ldc = a.n;
+    w.c_batch = (long long)a.m * a.n;
+    w.c_vec = a.n % 4 == 0 ? 4 : a.n % 2 == 0 ? 2 : 1;
+    const hipError_t st = fp4 ? qg::launch_wide_mx4_raw(w, s, false, 8, stream)
+                              : qg::launch_wide_mx8_raw(w, s, false, 4, stream);
+    if (st != hipSuccess) return st;
+    qg::SplitReduceArgs r{};
+    r.ws = part;
+    r.c = t.c;
+    r.m = a.m;
+    r.n = a.n;
+    r.ldc = t.ldc;
+    r.c_vec = t.c_vec;
+    r.splitk = s;
+    r.batch = 1;
+    r.c_batch = t.c_batch;
+    return qg::launch_splitk_reduce(r, bf16, stream);
+}
+
 // Launches the 128 x 128 kernel; a NULL workspace runs it without a K split.
 hipError_t run_mid(TileArgs t, int batch, Plan pl, bool bf16, qg::MidKind kind, void* ws, size_t ws_bytes,
                    int k_tiles, hipStream_t stream) {
@@ -946,8 +982,41 @@ struct MxRoute {
     StreamPlan sp;
     qg::BurstPlan bp;
     BandPlan bd;
+    int wsplit = 1;    // K slices of the four-wave kernel (plan_wide_split)
     size_t ws_bytes = 0;
 };
+
+// K split of the four-wave MX kernel (batch 1) where its 256 x 256 tiles
+// leave at least half of the CUs idle: the K slices run as batch entries of
+// the unchanged kernel (A / B / scale batch strides of one slice's bytes
+// along K, row-major scales, fp32 output into partial planes) and
+// splitk_reduce_kernel sums them.  Slices of >= kWideSplitMinKt K-tiles,
+// equal (the slice count divides the K-tiles): MXFP8 M = 512-1024,
+// N = 6144-12288 at 96-128 tiles, K = 7168 (28-K-tile slices) 1.0-1.12x,
+// K = 16384 1.2-1.36x; 16-K-tile slices (K = 4096) ran 4-17% slower than
+// the unsplit kernel.  MXFP8 only: the slices read row-major scales, and
+// MXFP4's unsplit kernel with 32-byte scale panels kept pace (K = 16384:
+// 0.87-1.05x split against unsplit)
+constexpr int kWideSplitMinKt = 24;
+int plan_wide_split(const opus_gemm_scale_kargs& a, bool fp4, int cus) {
+    if (fp4 || a.batch != 1 || (long long)a.m * a.n >= (1LL << 29)) return 1;
+    const int kt = a.k / (fp4 ? 256 : 128);
+    const long long tiles = (long long)ceil_div(a.m, 256) * ceil_div(a.n, 256);
+    int s = (int)std::min<long long>(cus / tiles, kt / kWideSplitMinKt);
+    while (s > 1 && kt % s) --s;
+    return std::max(s, 1);
+}
+size_t wide_split_bytes(const opus_gemm_scale_kargs& a, int s) {
+    return s > 1 ? kCounterBytes + (size_t)s * a.m * a.n * 4 : 0;
+}
+// The four-wave kernel's workspace: the split's partial planes when they fit
+// the caller's workspace (ws_cap), else the scale-panel copy.
+void plan_wide_ws(MxRoute& r, const opus_gemm_scale_kargs& a, bool fp4, int cus, size_t ws_cap) {
+    const int s = plan_wide_split(a, fp4, cus);
+    const size_t sb = wide_split_bytes(a, s);
+    r.wsplit = s > 1 && sb <= ws_cap ? s : 1;
+    r.ws_bytes = std::max(scale_panel_bytes(a), r.wsplit > 1 ? sb : 0);
+}
 
 // Burst plan for MX row-major B: the fp32-block-scale gate, and only up to
 // 32 K-tiles (4 KB of K per row) and past M = kStreamMaxM.  Measured
@@ -967,7 +1036,7 @@ qg::BurstPlan plan_mx_burst(int m, int n, int k_tiles, int batch, bool gate) {
     return qg::burst_plan(m, n, k_tiles, batch, device_cus(), kMaxCounters, gate, 16, true);
 }
 
-MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws) {
+MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws, size_t ws_cap) {
     MxRoute r;
     r.kid = kid;
     if (a.m <= 0 || a.n <= 0 || a.k <= 0 || a.batch <= 0 || a.k % (fp4 ? 256 : 128)) return r;
@@ -979,8 +1048,9 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.pl = plan_mx(a.m, a.n, kt, a.batch, bb, fp4);
             r.sp = plan_stream(a.m, a.n, a.k, a.batch, fp4);
             r.bp = plan_mx_burst(a.m, a.n, kt, a.batch, true);
+            if (!r.pl.skinny && !r.pl.mid) plan_wide_ws(r, a, fp4, cus, have_ws ? ws_cap : 0);
             r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
-                                   r.pl.skinny || r.pl.mid ? 0 : scale_panel_bytes(a)});
+                                   r.pl.skinny || r.pl.mid ? 0 : r.ws_bytes});
             r.ok = true;
             if (a.m > 16 && band_ok(a)) {
                 // the band kernel when one unsplit round of bands covers
@@ -1020,7 +1090,7 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             return r;
         }
         case QGEMM_KID_TILE256:
-            r.ws_bytes = scale_panel_bytes(a);
+            plan_wide_ws(r, a, fp4, cus, have_ws ? ws_cap : 0);
             break;
         case QGEMM_KID_MID:
             plan_mid(r.pl, a.m, a.n, kt, a.batch, cus, true);
@@ -1097,6 +1167,7 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
             return run_mid(t, a.batch, r.pl, bf16, fp4 ? qg::MidKind::MX4 : qg::MidKind::MX8, ws, ws_bytes, kt,
                            stream);
         default: {
+            if (r.wsplit > 1 && ws) return run_wide_split(t, a, fp4, r.wsplit, bf16, ws, stream);
             // fp8: 16-byte panels (32-byte ones cover 8 K-tiles and measured 1%
             // slower); fp4: 32-byte panels (4 K-tiles, two DMA lanes per scale
             // row) need whole panels, K % 1024 == 0
@@ -1251,7 +1322,7 @@ static hipError_t mx_entry(const opus_gemm_scale_kargs* args, bool fp4, int out_
     hipError_t st = validate_mx(args, out_dtype, args ? (fp4 ? args->k / 2 : args->k) : 0, fp4 ? 256 : 128, &sp);
     if (st != hipSuccess) return st;
     const auto& a = *args;
-    const MxRoute r = route_mx(a, fp4, kernel_id, workspace != nullptr);
+    const MxRoute r = route_mx(a, fp4, kernel_id, workspace != nullptr, workspace_bytes);
     if (!r.ok) return hipErrorInvalidValue;
     st = check_workspace(workspace, workspace_bytes, r.ws_bytes, sp);
     if (st != hipSuccess) return st;
@@ -1264,9 +1335,11 @@ static hipError_t mx_entry(const opus_gemm_scale_kargs* args, bool fp4, int out_
     return run_mx(r, t, a, fp4, out_dtype == QGEMM_OUT_BF16, workspace, workspace_bytes, stream);
 }
 
-static size_t mx_workspace(const opus_gemm_scale_kargs* args, bool fp4, int kernel_id) {
+// ws_cap: the most workspace the caller can bring (the four-wave kernel's
+// K split is planned only when its partial planes fit)
+static size_t mx_workspace(const opus_gemm_scale_kargs* args, bool fp4, int kernel_id, size_t ws_cap = SIZE_MAX) {
     if (!args) return 0;
-    const MxRoute r = route_mx(*args, fp4, kernel_id, true);
+    const MxRoute r = route_mx(*args, fp4, kernel_id, true, ws_cap);
     return r.ok ? r.ws_bytes : 0;
 }
 
@@ -1410,7 +1483,7 @@ size_t gemm_a4w4_mxfp4_noalloc_max_workspace_bytes(void) { return kScratchBytes;
 // workspace: no allocation and no caller buffer beyond A, B, scales and C.
 hipError_t gemm_a4w4_mxfp4_noalloc(const opus_gemm_scale_kargs* args, int out_dtype, hipStream_t stream) {
     qg::trace_reset();
-    const size_t need = gemm_a4w4_mxfp4_workspace_bytes(args);
+    const size_t need = mx_workspace(args, true, QGEMM_KID_AUTO, kScratchBytes);
     if (need > kScratchBytes) return hipErrorInvalidValue;    // beyond the static scratch
     Spans sp;
     hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256, &sp);

@@ -37,7 +37,7 @@ static void mid_kind(const MidArgs& a, const dim3& grid, bool bf16, MidKind kind
 
 // The slice sum after a split-K launch: one thread per 4 elements (N % 4
 // == 0) or per element, over batch x M x N.
-static hipError_t launch_splitk_reduce(const SplitReduceArgs& r, bool bf16, hipStream_t s) {
+hipError_t launch_splitk_reduce(const SplitReduceArgs& r, bool bf16, hipStream_t s) {
     const bool vec = r.n % 4 == 0;
     const long long total = (long long)r.m * r.n * r.batch;
     const long long blocks = ((vec ? total / 4 : total) + 255) / 256;

@@ -52,6 +52,9 @@ struct MidArgs;
 enum class MidKind : int { BS_KPANEL, BS_FRAG, MX8, MX4 };
 // stages: 2 (two workgroups per CU) or 4 (one, three K-tiles in flight)
 hipError_t launch_mid(const MidArgs& a, int batch, bool bf16, MidKind kind, int stages, hipStream_t s);
+// kernels_mid.hip: sum of fp32 split-K partial planes [splitk][batch][M][N] into C
+struct SplitReduceArgs;
+hipError_t launch_splitk_reduce(const SplitReduceArgs& r, bool bf16, hipStream_t s);
 // skinny_*.hip: skinny-M / split-K kernel (mb = M-tile rows / 16, nb = N-tile columns / 16)
 struct SkinnyArgs;
 enum class SkinnyKind : int { MX8_RAW, MX4_RAW, BSF32_KPANEL, BSF32_FRAG };
