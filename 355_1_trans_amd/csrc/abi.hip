@@ -787,6 +787,42 @@ size_t scale_panel_bytes(const opus_gemm_scale_kargs& a) {
 
 // Launches the wide MX kernel (panel width pb, kt_bytes scale bytes per
 // K-tile and row), through the panel-major copy when the workspace holds it.
+// Copies both operands' row-major E8M0 scales into the panel-major layout
+// [K/32/pb][rows][pb] after the workspace's counter block and points t at
+// it (per-K-tile stride rows * kt_bytes, batch strides whole planes).
+hipError_t copy_scale_panels(TileArgs& t, const opus_gemm_scale_kargs& a, int pb, int kt_bytes, void* ws,
+                             hipStream_t stream) {
+    const int kg = a.k / 32;
+    uint8_t* pa = static_cast<uint8_t*>(ws) + kCounterBytes;
+    uint8_t* pbp = pa + round256((size_t)a.batch * a.m * kg);
+    qg::ScalePanelArgs sp{};
+    sp.src[0] = t.sfa;
+    sp.src[1] = t.sfb;
+    sp.dst[0] = pa;
+    sp.dst[1] = pbp;
+    sp.rows[0] = a.m;
+    sp.rows[1] = a.n;
+    sp.ld[0] = a.stride_sfa;
+    sp.ld[1] = a.stride_sfb;
+    sp.src_batch[0] = a.stride_sfa_batch;
+    sp.src_batch[1] = a.stride_sfb_batch;
+    sp.dst_batch[0] = (long long)a.m * kg;
+    sp.dst_batch[1] = (long long)a.n * kg;
+    sp.ngroups = kg;
+    sp.pb = pb;
+    const hipError_t st = qg::launch_mx_scale_panels(sp, a.batch, stream);
+    if (st != hipSuccess) return st;
+    t.sfa = pa;
+    t.sfb = pbp;
+    t.sfa_sm = pb;
+    t.sfb_sn = pb;
+    t.sfa_sk = a.m * kt_bytes;
+    t.sfb_sk = a.n * kt_bytes;
+    t.sfa_batch = sp.dst_batch[0];
+    t.sfb_batch = sp.dst_batch[1];
+    return hipSuccess;
+}
+
 hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int pb, bool bf16, void* ws,
                        size_t ws_bytes, hipStream_t stream) {
     const int kt_bytes = fp4 ? 8 : 4;
@@ -794,34 +830,8 @@ hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int
     t.sfb_sk = kt_bytes;
     const size_t need = scale_panel_bytes(a);
     if (pb >= 16 && need && ws && ws_bytes >= need && aligned(ws, 256)) {
-        const int kg = a.k / 32;
-        uint8_t* pa = static_cast<uint8_t*>(ws) + kCounterBytes;
-        uint8_t* pbp = pa + round256((size_t)a.batch * a.m * kg);
-        qg::ScalePanelArgs sp{};
-        sp.src[0] = t.sfa;
-        sp.src[1] = t.sfb;
-        sp.dst[0] = pa;
-        sp.dst[1] = pbp;
-        sp.rows[0] = a.m;
-        sp.rows[1] = a.n;
-        sp.ld[0] = a.stride_sfa;
-        sp.ld[1] = a.stride_sfb;
-        sp.src_batch[0] = a.stride_sfa_batch;
-        sp.src_batch[1] = a.stride_sfb_batch;
-        sp.dst_batch[0] = (long long)a.m * kg;
-        sp.dst_batch[1] = (long long)a.n * kg;
-        sp.ngroups = kg;
-        sp.pb = pb;
-        const hipError_t st = qg::launch_mx_scale_panels(sp, a.batch, stream);
+        const hipError_t st = copy_scale_panels(t, a, pb, kt_bytes, ws, stream);
         if (st != hipSuccess) return st;
-        t.sfa = pa;
-        t.sfb = pbp;
-        t.sfa_sm = pb;
-        t.sfb_sn = pb;
-        t.sfa_sk = a.m * kt_bytes;
-        t.sfb_sk = a.n * kt_bytes;
-        t.sfa_batch = sp.dst_batch[0];
-        t.sfb_batch = sp.dst_batch[1];
     }
     return fp4 ? qg::launch_wide_mx4_raw(t, a.batch, bf16, pb, stream)
                : qg::launch_wide_mx8_raw(t, a.batch, bf16, pb, stream);
@@ -832,23 +842,38 @@ hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int
 // slice) and the row-major scales of those groups, and writes fp32 plane z
 // of the workspace (after the counter block); splitk_reduce_kernel then
 // sums the planes in slice order into C.
+int wide_split_pb(const opus_gemm_scale_kargs& a, bool fp4, int s);
+
 hipError_t run_wide_split(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int s, bool bf16, void* ws,
                           hipStream_t stream) {
     const int slice = a.k / s;                          // K elements per slice
     const int slice_bytes = fp4 ? slice / 2 : slice;    // multiple of 128 (>= kWideSplitMinKt K-tiles)
-    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+    const int kt_bytes = fp4 ? 8 : 4;
+    const int pb = wide_split_pb(a, fp4, s);
     TileArgs w = t;
     w.kbytes = slice_bytes;
     w.a_batch = slice_bytes;
     w.b_batch = slice_bytes;
-    w.sfa_sk = w.sfb_sk = fp4 ? 8 : 4;    // row-major scales: one K-tile's bytes
-    w.sfa_batch = w.sfb_batch = slice / 32;
+    size_t head = kCounterBytes;
+    if (pb >= 16) {
+        // panel-major copy [K/32/pb][rows][pb]: a slice of whole panels
+        // starts (slice / 32) * rows bytes further
+        const hipError_t st = copy_scale_panels(w, a, pb, kt_bytes, ws, stream);
+        if (st != hipSuccess) return st;
+        w.sfa_batch = (long long)(slice / 32) * a.m;
+        w.sfb_batch = (long long)(slice / 32) * a.n;
+        head = scale_panel_bytes(a);
+    } else {
+        w.sfa_sk = w.sfb_sk = kt_bytes;    // row-major scales: one K-tile's bytes
+        w.sfa_batch = w.sfb_batch = slice / 32;
+    }
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + head);
     w.c = part;
     w.ldc = a.n;
     w.c_batch = (long long)a.m * a.n;
     w.c_vec = a.n % 4 == 0 ? 4 : a.n % 2 == 0 ? 2 : 1;
-    const hipError_t st = fp4 ? qg::launch_wide_mx4_raw(w, s, false, 8, stream)
-                              : qg::launch_wide_mx8_raw(w, s, false, 4, stream);
+    const hipError_t st = fp4 ? qg::launch_wide_mx4_raw(w, s, false, pb, stream)
+                              : qg::launch_wide_mx8_raw(w, s, false, pb, stream);
     if (st != hipSuccess) return st;
     qg::SplitReduceArgs r{};
     r.ws = part;
@@ -991,29 +1016,43 @@ struct MxRoute {
 // the unchanged kernel (A / B / scale batch strides of one slice's bytes
 // along K, row-major scales, fp32 output into partial planes) and
 // splitk_reduce_kernel sums them.  Slices of >= kWideSplitMinKt K-tiles,
-// equal (the slice count divides the K-tiles): MXFP8 M = 512-1024,
-// N = 6144-12288 at 96-128 tiles, K = 7168 (28-K-tile slices) 1.0-1.12x,
-// K = 16384 1.2-1.36x; 16-K-tile slices (K = 4096) ran 4-17% slower than
-// the unsplit kernel.  MXFP8 only: the slices read row-major scales, and
-// MXFP4's unsplit kernel with 32-byte scale panels kept pace (K = 16384:
-// 0.87-1.05x split against unsplit)
+// equal (the slice count divides the K-tiles).  The slices read the
+// scale-panel copy when the panels divide them (whole panels per slice),
+// else row-major scales.  M = 512-1024, N = 6144-12288 at 96-128 tiles:
+// MXFP8 K = 7168 (28-K-tile slices) 1.07-1.2x, K = 16384 1.35-1.49x;
+// MXFP4 K = 16384 1.16-1.18x; 16-K-tile slices (K = 4096) ran 4-17%
+// slower than the unsplit kernel, and MXFP4 on row-major scales 0.87-1.05x
+// against its unsplit kernel on 32-byte panels, so it splits only on
+// panels.
 constexpr int kWideSplitMinKt = 24;
+// panel width of a split into s slices: 16 (fp8) / 32 or 16 (fp4) when the
+// panels divide the slices, else the row-major widths 4 / 8
+int wide_split_pb(const opus_gemm_scale_kargs& a, bool fp4, int s) {
+    const int kt_bytes = fp4 ? 8 : 4;
+    const int pb = fp4 ? (a.k % 1024 == 0 ? 32 : 16) : 16;
+    const int slice_kt = a.k / (fp4 ? 256 : 128) / s;
+    return mx_wide_panels(a) && slice_kt % (pb / kt_bytes) == 0 ? pb : kt_bytes;
+}
 int plan_wide_split(const opus_gemm_scale_kargs& a, bool fp4, int cus) {
-    if (fp4 || a.batch != 1 || (long long)a.m * a.n >= (1LL << 29)) return 1;
+    if (a.batch != 1 || (long long)a.m * a.n >= (1LL << 29)) return 1;
     const int kt = a.k / (fp4 ? 256 : 128);
     const long long tiles = (long long)ceil_div(a.m, 256) * ceil_div(a.n, 256);
     int s = (int)std::min<long long>(cus / tiles, kt / kWideSplitMinKt);
     while (s > 1 && kt % s) --s;
+    if (s > 1 && fp4 && wide_split_pb(a, fp4, s) < 16) return 1;
     return std::max(s, 1);
 }
-size_t wide_split_bytes(const opus_gemm_scale_kargs& a, int s) {
-    return s > 1 ? kCounterBytes + (size_t)s * a.m * a.n * 4 : 0;
+// [counters | scale panels (when used) | s fp32 partial planes]
+size_t wide_split_bytes(const opus_gemm_scale_kargs& a, bool fp4, int s) {
+    if (s <= 1) return 0;
+    const size_t head = wide_split_pb(a, fp4, s) >= 16 ? scale_panel_bytes(a) : kCounterBytes;
+    return head + (size_t)s * a.m * a.n * 4;
 }
 // The four-wave kernel's workspace: the split's partial planes when they fit
 // the caller's workspace (ws_cap), else the scale-panel copy.
 void plan_wide_ws(MxRoute& r, const opus_gemm_scale_kargs& a, bool fp4, int cus, size_t ws_cap) {
     const int s = plan_wide_split(a, fp4, cus);
-    const size_t sb = wide_split_bytes(a, s);
+    const size_t sb = wide_split_bytes(a, fp4, s);
     r.wsplit = s > 1 && sb <= ws_cap ? s : 1;
     r.ws_bytes = std::max(scale_panel_bytes(a), r.wsplit > 1 ? sb : 0);
 }

@@ -114,13 +114,13 @@ def test_workspace_queries(qgemm):
         2048 + 4 * 128 * 7168 * 4
     assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(_kargs(qgemm, m=128, n=7168, k=16384))) == \
         2048 + 4 * 128 * 7168 * 4
-    # MXFP8 M > 256 on 96 256 x 256 tiles with 56 K-tiles: the four-wave
-    # kernel's K split in two (28-K-tile slices), two fp32 partial planes;
-    # MXFP4 keeps the scale-panel copy
+    # M > 256 on 96 256 x 256 tiles: the four-wave kernel's K split in two
+    # (MXFP8 56 K-tiles, MXFP4 64), whole scale panels per slice: counters,
+    # both operands' panel copies, then two fp32 partial planes
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=512, n=12288, k=7168))) == \
-        2048 + 2 * 512 * 12288 * 4
+        2048 + 512 * 224 + 12288 * 224 + 2 * 512 * 12288 * 4
     assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(_kargs(qgemm, m=512, n=12288, k=16384))) == \
-        2048 + 512 * 512 + 12288 * 512
+        2048 + 512 * 512 + 12288 * 512 + 2 * 512 * 12288 * 4
     # 136 tiles (> kCUs / 2): two workgroups per CU, 56 K-tiles / 16 -> 3 slices
     assert L.gemm_a8w8_mxfp8_workspace_bytes(ctypes.byref(_kargs(qgemm, m=1024, n=2112, k=7168))) == \
         2048 + 3 * 1024 * 2112 * 4
