@@ -1087,12 +1087,13 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.pl = plan_mx(a.m, a.n, kt, a.batch, bb, fp4);
             r.sp = plan_stream(a.m, a.n, a.k, a.batch, fp4);
             r.bp = plan_mx_burst(a.m, a.n, kt, a.batch, true);
-            if (r.pl.mid && a.m > 256 && have_ws) {
-                // M > 256 below 96 tiles: the four-wave kernel's K split
-                // where its slices fill >= 9/16 of the CUs (M = 512 / 768,
-                // N = 6144 / 8192, K = 12288 / 16384: 1.4-1.6x over the
+            if (r.pl.mid && a.m > 128 && have_ws) {
+                // M > 128 on a 128 x 128 plan: the four-wave kernel's K
+                // split where its slices fill >= 9/16 of the CUs (M = 512 /
+                // 768, N = 6144 / 8192, K = 12288 / 16384: 1.4-1.6x over the
                 // 128 x 128 kernel MXFP8, 1.15-1.35x MXFP4 at 144 workgroups;
-                // 96-128 workgroups within 8% either way)
+                // M = 160-256, N = 24576: MXFP8 1.35-1.42x, MXFP4 K = 16384
+                // 1.16-1.26x; 96-128 workgroups within 8% either way)
                 const int s = plan_wide_split(a, fp4, cus);
                 const long long tiles = (long long)ceil_div(a.m, 256) * ceil_div(a.n, 256);
                 if (s > 1 && 16 * tiles * s >= 9LL * cus && wide_split_bytes(a, fp4, s) <= ws_cap) r.pl = Plan{};

@@ -5,8 +5,9 @@ runs, and its outputs at 4096 sampled points against the oracle.
 * MX, M > 256: 256 x 256 tiles from 96 tiles with long K, their K split
   into batch-strided slices of whole scale panels summed by
   splitk_reduce_kernel while the tiles leave half of the CUs idle (also
-  with N % 4 != 0), and below 96 tiles where the slices fill 9/16 of the
-  CUs; the 128 x 128 kernel at exactly 128 tiles with short K;
+  with N % 4 != 0), and for M > 128 in place of a 128 x 128 plan where the
+  slices fill 9/16 of the CUs; the 128 x 128 kernel at exactly 128 tiles
+  with short K;
 * MX, M <= 64 from N = 12288: the 128 x 128 kernel (M = 33-64, and M = 17-32
   where the skinny plan spills into a second round), split band plans;
 * fp32 block scales: the 128 x 128 kernel with a deep split where one round
@@ -56,6 +57,7 @@ def _host(t):
     ("mx8", 600, 10002, 7168, "mx_scale_panels<pb16>+wide_gemm<fp8,MX,RAW,fp32,pb16>+splitk_reduce<bf16,x1,splitk2>"),
     ("mx8", 768, 6144, 12288, "mx_scale_panels<pb16>+wide_gemm<fp8,MX,RAW,fp32,pb16>+splitk_reduce<bf16,x4,splitk3>"),
     ("mx4", 768, 6144, 7168, "mid_gemm<fp4,MX"),
+    ("mx8", 192, 24576, 7168, "mx_scale_panels<pb16>+wide_gemm<fp8,MX,RAW,fp32,pb16>+splitk_reduce<bf16,x4,splitk2>"),
     ("mx8", 4096, 2048, 1536, "mid_gemm<fp8,MX"),
     ("mx4", 4096, 2048, 1536, "mid_gemm<fp4,MX"),
     ("mx4", 1024, 6144, 4096, "mx_scale_panels<pb32>+wide_gemm<fp4"),
