@@ -26,8 +26,8 @@ There is no CPU fallback: every wrapper raises if the library is missing or
 the tensors are not on a GPU.
 
 Skinny-M calls split K across workgroups and reduce the fp32 partials in the
-same launch; they need a workspace whose counter words start at zero (every
-call leaves them zero).  ``workspace=None`` uses one cached, zero-initialised
+same launch; the workspace's counter words are tagged with a per-launch
+epoch, so any initial contents work.  ``workspace=None`` uses one cached
 buffer per (device, stream); pass a tensor to supply your own, or
 ``workspace=False`` to run without split-K.
 """
@@ -195,8 +195,9 @@ def _workspace(query, args, workspace, dev, stream):
 
     ``query`` is the entry's *_workspace_bytes function; 0 means the call
     does not split K.  The cached buffer is zero-filled on allocation (on the
-    call's stream, so it is ordered before the launch) and every launch
-    leaves its counter words zero again."""
+    call's stream, so it is ordered before the launch); split launches count
+    their slices in epoch-tagged counter words, so no clearing is needed
+    between calls."""
     if workspace is False:
         return None, 0
     need = query(ctypes.byref(args))

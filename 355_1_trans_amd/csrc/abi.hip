@@ -189,9 +189,10 @@ bool dma_aligned(const opus_gemm_scale_kargs& a, bool scales_dword) {
 // tile (64, 32 or 16 columns) that gives at least kMinTiles workgroups.  When
 // even 16-column tiles give fewer than kSplitBelow, K is split across
 // workgroups -- only up to one round of workgroups (cus), keeping >= 16
-// K-tiles per slice and the fp32 partials below a quarter of B's bytes.  The
-// plan depends on the shape only, so the workspace query and the launch
-// always agree.
+// K-tiles per slice and the fp32 partials below a quarter of B's bytes.  This
+// plan depends on the shape only, so its workspace query and its launch
+// always agree (the MX entries' four-wave K split also depends on the
+// workspace bytes passed: see plan_wide_ws).
 constexpr int kMinTiles = 192;
 constexpr int kSplitBelow = 128;
 // Split-K counters sit in a fixed block at the start of the workspace (the
@@ -201,6 +202,16 @@ constexpr int kSplitBelow = 128;
 constexpr size_t kCounterBytes = 2048;
 constexpr long long kMaxCounters = kCounterBytes / sizeof(unsigned);
 static_assert(kSplitBelow <= kMaxCounters, "counter block too small");
+// Each split launch tags its counters with a fresh 24-bit epoch
+// (qg::split_arrive, common.hpp), so arrivals are counted from zero whatever
+// a counter word held before: a workspace needs no clearing, and one left
+// mid-count (an interrupted launch) or never zeroed cannot make a slice
+// take itself for the last.  Launches that share a workspace are
+// stream-ordered, so consecutive epochs never meet on one word.
+std::atomic<unsigned> g_epoch{0};
+unsigned next_epoch() { return (g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u) & 0xffffffu; }
+// the counter word's arrival count is 8 bits: no plan splits K more ways
+constexpr int kMaxSplit = 255;
 
 struct Plan {
     bool skinny = false;
@@ -229,7 +240,7 @@ void plan_decode(Plan& p, int m, int n, int k_tiles, int batch, long long b_byte
             (long long)m * n < (1LL << 29)) {    // partial offsets are 32-bit bytes
             split = std::min<long long>(cus / tiles, k_tiles / kDecodeMinKt);
             split = std::min<long long>(split, b_bytes / (16LL * m * n));
-            split = std::max<long long>(split, 1);
+            split = std::max<long long>(std::min<long long>(split, kMaxSplit), 1);
         }
         const int kt_per = ceil_div(k_tiles, (int)split);
         const int sk = ceil_div(k_tiles, kt_per);
@@ -298,6 +309,7 @@ Plan plan_gemm(int m, int n, int k_tiles, int batch, long long b_bytes, int cus,
     long long split = cus / base;
     split = std::min<long long>(split, k_tiles / 16);
     split = std::min<long long>(split, b_bytes / (16LL * m * n));
+    split = std::min<long long>(split, kMaxSplit);
     if (split <= 1) return p;
     p.kt_per_split = ceil_div(k_tiles, (int)split);
     p.splitk = ceil_div(k_tiles, p.kt_per_split);
@@ -392,6 +404,7 @@ hipError_t run_burst(const TileArgs& t, int batch, const qg::BurstPlan& pl, bool
     a.b_bytes = b_bytes;
     if (pl.splitk > 1) {    // the caller brought the workspace (checked before routing)
         a.counters = static_cast<unsigned*>(ws);
+        a.epoch = next_epoch();
         a.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
     }
     return qg::launch_burst(a, frag, pl.mb, pl.nb, pl.waves, batch, bf16, stream);
@@ -675,6 +688,7 @@ StreamPlan plan_stream(int m, int n, int k, int batch, bool fp4) {
         rows = (n + rounds * nblk_target - 1) / (rounds * nblk_target);
     }
     p.rows = (int)std::max<long long>(rows, 1);
+    if (p.splitk > kMaxSplit) return p;
     if (p.splitk > 1) {
         const long long blocks = (long long)ceil_div(n, p.rows) * batch;
         if (blocks > (long long)(kCounterBytes / sizeof(unsigned)) || (long long)m * n >= (1LL << 29)) return p;
@@ -716,7 +730,7 @@ BandPlan plan_band(int m, int n, int k_tiles, int batch) {
             const int sp = ceil_div(k_tiles, kps);
             if (sp != sk) continue;
             const long long wgs = (long long)bands * sp * batch;
-            if (wgs > cus) break;
+            if (wgs > cus || sp > kMaxSplit) break;
             if (sp > 1 && ((long long)bands * batch > kMaxCounters || (long long)m * n >= (1LL << 29))) break;
             if (wgs > best_wgs) {
                 best_wgs = wgs;
@@ -749,6 +763,7 @@ hipError_t run_band(const BandPlan& bp, const TileArgs& t, int batch, bool fp4, 
     b.bands = bp.bands;
     if (bp.splitk > 1) {    // the caller brought the workspace (checked before routing)
         b.counters = static_cast<unsigned*>(ws);
+        b.epoch = next_epoch();
         b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
     }
     return qg::launch_band(b, fp4, bp.mb, bp.cb, batch, bf16, stream);
@@ -767,6 +782,7 @@ bool run_stream(const TileArgs& t, int k, int batch, bool fp4, bool bf16, void* 
     if (pl.splitk > 1) {
         if (!ws || ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return false;
         s.counters = static_cast<unsigned*>(ws);
+        s.epoch = next_epoch();
         s.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
     }
     *st = qg::launch_stream(s, fp4, pl.wr, pl.mb, batch, bf16, stream);
@@ -839,9 +855,11 @@ hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int
 
 // The four-wave MX kernel split into s equal K slices (plan_wide_split):
 // slice z of the launch's batch reads A / B row bytes [z * slice, (z + 1) *
-// slice) and the row-major scales of those groups, and writes fp32 plane z
-// of the workspace (after the counter block); splitk_reduce_kernel then
-// sums the planes in slice order into C.
+// slice) and the scales of those groups -- whole panels of the panel-major
+// copy when the panels divide the slices (pb >= 16; the copy follows the
+// counter block and the planes follow the copy), else the row-major scales
+// (the planes follow the counter block) -- and writes fp32 plane z;
+// splitk_reduce_kernel then sums the planes in slice order into C.
 int wide_split_pb(const opus_gemm_scale_kargs& a, bool fp4, int s);
 
 hipError_t run_wide_split(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int s, bool bf16, void* ws,
@@ -931,6 +949,7 @@ hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bo
         d.t = t;
         d.ws = partials;
         d.counters = counters;
+        d.epoch = next_epoch();
         d.splitk = pl.splitk;
         d.kt_per_split = pl.kt_per_split;
         d.n_tiles = pl.n_tiles;
@@ -939,6 +958,7 @@ hipError_t run_skinny(SkinnyKind kind, const TileArgs& t, int batch, Plan pl, bo
     SkinnyArgs s{};
     s.t = t;
     s.counters = counters;
+    s.epoch = next_epoch();
     s.ws = partials;
     s.splitk = pl.splitk;
     s.kt_per_split = pl.kt_per_split;
@@ -989,6 +1009,7 @@ hipError_t run_bsf32(const BsfRoute& r, const TileArgs& t, int batch, bool frag,
                 a.tail_split = r.tp.split;
                 a.kt_per_split = r.tp.kps;
                 a.counters = static_cast<unsigned*>(ws);
+                a.epoch = next_epoch();
                 a.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
             }
             return qg::launch_bsf32(a, batch, bf16, frag, stream);
@@ -1203,6 +1224,7 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
             b.b_bytes = (long long)(a.n - 1) * a.stride_b + (fp4 ? a.k / 2 : a.k);
             if (r.bp.splitk > 1) {
                 b.counters = static_cast<unsigned*>(ws);
+                b.epoch = next_epoch();
                 b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
             }
             return qg::launch_burst_mx(b, fp4, r.bp.mb, r.bp.nb, r.bp.waves, a.batch, bf16, stream);
@@ -1531,9 +1553,15 @@ size_t gemm_a4w4_mxfp4_noalloc_max_workspace_bytes(void) { return kScratchBytes;
 
 // gemm_a4w4_mxfp4 with the library's static per-device scratch as its
 // workspace: no allocation and no caller buffer beyond A, B, scales and C.
+// The plan is the one gemm_a4w4_mxfp4 runs with the queried workspace (the
+// query is planned without a cap): a call whose query exceeds the scratch is
+// refused rather than planned onto another kernel, whose rounding could
+// differ.  With need <= kScratchBytes the routes below plan the same: the
+// only workspace-dependent choice, the four-wave K split, is taken exactly
+// when its bytes fit, and they are part of `need`.
 hipError_t gemm_a4w4_mxfp4_noalloc(const opus_gemm_scale_kargs* args, int out_dtype, hipStream_t stream) {
     qg::trace_reset();
-    const size_t need = mx_workspace(args, true, QGEMM_KID_AUTO, kScratchBytes);
+    const size_t need = mx_workspace(args, true, QGEMM_KID_AUTO);
     if (need > kScratchBytes) return hipErrorInvalidValue;    // beyond the static scratch
     Spans sp;
     hipError_t st = validate_mx(args, out_dtype, args ? args->k / 2 : 0, 256, &sp);
@@ -1997,3 +2025,4 @@ const char* qgemm_version(void) { return "qgemm gfx950 2"; }
 const char* qgemm_last_launch(void) { return qg::g_trace_str(); }
 
 }  // extern "C"
+

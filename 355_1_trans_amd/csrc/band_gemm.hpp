@@ -39,7 +39,8 @@ namespace qg {
 struct BandArgs {
     TileArgs t;            // operands, shapes, strides (tiles_* / group_m unused)
     float* ws;             // fp32 partials [splitk][batch][M][N] (splitk > 1)
-    unsigned* counters;    // [batch][bands] (splitk > 1), zero between launches
+    unsigned* counters;    // [batch][bands] (splitk > 1): epoch-tagged arrival counters
+    unsigned epoch;        // this launch's counter epoch (split_arrive)
     int splitk, kt_per_split, bands;
 };
 
@@ -305,8 +306,7 @@ __global__ __launch_bounds__(kBandWaves * 64, 1) void band_gemm_kernel(const Ban
     __syncthreads();
     unsigned* ctr = ba.counters + (long long)bz * ba.bands + bnd;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(ba.splitk - 1);
+        last_flag = split_arrive(ctr, ba.epoch, ba.splitk);
     __syncthreads();
     if (!last_flag) return;
     // the band's ROWS x COLS outputs, 4 per thread and element: E elements

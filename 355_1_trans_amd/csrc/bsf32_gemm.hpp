@@ -63,7 +63,8 @@ namespace qg {
 struct Bsf32Args {
     TileArgs t;
     float* ws;            // tail_split > 1: fp32 partial images [tail][tail_split][256 * 256]
-    unsigned* counters;   // tail_split > 1: one per tail tile, zero between launches
+    unsigned* counters;   // tail_split > 1: one per tail tile, epoch-tagged arrival counters
+    unsigned epoch;       // this launch's counter epoch (split_arrive)
     int dp_tiles;         // batch x tiles run whole (the rest is the tail)
     int tail_split;       // K slices per tail tile (1: no tail split)
     int kt_per_split;     // K-tiles per slice
@@ -399,8 +400,7 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const Bsf32Args ba) 
         wait_vmcnt<0>();
         __syncthreads();
         if (tid == 0)
-            last_flag = __hip_atomic_fetch_add(ba.counters + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                        (unsigned)(S - 1);
+            last_flag = split_arrive(ba.counters + r, ba.epoch, S);
         __syncthreads();
         if (!last_flag) return;
         // thread tid sums 4 consecutive columns of rows tid / 64 + 8u

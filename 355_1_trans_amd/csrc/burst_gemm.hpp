@@ -51,7 +51,8 @@ namespace qg {
 struct BurstArgs {
     TileArgs t;           // operands, shapes, strides (tiles_* / group_m unused)
     float* ws;            // fp32 partials [splitk][batch][M][N] (splitk > 1)
-    unsigned* counters;   // [batch][n_tiles], zero between launches
+    unsigned* counters;   // [batch][n_tiles]: epoch-tagged arrival counters
+    unsigned epoch;       // this launch's counter epoch (split_arrive)
     int splitk, kt_per_split, n_tiles;
     long long b_bytes;    // bytes of B per batch (loads past it read zeros)
 };
@@ -452,8 +453,7 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
     __syncthreads();
     unsigned* ctr = bp.counters + (long long)bz * bp.n_tiles + nt;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(bp.splitk - 1);
+        last_flag = split_arrive(ctr, bp.epoch, bp.splitk);
     __syncthreads();
     if (!last_flag) return;
     const float* ws0 = bp.ws + (long long)bz * plane;

@@ -85,6 +85,35 @@ __device__ __forceinline__ float load_partial1(__amdgpu_buffer_rsrc_t r, int ele
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, elem * 4, 0, kCoherent));
 }
 
+// Split-K arrival counter of one output tile, tagged with the launch's
+// epoch: bits 8..31 hold the epoch (a 24-bit number the host takes from a
+// process-wide sequence, a new one per launch), bits 0..7 the slices of
+// that epoch that have arrived.  A word carrying another epoch -- zero, a
+// completed or interrupted earlier launch, or whatever a never-cleared
+// workspace holds -- counts as zero arrivals, so the workspace needs no
+// clearing between launches and a stale word cannot make a slice
+// mistake itself for the last one.  (Only a word that already holds this
+// very epoch, 2^-24 for arbitrary bytes, would be miscounted.)
+// Fast path: one relaxed fetch_add, which lands on the tagged word for
+// every slice after the first.  A slice whose add found a word of another
+// epoch claims the word with a compare-and-swap (to this epoch, one
+// arrival) or, when another slice claimed it first, counts itself into the
+// claimed word; every failed swap means another slice's swap succeeded, so
+// the loop ends within splitk rounds.  Called by one lane; true for the
+// slice that completes the count.
+__device__ __forceinline__ bool split_arrive(unsigned* ctr, unsigned epoch, int splitk) {
+    const unsigned tag = epoch << 8;
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old & ~0xffu) == tag) return (int)(old & 0xffu) + 1 == splitk;
+    unsigned expect = old + 1u;    // the word as this slice's add left it
+    for (;;) {
+        const unsigned want = (expect & ~0xffu) == tag ? expect + 1u : tag | 1u;
+        if (__hip_atomic_compare_exchange_strong(ctr, &expect, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+            return (int)(want & 0xffu) == splitk;
+    }
+}
+
 // fp32 -> bf16 with round-to-nearest-even (the rounding the reference
 // validates against, SNAP host.cc:185-193): v_cvt_pk_bf16_f32 converts two
 // values per instruction in hardware.

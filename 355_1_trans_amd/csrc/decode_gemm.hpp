@@ -39,7 +39,8 @@ namespace qg {
 struct DecodeArgs {
     TileArgs t;           // operands, shapes, strides (tiles_* / group_m unused)
     float* ws;            // fp32 partials [splitk][batch][M][N] (splitk > 1)
-    unsigned* counters;   // [batch][n_tiles], zero between launches
+    unsigned* counters;   // [batch][n_tiles]: epoch-tagged arrival counters
+    unsigned epoch;       // this launch's counter epoch (split_arrive)
     int splitk, kt_per_split, n_tiles;
 };
 
@@ -318,8 +319,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
     __syncthreads();
     unsigned* ctr = dp.counters + (long long)bz * dp.n_tiles + nt;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(dp.splitk - 1);
+        last_flag = split_arrive(ctr, dp.epoch, dp.splitk);
     __syncthreads();
     if (!last_flag) return;
     const float* ws0 = dp.ws + (long long)bz * plane;

@@ -60,7 +60,8 @@ constexpr int kSkinnyWaves = 8;
 struct SkinnyArgs {
     TileArgs t;              // operands, shapes, strides (tiles_* / group_m unused)
     float* ws;               // fp32 partials [splitk][batch][M][N] (splitk > 1)
-    unsigned* counters;      // [batch][m_tiles][n_tiles], zero between launches
+    unsigned* counters;      // [batch][m_tiles][n_tiles]: epoch-tagged arrival counters
+    unsigned epoch;          // this launch's counter epoch (split_arrive)
     int splitk, kt_per_split, n_tiles, m_tiles;
     int scale_panel;         // MX: per-wave scale panels (skinny_scale_panel_ok)
 };
@@ -497,8 +498,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     __syncthreads();
     unsigned* ctr = sp.counters + ((long long)bz * sp.m_tiles + mt) * sp.n_tiles + nt;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(sp.splitk - 1);
+        last_flag = split_arrive(ctr, sp.epoch, sp.splitk);
     __syncthreads();
     if (!last_flag) return;
     const float* ws0 = sp.ws + (long long)bz * plane;

@@ -71,7 +71,8 @@ struct StreamArgs {
     int splitk;           // K slices (grid.z)
     int seg_per_split;    // segments per slice (stream_seg_cap at most)
     float* ws;            // splitk > 1: fp32 partials [splitk][batch][M][N]
-    unsigned* counters;   // splitk > 1: one per (batch, row block), zero on entry and exit
+    unsigned* counters;   // splitk > 1: one per (batch, row block), epoch-tagged arrival counters
+    unsigned epoch;       // this launch's counter epoch (split_arrive)
 };
 
 constexpr int kStreamWaves = 8;
@@ -355,8 +356,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
     __syncthreads();
     unsigned* ctr = sa.counters + (long long)bz * gridDim.x + blockIdx.x;
     if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    (unsigned)(sa.splitk - 1);
+        last_flag = split_arrive(ctr, sa.epoch, sa.splitk);
     __syncthreads();
     if (!last_flag) return;
     for (int idx = tid; idx < MB * R; idx += kStreamWaves * 64) {

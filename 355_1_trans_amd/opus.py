@@ -142,8 +142,8 @@ def gemm_a8w8_bpreshuffle_opus(A, B, x_scale, w_scale, out_dtype=torch.bfloat16,
 def gemm_a8w8_mxfp8_opus(A, B, x_scale, w_scale, out=None):
     """MXFP8 GEMM: A [batch, M, K], B [batch, N, K] e4m3 (2-D accepted);
     x_scale [batch, M, K/32], w_scale [batch, N, K/32] E8M0 bytes; fp32
-    output Y [batch, M, N] (``out`` reused when given)."""
-    dev = _require_gpu(A, B, x_scale, w_scale)
+    output Y [batch, M, N] (``out`` reused when given: [batch, M, N], or
+    [M, N] when batch is 1).  Shapes are checked before the device."""
     A3, squeeze = _batched(A, "A", 3)
     B3, _ = _batched(B, "B", 3)
     batch, m, k = A3.shape
@@ -157,10 +157,14 @@ def gemm_a8w8_mxfp8_opus(A, B, x_scale, w_scale, out=None):
     for t in (A3, B3, xs, wsc):
         if not t.is_contiguous():
             raise ValueError("A, B and the scales must be contiguous")
+    if out is not None:
+        # a 2-D out holds one batch entry only: the kernel writes batch * M * N values
+        shapes = ((batch, m, n), (m, n)) if batch == 1 else ((batch, m, n),)
+        if tuple(out.shape) not in shapes or out.dtype != torch.float32 or not out.is_contiguous():
+            raise ValueError("out must be a contiguous fp32 [batch, M, N] tensor ([M, N] only when batch is 1)")
+    dev = _require_gpu(A, B, x_scale, w_scale) if out is None else _require_gpu(A, B, x_scale, w_scale, out)
     if out is None:
         out = torch.empty((batch, m, n), dtype=torch.float32, device=dev)
-    elif tuple(out.shape) not in ((batch, m, n), (m, n)) or out.dtype != torch.float32 or not out.is_contiguous():
-        raise ValueError("out must be a contiguous fp32 [batch, M, N] tensor")
     args = Kargs(A3.data_ptr(), B3.data_ptr(), out.data_ptr(), m, n, k, batch, k, k, n, m * k, n * k, m * n,
                  xs.data_ptr(), wsc.data_ptr(), kg, kg, m * kg, n * kg)
     L = lib()

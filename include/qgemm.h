@@ -142,9 +142,13 @@ size_t gemm_a8w8_blockscale_layout_workspace_bytes(const opus_gemm_scale_kargs* 
  * Any M >= 1, N >= 1 (tails are masked), K a multiple of 128.
  * `workspace` (fp32 split-K partials) may be NULL; then no split-K is used.
  * Split-K workspace (every entry with a *_workspace_bytes query): at least
- * the queried bytes, 256-byte aligned; its first 2048 bytes are counter
- * words that must be zero before the first call, and every call leaves them
- * zero.  Calls that share a workspace must be ordered (same stream). */
+ * the queried bytes, 256-byte aligned, any contents; its first 2048 bytes
+ * are arrival counters that each launch tags with a fresh epoch, so they
+ * need no clearing (a completed call leaves them zero).  Calls that share a
+ * workspace must be ordered (same stream).  The MX entries' plan, and so
+ * the rounding of their last bits, also depends on workspace_bytes: the
+ * four-wave kernel's K split is taken only when its planes fit (a workspace
+ * of at least the scale-panel bytes but less than the query runs unsplit). */
 hipError_t gemm_a8w8_blockscale_bpreshuffle(const opus_gemm_kargs* args, int out_dtype, void* workspace,
                                      size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_workspace_bytes(const opus_gemm_kargs* args);

@@ -311,3 +311,38 @@ def test_extreme_dimensions_do_not_overflow(qgemm):
     assert L.qgemm_e8m0_shuffle_bytes(big, 8) == (big + 31) // 32 * 32 * 8
     assert L.qgemm_e8m0_shuffle_bytes(32, big) == 32 * ((big + 7) // 8 * 8)
     assert L.qgemm_ldsbypass_b_bytes(big, 128) == (big + 15) // 16 * 16 * 128
+
+
+def test_mxfp8_opus_rejects_2d_out_for_batches(qgemm):
+    """A 2-D ``out`` holds one batch entry: with batch > 1 the kernel would
+    write batch * M * N values into it, so the wrapper refuses it before any
+    device work (CPU tensors: the shape check comes first)."""
+    from importlib import import_module
+    opus = import_module("355_1_trans_amd.opus")
+    b, m, n, k = 2, 16, 32, 128
+    A = torch.zeros(b, m, k, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    B = torch.zeros(b, n, k, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    sa, sb = torch.zeros(b, m, k // 32, dtype=torch.uint8), torch.zeros(b, n, k // 32, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="only when batch is 1"):
+        opus.gemm_a8w8_mxfp8_opus(A, B, sa, sb, out=torch.empty(m, n, dtype=torch.float32))
+    # batch 1 may pass [M, N]; it gets as far as the device check
+    with pytest.raises(ValueError, match="GPU"):
+        opus.gemm_a8w8_mxfp8_opus(A[0], B[0], sa[0], sb[0], out=torch.empty(m, n, dtype=torch.float32))
+
+
+def test_noalloc_plans_as_the_query(qgemm):
+    """gemm_a4w4_mxfp4_noalloc runs exactly the plan gemm_a4w4_mxfp4 runs with
+    the queried workspace: it is refused wherever that query exceeds the
+    static scratch -- here a four-wave K split whose partial planes (55 MB)
+    do not fit 32 MiB -- instead of silently planning another kernel; a split
+    whose planes fit is accepted (stops at the device check without a GPU)."""
+    L = qgemm.lib()
+    cap = L.gemm_a4w4_mxfp4_noalloc_max_workspace_bytes()
+    big = _far_kargs(qgemm, 768, 8192, 16384, fp4=True)
+    assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(big)) > cap
+    assert L.gemm_a4w4_mxfp4_noalloc(ctypes.byref(big), 1, None) == HIP_INVALID_VALUE
+    fit = _far_kargs(qgemm, 129, 18432, 16384, fp4=True)
+    need = L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(fit))
+    assert 2 * 129 * 18432 * 4 < need <= cap                # two fp32 planes + panels
+    if not torch.cuda.is_available():
+        assert L.gemm_a4w4_mxfp4_noalloc(ctypes.byref(fit), 1, None) != HIP_INVALID_VALUE

@@ -102,3 +102,36 @@ def test_bs_plan_route(qgemm, gpu, m, n, k, expect):
     rows, cols = _points(m, n, m + n + k)
     ref = O.gemm_bs_fp32_points(_host(A), _host(B), _host(SA), _host(SB), rows, cols)
     assert_close(ref, y.float().cpu().numpy()[rows, cols], f"bs {m}x{n}x{k} ({trace})")
+
+
+def _panel_bytes(m, n, k):
+    r256 = lambda b: (b + 255) // 256 * 256
+    return 2048 + r256(m * (k // 32)) + r256(n * (k // 32))
+
+
+@pytest.mark.parametrize("case", ["rowmajor_bf16", "rowmajor_fp32", "panels_only_ws"])
+def test_mx8_wide_split_variants(qgemm, gpu, case):
+    """The four-wave kernel's K split on row-major scales (K % 512 != 0, so
+    no panel copy: 50 K-tiles in two 25-K-tile slices, pb4), with bf16 and
+    fp32 output, and a caller workspace of exactly the scale-panel bytes,
+    where the split's planes do not fit and the kernel runs unsplit."""
+    m, n, k = (512, 12288, 6400) if case.startswith("rowmajor") else (512, 12288, 7168)
+    dtype = torch.float32 if case == "rowmajor_fp32" else torch.bfloat16
+    A, SA = qgemm.quant_mxfp8(_randn((m, k), m + k, gpu))
+    B, SB = qgemm.quant_mxfp8(_randn((n, k), m + k + 1, gpu))
+    ws = None
+    if case == "panels_only_ws":
+        ws = torch.zeros(_panel_bytes(m, n, k), dtype=torch.uint8, device=gpu)
+    y = qgemm.gemm_a8w8_mxfp8(A, B, SA, SB, dtype=dtype, workspace=ws)
+    trace = qgemm.last_launch()
+    torch.cuda.synchronize()
+    expect = {
+        "rowmajor_bf16": "wide_gemm<fp8,MX,RAW,fp32,pb4>+splitk_reduce<bf16,x4,splitk2>",
+        "rowmajor_fp32": "wide_gemm<fp8,MX,RAW,fp32,pb4>+splitk_reduce<fp32,x4,splitk2>",
+        "panels_only_ws": "mx_scale_panels<pb16>+wide_gemm<fp8,MX,RAW,bf16,pb16>",
+    }[case]
+    if _cus(gpu) == 256:
+        assert trace == expect, trace
+    rows, cols = _points(m, n, m + n + k)
+    ref = O.gemm_mx8_points(_host(A), _host(B), _host(SA), _host(SB), rows, cols)
+    assert_close(ref, y.float().cpu().numpy()[rows, cols], f"mx8 {m}x{n}x{k} {case} ({trace})")

@@ -63,3 +63,41 @@ def test_noalloc_rejects_beyond_the_scratch(qgemm, gpu):
                        kg, kg, m * kg, n * kg)
     assert L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(args)) > 32 << 20
     assert L.gemm_a4w4_mxfp4_noalloc(ctypes.byref(args), 1, None) == 1
+
+
+def test_noalloc_split_within_the_scratch(qgemm, gpu):
+    """A four-wave K split whose planes fit the 32 MiB scratch (M = 129:
+    two 129 x 18432 fp32 planes + the scale panels): the allocation-free
+    entry runs the same split as the workspace entry with the queried
+    bytes, bit for bit, and matches the oracle at 4096 sampled points."""
+    L = qgemm.lib()
+    m, n, k = 129, 18432, 16384
+    g = torch.Generator(device=gpu)
+    g.manual_seed(129)
+    A, SA = qgemm.quant_mxfp4(torch.randn((m, k), generator=g, device=gpu))
+    B, SB = qgemm.quant_mxfp4(torch.randn((n, k), generator=g, device=gpu))
+    stream = torch.cuda.current_stream()
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    outs, traces = [], []
+    for noalloc in (True, False):
+        C = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        args = _kargs(qgemm, A, B, C, SA, SB, m, n, k)
+        need = L.gemm_a4w4_mxfp4_workspace_bytes(ctypes.byref(args))
+        assert 2 * m * n * 4 < need <= 32 << 20, need
+        if noalloc:
+            st = L.gemm_a4w4_mxfp4_noalloc(ctypes.byref(args), qgemm.OUT_BF16, sptr)
+        else:
+            ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+            st = L.gemm_a4w4_mxfp4(ctypes.byref(args), qgemm.OUT_BF16, ws.data_ptr(), need, sptr)
+        assert st == 0
+        traces.append(qgemm.last_launch())
+        torch.cuda.synchronize()
+        outs.append(C)
+    assert traces[0] == traces[1] and "splitk_reduce" in traces[0], traces
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    rng = np.random.default_rng(5)
+    rows = rng.integers(0, m, 4096).astype(np.int32)
+    cols = rng.integers(0, n, 4096).astype(np.int32)
+    host = lambda t: t.contiguous().view(torch.uint8).cpu().numpy()
+    ref = O.gemm_mx4_points(host(A), host(B), host(SA), host(SB), rows, cols)
+    assert_close(ref, outs[0].float().cpu().numpy()[rows, cols], f"noalloc split {m}x{n}x{k} ({traces[0]})")
