@@ -137,6 +137,17 @@ EXPORTS = {
     "qgemm_shuffle_weight_16x16_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
     "qgemm_pack_b_ldsbypass_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
     "qgemm_e8m0_shuffle_device": (ctypes.c_int, [_V, _V, _I, _I, _I, _V]),
+    "gemm_a8w8_blockscale_bpreshuffle_grouped": (ctypes.c_int, [ctypes.POINTER(Kargs), _I, _I, _I, _V, ctypes.c_size_t,
+                                                                _V]),
+    "gemm_a8w8_blockscale_bpreshuffle_grouped_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), _I]),
+    "gemm_a8w8_blockscale_ldsbypass_grouped": (ctypes.c_int, [ctypes.POINTER(LdsBypassKargs), _I, _I, _I, _V,
+                                                              ctypes.c_size_t, _V]),
+    "gemm_a8w8_blockscale_ldsbypass_grouped_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LdsBypassKargs), _I]),
+    "gemm_a8w8_mxfp8_grouped": (ctypes.c_int, [ctypes.POINTER(Kargs), _I, _I, _I, _V, ctypes.c_size_t, _V]),
+    "gemm_a8w8_mxfp8_grouped_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), _I]),
+    "gemm_a4w4_mxfp4_grouped": (ctypes.c_int, [ctypes.POINTER(Kargs), _I, _I, _I, _V, ctypes.c_size_t, _V]),
+    "gemm_a4w4_mxfp4_grouped_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), _I]),
+    "qgemm_reference_gemm": (ctypes.c_int, [_I, ctypes.POINTER(Kargs), _V]),
     "qgemm_version": (ctypes.c_char_p, []),
     "qgemm_last_launch": (ctypes.c_char_p, []),
 }
@@ -495,3 +506,127 @@ from .opus import (gemm_a8w8_bpreshuffle_opus, gemm_a8w8_mxfp8_opus, opus_gemm_m
                    opus_gemm_mxfp8_nt, opus_gemm_mxfp8_tn, opus_gemm_mxfp8_tt)
 from .quant import (e8m0_shuffle, quant_fp8_blockscale, quant_fp8_e8m0_blockscale,  # noqa: E402,F401
                     quant_mxfp4, quant_mxfp8)
+
+
+GROUP_MAX = 16
+_GROUPED = {
+    "bpreshuffle": ("gemm_a8w8_blockscale_bpreshuffle_grouped", Kargs),
+    "ldsbypass": ("gemm_a8w8_blockscale_ldsbypass_grouped", LdsBypassKargs),
+    "mxfp8": ("gemm_a8w8_mxfp8_grouped", Kargs),
+    "mxfp4": ("gemm_a4w4_mxfp4_grouped", Kargs),
+}
+
+
+def _group_kargs(kind, A, B, A_scale, B_scale, out, n):
+    """kargs of one grouped problem (batch 1, M <= 64, contiguous operands)."""
+    m = A.shape[0]
+    if kind in ("mxfp8", "mxfp4"):
+        fp4 = kind == "mxfp4"
+        kb = A.shape[1]
+        k = 2 * kb if fp4 else kb
+        if B.dim() != 2 or B.shape[1] != kb or A_scale.shape != (m, k // 32) or B_scale.shape != (B.shape[0], k // 32):
+            raise ValueError(f"{kind}: A [M,{'K/2' if fp4 else 'K'}], B [N,...], scales [rows, K/32]")
+        n = B.shape[0]
+        return Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
+                     A_scale.data_ptr(), B_scale.data_ptr(), k // 32, k // 32, m * (k // 32), n * (k // 32))
+    k = A.shape[1]
+    kg = k // 128
+    if kind == "bpreshuffle":
+        if B.dim() != 3 or B.shape[0] * 128 != k or B.shape[2] != 128:
+            raise ValueError("bpreshuffle: B must be the K-panel [K/128, N, 128]")
+        n = B.shape[1]
+    elif n is None:
+        raise ValueError("ldsbypass: give N for each B'' (problems as (A, B'', A_scale, B_scale, N))")
+    if A_scale.shape != (m, kg) or B_scale.shape != ((n + 127) // 128, kg) or not B_scale.is_contiguous():
+        raise ValueError("block scales: A_scale fp32 [M,K/128], B_scale fp32 [ceil(N/128),K/128]")
+    sfa = _sfa_stride(A_scale, m)
+    if kind == "bpreshuffle":
+        return Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, k, 128, n, m * k, n * k, m * n,
+                     A_scale.data_ptr(), B_scale.data_ptr(), sfa, kg, m * kg, B_scale.shape[0] * kg)
+    return LdsBypassKargs(A.data_ptr(), None, B.data_ptr(), out.data_ptr(), m, n, k, 1, k, 128, n, m * k, 0, m * n,
+                          A_scale.data_ptr(), B_scale.data_ptr(), sfa, kg, m * kg, B_scale.shape[0] * kg, B.numel())
+
+
+def gemm_grouped(kind, problems, dtype=torch.bfloat16, outs=None, grid_blocks=0, workspace=None):
+    """Several decode GEMMs (M <= 64 each, up to GROUP_MAX) in one launch.
+
+    ``kind``: "bpreshuffle" (problems (A, B_kpanel, A_scale, B_scale), fp32
+    block scales), "ldsbypass" ((A, B'', A_scale, B_scale, N)), "mxfp8" or
+    "mxfp4" ((A, B, A_scale, B_scale), row-major, E8M0 per 32).  Each problem
+    has its own N, K, M, operands and output; one grid walks all their
+    (tile, K slice) items.  ``grid_blocks`` > 0 runs a persistent grid of
+    that many workgroups.  Returns the list of outputs [M, N]."""
+    if kind not in _GROUPED:
+        raise ValueError(f"kind must be one of {sorted(_GROUPED)}")
+    if not 1 <= len(problems) <= GROUP_MAX:
+        raise ValueError(f"1 to {GROUP_MAX} problems")
+    name, ktype = _GROUPED[kind]
+    flat = [t for pr in problems for t in pr[:4]]
+    dev = _require_gpu(*flat)
+    for pr in problems:
+        if not all(t.is_contiguous() for t in (pr[0], pr[1], pr[3])):
+            raise ValueError("A, B and B_scale must be contiguous")
+        if kind in ("mxfp8", "mxfp4") and not pr[2].is_contiguous():
+            raise ValueError("E8M0 scales must be contiguous")
+    if outs is None:
+        outs = []
+        for pr in problems:
+            n = pr[1].shape[1] if kind == "bpreshuffle" else (pr[4] if kind == "ldsbypass" else pr[1].shape[0])
+            outs.append(torch.empty((pr[0].shape[0], n), dtype=dtype, device=dev))
+    arr = (ktype * len(problems))(*[_group_kargs(kind, pr[0], pr[1], pr[2], pr[3], o, pr[4] if len(pr) > 4 else None)
+                                    for pr, o in zip(problems, outs)])
+    L = lib()
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        if workspace is False:
+            wp, wb = None, 0
+        elif workspace is not None:
+            wp, wb = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        else:
+            need = getattr(L, name + "_workspace_bytes")(arr, len(problems))
+            buf = _WORKSPACES.get(("grouped", dev.index, s.cuda_stream))
+            if need and (buf is None or buf.numel() < need):
+                buf = torch.zeros((need + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+                _WORKSPACES[("grouped", dev.index, s.cuda_stream)] = buf
+            wp, wb = (buf.data_ptr(), buf.numel()) if need else (None, 0)
+        st = getattr(L, name)(arr, len(problems), _out_code(dtype), int(grid_blocks), wp, wb,
+                              ctypes.c_void_p(s.cuda_stream))
+        _record(s, *flat, *outs)
+    _check(st, name)
+    return outs
+
+
+_REF_FAMILY = {"bs_fp32": 0, "bs_e8m0": 1, "mxfp8": 2, "mxfp4": 3}
+
+
+def reference_gemm(kind, A, B, A_scale, B_scale):
+    """The whole-output GPU reference GEMM (qgemm_reference_gemm): fp32
+    [M, N] from fp64 sums of decoded, scaled products.  Row-major codes A
+    [M, K] (fp4: [M, K/2]) and B [N, K]; scales as the family's entry takes
+    them -- "bs_fp32": fp32 [M, K/128] (row-major, or the strides-(1, M) view
+    of [K/128][M]) and [ceil(N/128), K/128]; "bs_e8m0": the same in E8M0
+    bytes; "mxfp8" / "mxfp4": E8M0 [rows, K/32]."""
+    if kind not in _REF_FAMILY:
+        raise ValueError(f"kind must be one of {sorted(_REF_FAMILY)}")
+    dev = _require_gpu(A, B, A_scale, B_scale)
+    fp4 = kind == "mxfp4"
+    m, kb = A.shape
+    n = B.shape[0]
+    k = 2 * kb if fp4 else kb
+    if B.shape[1] != kb or not (A.is_contiguous() and B.is_contiguous() and B_scale.is_contiguous()):
+        raise ValueError("A [M, K] and B [N, K] contiguous codes, B_scale contiguous")
+    if kind in ("mxfp8", "mxfp4"):
+        if not A_scale.is_contiguous():
+            raise ValueError("A_scale must be contiguous")
+        sfa, sfb = A_scale.stride(0), B_scale.stride(0)
+    else:
+        sfa, sfb = _sfa_stride(A_scale, m), B_scale.stride(0)
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    args = Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, kb, kb, n, 0, 0, 0,
+                 A_scale.data_ptr(), B_scale.data_ptr(), sfa, sfb, 0, 0)
+    with torch.cuda.device(dev):
+        s = _stream(dev)
+        st = lib().qgemm_reference_gemm(_REF_FAMILY[kind], ctypes.byref(args), ctypes.c_void_p(s.cuda_stream))
+        _record(s, A, B, A_scale, B_scale, out)
+    _check(st, "qgemm_reference_gemm")
+    return out

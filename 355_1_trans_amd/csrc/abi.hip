@@ -2026,3 +2026,395 @@ const char* qgemm_last_launch(void) { return qg::g_trace_str(); }
 
 }  // extern "C"
 
+// ---------------------------------------------------------------- grouped decode GEMMs
+// Several decode GEMMs -- M <= 64 each, batch 1, each with its own N, K,
+// operands, scales and output -- in one launch of the burst kernel's grouped
+// form (burst_gemm.hpp, BurstGroup): one grid walks every problem's (tile,
+// K slice) items, each problem with the fused last-slice split-K reduce of
+// its own counters and partial planes.  This is the persistent scheduling
+// across mixed decode batches that the reference plans next to its fused
+// split-K reduce (R/opus_gemm_splitk_and_interface_refactor.md:41-45) and
+// the persistent tile walk of MX4/MULTITILE_DESIGN.md:78: a narrow-N decode
+// GEMM alone fills a fraction of the CUs and pays a launch of its own
+// (configs[2] M <= 64 at N = 2112-7168 run at 0.13-0.45 of HBM one by one).
+namespace {
+
+struct GroupProblem {
+    int m, n, kt;    // kt: K-tiles of 128 bytes of K
+};
+
+struct GroupPlan {
+    bool ok = false;
+    int mb = 1, nb = 2, waves = 8, items = 0;
+    int splitk[qg::kGroupMax], kt_per[qg::kGroupMax], n_tiles[qg::kGroupMax];
+    size_t ctr_off[qg::kGroupMax], part_off[qg::kGroupMax];
+    size_t ws_bytes = 0;
+    double cost_us = 1e30;
+};
+
+// The burst kernel's cost model (burst_gemm.hpp: ~2.5 us per launch, ~25 ns
+// per KB one CU streams, ~3.4 us for a K split's coherent round trips) over
+// the whole item list, with the HBM stream as a floor: the longest item
+// bounds a launch whose items all run at once, the bytes per CU one whose
+// items take several rounds.
+constexpr double kGroupHbmBytesPerUs = 6.0e6;
+
+double group_cost(const GroupProblem* p, int count, int nb, const int* splitk, const int* kt_per, int cus) {
+    double max_kb = 0, sum_kb = 0, bytes = 0;
+    bool split = false;
+    for (int j = 0; j < count; ++j) {
+        const double tiles = ceil_div(p[j].n, 16 * nb);
+        const double kb = (16.0 * nb + p[j].m) * kt_per[j] * 128 / 1024.0;
+        max_kb = std::max(max_kb, kb);
+        sum_kb += kb * tiles * splitk[j];
+        bytes += ((double)p[j].n + p[j].m) * p[j].kt * 128;
+        split = split || splitk[j] > 1;
+    }
+    return 2.5 + std::max(0.025 * std::max(max_kb, sum_kb / cus), bytes / kGroupHbmBytesPerUs) + (split ? 3.4 : 0.0);
+}
+
+// The plan of a grouped launch: one tile shape, wave count and K-tiles per
+// wave for every problem (the kernel is one instantiation), per problem the
+// smallest K split the registers allow, then -- with a workspace -- further
+// splits of the problem whose items stream the most bytes while the cost
+// model drops by at least 1%.  Workspace: the split problems' counter words
+// (one per tile), then each split problem's fp32 partial planes.
+GroupPlan plan_grouped(const GroupProblem* p, int count, bool mx, bool frag, int cus, bool allow_split) {
+    GroupPlan best;
+    if (count < 1 || count > qg::kGroupMax) return best;
+    int mmax = 0;
+    for (int j = 0; j < count; ++j) {
+        if (p[j].m < 1 || p[j].m > 64 || p[j].n < 1 || p[j].kt < 1) return best;
+        mmax = std::max(mmax, p[j].m);
+    }
+    const int mb = mmax <= 16 ? 1 : (mmax <= 32 ? 2 : 4);
+    // 16 waves first: on a tie (the same items and bytes) the plan that puts
+    // twice the waves' loads in flight per item wins -- configs[2]'s decode
+    // trio, fp32 block scales, M = 1 / 16: 18.3 / 21.1 us with 8 waves x 8
+    // K-tiles, 17.5 / 19.2 us with 16 x 4
+    for (int nb : {2, 1})
+        for (int waves : {16, 8}) {
+            const int kmax = qg::burst_max_kpw(mb, nb, waves, mx);
+            if (kmax == 0 || qg::burst_lds_bytes(mb, nb, waves, !frag) > qg::kBurstLdsMax) continue;
+            const int cap = waves * kmax;
+            GroupPlan c;
+            c.mb = mb;
+            c.nb = nb;
+            c.waves = waves;
+            bool ok = true;
+            auto can_split = [&](int j) { return allow_split && (long long)p[j].m * p[j].n < (1LL << 29); };
+            for (int j = 0; j < count && ok; ++j) {
+                int s = ceil_div(p[j].kt, cap);
+                const int kp = ceil_div(p[j].kt, s);
+                s = ceil_div(p[j].kt, kp);
+                if (s > 1 && (!can_split(j) || s > kMaxSplit)) ok = false;
+                c.splitk[j] = s;
+                c.kt_per[j] = kp;
+                c.n_tiles[j] = ceil_div(p[j].n, 16 * nb);
+            }
+            if (!ok) continue;
+            c.cost_us = group_cost(p, count, nb, c.splitk, c.kt_per, cus);
+            for (int step = 0; step < 64; ++step) {
+                int jb = -1;
+                double kb_max = 0;
+                for (int j = 0; j < count; ++j) {
+                    const double kb = (16.0 * nb + p[j].m) * c.kt_per[j];
+                    if (can_split(j) && c.kt_per[j] > 1 && c.splitk[j] < kMaxSplit && kb > kb_max) {
+                        kb_max = kb;
+                        jb = j;
+                    }
+                }
+                if (jb < 0) break;
+                const int s0 = c.splitk[jb], k0 = c.kt_per[jb];
+                const int kp = ceil_div(p[jb].kt, s0 + 1);
+                c.kt_per[jb] = kp;
+                c.splitk[jb] = ceil_div(p[jb].kt, kp);
+                const double cost = group_cost(p, count, nb, c.splitk, c.kt_per, cus);
+                if (cost < 0.99 * c.cost_us) {
+                    c.cost_us = cost;
+                } else {
+                    c.splitk[jb] = s0;
+                    c.kt_per[jb] = k0;
+                    break;
+                }
+            }
+            if (c.cost_us < best.cost_us) {
+                c.ok = true;
+                best = c;
+            }
+        }
+    if (!best.ok) return best;
+    size_t ctr = 0, part = 0;
+    best.items = 0;
+    for (int j = 0; j < count; ++j) {
+        best.items += best.n_tiles[j] * best.splitk[j];
+        best.ctr_off[j] = ctr;
+        if (best.splitk[j] > 1) ctr += (size_t)best.n_tiles[j] * sizeof(unsigned);
+    }
+    ctr = round256(ctr);
+    for (int j = 0; j < count; ++j) {
+        best.part_off[j] = ctr + part;
+        if (best.splitk[j] > 1) part += round256((size_t)best.splitk[j] * p[j].m * p[j].n * sizeof(float));
+    }
+    best.ws_bytes = part ? ctr + part : 0;
+    return best;
+}
+
+enum class GroupFam { BS_KPANEL, BS_FRAG, MX8, MX4 };
+
+// A grouped call's problems, validated one by one as their single-problem
+// entries do (batch 1, M <= 64 added), as kernel tiles.
+struct GroupCall {
+    int count = 0;
+    qg::TileArgs t[qg::kGroupMax];
+    long long b_bytes[qg::kGroupMax];
+    GroupProblem shape[qg::kGroupMax];
+    const void* span_p[qg::kGroupMax * 6];
+    uint64_t span_b[qg::kGroupMax * 6];
+    int spans = 0;
+};
+
+hipError_t group_problem(GroupFam fam, const void* kargs, int j, int out_dtype, GroupCall* g) {
+    opus_gemm_scale_kargs a{};
+    const void* b_data = nullptr;
+    long long bb = 0;
+    Spans sp;
+    int sfa_sm = 0, sfa_sk = 0;
+    hipError_t st = hipSuccess;
+    if (fam == GroupFam::BS_FRAG) {
+        const auto& l = static_cast<const opus_gemm_ldsbypass_kargs*>(kargs)[j];
+        a = from_ldsbypass(l);
+        b_data = l.ptr_b_pp;
+        bb = a.n > 0 && a.k > 0 ? (long long)frag_bytes(a.n, a.k) : 0;
+    } else {
+        a = static_cast<const opus_gemm_scale_kargs*>(kargs)[j];
+        b_data = a.ptr_b;
+    }
+    if (a.batch != 1 || a.m < 1 || a.m > 64) return hipErrorInvalidValue;
+    const bool fp4 = fam == GroupFam::MX4;
+    const int kbytes = fp4 ? a.k / 2 : a.k;
+    if (fam == GroupFam::BS_KPANEL || fam == GroupFam::BS_FRAG) {
+        if (fam == GroupFam::BS_KPANEL) {
+            if (a.stride_b != 128) return hipErrorInvalidValue;    // K-panel B' (BPS host.cc:263)
+            bb = (long long)a.n * a.k;
+        }
+        st = validate_bsf32(a, b_data, bb, out_dtype, &sfa_sm, &sfa_sk, &sp);
+        if (st != hipSuccess) return st;
+        sp.add(b_data, (uint64_t)bb);
+        if (sp.overlap_any(sp.p[0], sp.bytes[0], sp.n - 1)) return hipErrorInvalidValue;
+    } else {
+        st = validate_mx(&a, out_dtype, kbytes, fp4 ? 256 : 128, &sp);
+        if (st != hipSuccess) return st;
+        bb = (long long)(a.n - 1) * a.stride_b + kbytes;
+    }
+    qg::TileArgs& t = g->t[j];
+    t = qg::TileArgs{};
+    fill_common(t, a, kbytes, out_dtype ? 2 : 4);
+    if (fam == GroupFam::BS_KPANEL || fam == GroupFam::BS_FRAG) {
+        t.sfa_sm = sfa_sm;
+        t.sfa_sk = sfa_sk;
+    } else {
+        t.sfa_sm = a.stride_sfa;
+    }
+    t.sfb_sn = a.stride_sfb;
+    g->b_bytes[j] = bb;
+    g->shape[j] = GroupProblem{a.m, a.n, kbytes / 128};
+    // C first: every problem's output is checked against every operand of the call
+    for (int i = 0; i < sp.n; ++i) {
+        g->span_p[g->spans] = sp.p[i];
+        g->span_b[g->spans++] = sp.bytes[i];
+    }
+    return hipSuccess;
+}
+
+hipError_t group_collect(GroupFam fam, const void* kargs, int count, int out_dtype, GroupCall* g,
+                         int* span_begin) {
+    if (!kargs || count < 1 || count > qg::kGroupMax || !flag01(out_dtype)) return hipErrorInvalidValue;
+    g->count = count;
+    for (int j = 0; j < count; ++j) {
+        span_begin[j] = g->spans;
+        const hipError_t st = group_problem(fam, kargs, j, out_dtype, g);
+        if (st != hipSuccess) return st;
+    }
+    span_begin[count] = g->spans;
+    // outputs may not overlap any other problem's operands or outputs
+    for (int j = 0; j < count; ++j) {
+        const void* c = g->span_p[span_begin[j]];
+        const uint64_t cb = g->span_b[span_begin[j]];
+        for (int i = 0; i < g->spans; ++i)
+            if ((i < span_begin[j] || i >= span_begin[j + 1]) && overlaps(c, cb, g->span_p[i], g->span_b[i]))
+                return hipErrorInvalidValue;
+    }
+    return hipSuccess;
+}
+
+GroupPlan group_plan(GroupFam fam, const GroupCall& g, bool allow_split) {
+    return plan_grouped(g.shape, g.count, fam == GroupFam::MX8 || fam == GroupFam::MX4, fam == GroupFam::BS_FRAG,
+                        device_cus(), allow_split);
+}
+
+hipError_t group_entry(GroupFam fam, const void* kargs, int count, int out_dtype, int grid_blocks, void* ws,
+                       size_t ws_bytes, hipStream_t stream) {
+    qg::trace_reset();
+    if (grid_blocks < 0) return hipErrorInvalidValue;
+    GroupCall g;
+    int span_begin[qg::kGroupMax + 1];
+    hipError_t st = group_collect(fam, kargs, count, out_dtype, &g, span_begin);
+    if (st != hipSuccess) return st;
+    const GroupPlan pl = group_plan(fam, g, ws != nullptr);
+    if (!pl.ok) return hipErrorInvalidValue;
+    if (ws && pl.ws_bytes) {
+        if (ws_bytes < pl.ws_bytes || !aligned(ws, 256)) return hipErrorInvalidValue;
+        for (int i = 0; i < g.spans; ++i)
+            if (overlaps(ws, pl.ws_bytes, g.span_p[i], g.span_b[i])) return hipErrorInvalidValue;
+    }
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    qg::BurstGroup bg{};
+    bg.count = count;
+    const unsigned epoch = next_epoch();
+    int item = 0;
+    for (int j = 0; j < count; ++j) {
+        qg::BurstArgs& b = bg.p[j];
+        b.t = g.t[j];
+        b.splitk = pl.splitk[j];
+        b.kt_per_split = pl.kt_per[j];
+        b.n_tiles = pl.n_tiles[j];
+        b.b_bytes = g.b_bytes[j];
+        b.epoch = epoch;
+        if (pl.splitk[j] > 1) {
+            b.counters = reinterpret_cast<unsigned*>(static_cast<uint8_t*>(ws) + pl.ctr_off[j]);
+            b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + pl.part_off[j]);
+        }
+        bg.item_begin[j] = item;
+        item += pl.n_tiles[j] * pl.splitk[j];
+    }
+    bg.item_begin[count] = item;
+    const int grid = grid_blocks > 0 ? std::min(grid_blocks, item) : item;
+    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
+    switch (fam) {
+        case GroupFam::BS_KPANEL:
+            return qg::launch_burst_grouped(bg, false, pl.mb, pl.nb, pl.waves, grid, bf16, stream);
+        case GroupFam::BS_FRAG:
+            return qg::launch_burst_grouped(bg, true, pl.mb, pl.nb, pl.waves, grid, bf16, stream);
+        case GroupFam::MX8:
+            return qg::launch_burst_mx_grouped(bg, false, pl.mb, pl.nb, pl.waves, grid, bf16, stream);
+        default:
+            return qg::launch_burst_mx_grouped(bg, true, pl.mb, pl.nb, pl.waves, grid, bf16, stream);
+    }
+}
+
+// The workspace the grouped call's split plan needs (0: no problem splits,
+// or the arguments are not a valid grouped call).
+size_t group_workspace(GroupFam fam, const void* kargs, int count) {
+    GroupCall g;
+    int span_begin[qg::kGroupMax + 1];
+    if (group_collect(fam, kargs, count, QGEMM_OUT_BF16, &g, span_begin) != hipSuccess) return 0;
+    const GroupPlan pl = group_plan(fam, g, true);
+    return pl.ok ? pl.ws_bytes : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+hipError_t gemm_a8w8_blockscale_bpreshuffle_grouped(const opus_gemm_kargs* args, int group_count, int out_dtype,
+                                                    int grid_blocks, void* workspace, size_t workspace_bytes,
+                                                    hipStream_t stream) {
+    return group_entry(GroupFam::BS_KPANEL, args, group_count, out_dtype, grid_blocks, workspace, workspace_bytes,
+                       stream);
+}
+size_t gemm_a8w8_blockscale_bpreshuffle_grouped_workspace_bytes(const opus_gemm_kargs* args, int group_count) {
+    return group_workspace(GroupFam::BS_KPANEL, args, group_count);
+}
+
+hipError_t gemm_a8w8_blockscale_ldsbypass_grouped(const opus_gemm_ldsbypass_kargs* args, int group_count,
+                                                  int out_dtype, int grid_blocks, void* workspace,
+                                                  size_t workspace_bytes, hipStream_t stream) {
+    return group_entry(GroupFam::BS_FRAG, args, group_count, out_dtype, grid_blocks, workspace, workspace_bytes,
+                       stream);
+}
+size_t gemm_a8w8_blockscale_ldsbypass_grouped_workspace_bytes(const opus_gemm_ldsbypass_kargs* args,
+                                                              int group_count) {
+    return group_workspace(GroupFam::BS_FRAG, args, group_count);
+}
+
+hipError_t gemm_a8w8_mxfp8_grouped(const opus_gemm_scale_kargs* args, int group_count, int out_dtype, int grid_blocks,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return group_entry(GroupFam::MX8, args, group_count, out_dtype, grid_blocks, workspace, workspace_bytes, stream);
+}
+size_t gemm_a8w8_mxfp8_grouped_workspace_bytes(const opus_gemm_scale_kargs* args, int group_count) {
+    return group_workspace(GroupFam::MX8, args, group_count);
+}
+
+hipError_t gemm_a4w4_mxfp4_grouped(const opus_gemm_scale_kargs* args, int group_count, int out_dtype, int grid_blocks,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return group_entry(GroupFam::MX4, args, group_count, out_dtype, grid_blocks, workspace, workspace_bytes, stream);
+}
+size_t gemm_a4w4_mxfp4_grouped_workspace_bytes(const opus_gemm_scale_kargs* args, int group_count) {
+    return group_workspace(GroupFam::MX4, args, group_count);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- whole-output reference GEMM
+extern "C" {
+
+// Validation and launch of ref_gemm.hip (see qgemm.h): batch 1, row-major
+// codes, fp32 output that overlaps no input.
+hipError_t qgemm_reference_gemm(int family, const opus_gemm_scale_kargs* args, hipStream_t stream) {
+    qg::trace_reset();
+    if (!args || family < QGEMM_REF_BS_FP32 || family > QGEMM_REF_MXFP4) return hipErrorInvalidValue;
+    const auto& a = *args;
+    if (!a.ptr_a || !a.ptr_b || !a.ptr_c || !a.ptr_sfa || !a.ptr_sfb || a.batch != 1 || a.m <= 0 || a.n <= 0 ||
+        a.k <= 0)
+        return hipErrorInvalidValue;
+    const bool mx = family == QGEMM_REF_MXFP8 || family == QGEMM_REF_MXFP4;
+    const bool fp4 = family == QGEMM_REF_MXFP4;
+    if (a.k % (mx ? 32 : 128)) return hipErrorInvalidValue;
+    const long long kbytes = fp4 ? a.k / 2 : a.k, kg = a.k / (mx ? 32 : 128), nbk = ceil_div(a.n, 128);
+    if (a.stride_a < kbytes || a.stride_b < kbytes || a.stride_c < a.n || !aligned(a.ptr_c, 4))
+        return hipErrorInvalidValue;
+    qg::RefArgs r{};
+    r.a = static_cast<const uint8_t*>(a.ptr_a);
+    r.b = static_cast<const uint8_t*>(a.ptr_b);
+    r.sfa = static_cast<const uint8_t*>(a.ptr_sfa);
+    r.sfb = static_cast<const uint8_t*>(a.ptr_sfb);
+    r.c = static_cast<float*>(a.ptr_c);
+    r.m = a.m;
+    r.n = a.n;
+    r.k = a.k;
+    r.lda = a.stride_a;
+    r.ldb = a.stride_b;
+    r.ldc = a.stride_c;
+    uint64_t sfa_bytes, sfb_bytes;
+    const int elem = family == QGEMM_REF_BS_FP32 ? 4 : 1;
+    if (mx) {
+        if (a.stride_sfa < kg || a.stride_sfb < kg) return hipErrorInvalidValue;
+        r.sfa_sm = a.stride_sfa;
+        r.sfb_sm = a.stride_sfb;
+        sfa_bytes = (uint64_t)(a.m - 1) * a.stride_sfa + kg;
+        sfb_bytes = (uint64_t)(a.n - 1) * a.stride_sfb + kg;
+    } else {
+        // A's scales: row-major [M][K/128] (stride_sfa = 1, M > 1) or
+        // column-major [K/128][M] (stride_sfa >= M), as the product entries
+        const bool rowmajor = a.stride_sfa == 1 && a.m > 1;
+        if (a.stride_sfb < kg || (!rowmajor && a.stride_sfa < a.m)) return hipErrorInvalidValue;
+        if (elem == 4 && (!aligned(a.ptr_sfa, 4) || !aligned(a.ptr_sfb, 4))) return hipErrorInvalidValue;
+        r.sfa_sm = rowmajor ? kg : 1;
+        r.sfa_sk = rowmajor ? 1 : a.stride_sfa;
+        r.sfb_sm = a.stride_sfb;
+        sfa_bytes = (rowmajor ? (uint64_t)a.m * kg : (uint64_t)(kg - 1) * a.stride_sfa + a.m) * elem;
+        sfb_bytes = ((uint64_t)(nbk - 1) * a.stride_sfb + kg) * elem;
+    }
+    const uint64_t cb = ((uint64_t)(a.m - 1) * a.stride_c + a.n) * 4;
+    if (overlaps(a.ptr_c, cb, a.ptr_a, (uint64_t)(a.m - 1) * a.stride_a + kbytes) ||
+        overlaps(a.ptr_c, cb, a.ptr_b, (uint64_t)(a.n - 1) * a.stride_b + kbytes) ||
+        overlaps(a.ptr_c, cb, a.ptr_sfa, sfa_bytes) || overlaps(a.ptr_c, cb, a.ptr_sfb, sfb_bytes))
+        return hipErrorInvalidValue;
+    const hipError_t st = check_arch();
+    if (st != hipSuccess) return st;
+    return qg::launch_ref_gemm(r, static_cast<qg::RefFam>(family), stream);
+}
+
+}  // extern "C"

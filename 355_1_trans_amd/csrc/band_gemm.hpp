@@ -119,6 +119,7 @@ __global__ __launch_bounds__(kBandWaves * 64, 1) void band_gemm_kernel(const Ban
     const int nk = min(NKT, kt0 + ba.kt_per_split) - kt0;    // 1 .. KTM (host plan)
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
     const int q = L >> 4, l16 = L & 15;
+    if (ba.splitk > 1 && tid == 0) split_claim(ba.counters + (long long)bz * ba.bands + bnd, ba.epoch);
     const int n0 = bnd * COLS;
     const int nw = n0 + w * CB * 16;         // the wave's first B row
 

@@ -133,6 +133,7 @@ __global__ __launch_bounds__(512, 1) void bsf32_gemm_kernel(const Bsf32Args ba) 
     const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
 
     const int tid = threadIdx.x;
+    if (slice && tid == 0) split_claim(ba.counters + (v - ba.dp_tiles), ba.epoch);
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
     const int wm = w >> 1, wn = w & 1;
     const int q = L >> 4, l16 = L & 15;

@@ -144,8 +144,13 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
     return best;
 }
 
+// One work item of the burst kernel: output tile nt (NB * 16 columns, all
+// rows) of batch entry bz over K slice sk, with its split-K reduce.  Called
+// once per workgroup by burst_gemm_kernel and once per item by the grouped
+// kernel's persistent loop; every thread of the workgroup returns together.
 template <int FMT, BLay BL, int MB, int NB, int WAVES, int KPW, bool BF16>
-__global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs bp) {
+__device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, const int sk, const int bz,
+                                           const int batch) {
     constexpr int kBurstWaves = WAVES;
     // RAW: MXFP8 / MXFP4 with row-major B and E8M0 scales; else fp8 with
     // fp32 block scales on B' (K-panel) or B'' (fragment order)
@@ -170,13 +175,13 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
     const int M = p.m, N = p.n, KB = p.kbytes, LDA = p.lda, LDB = p.ldb, LDC = p.ldc;
     const int SFA_SM = p.sfa_sm, SFA_SK = p.sfa_sk, SFB_SN = p.sfb_sn;
     const int nk = KB / BKB;
-    const int nt = blockIdx.x % bp.n_tiles, sk = blockIdx.x / bp.n_tiles, bz = blockIdx.y;
     const int n0 = nt * COLS;
     const int kt_begin = sk * bp.kt_per_split;
     const int kt_end = min(nk, kt_begin + bp.kt_per_split);
     const int per_wave = (bp.kt_per_split + kBurstWaves - 1) / kBurstWaves;    // <= KPW (host plan)
     static_assert(KPW <= burst_max_kpw(MB, NB, WAVES, MX), "registers");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
+    if (bp.splitk > 1 && tid == 0) split_claim(bp.counters + (long long)bz * bp.n_tiles + nt, bp.epoch);
     const int q = L >> 4, l16 = L & 15;
     const int kw0 = kt_begin + w * per_wave;
     const int nkw = max(0, min(kt_end, kw0 + per_wave) - kw0);     // this wave's K-tiles
@@ -430,7 +435,6 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
 
     // ---- split-K: partial tile out, the last workgroup of the tile sums ----
     const long long plane = (long long)M * N;
-    const int batch = gridDim.y;
     const long long split_stride = (long long)batch * plane;
     const bool vec_ok = (N & 3) == 0;
     {
@@ -488,6 +492,40 @@ __global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs 
     }
     __syncthreads();
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int FMT, BLay BL, int MB, int NB, int WAVES, int KPW, bool BF16>
+__global__ __launch_bounds__(WAVES * 64) void burst_gemm_kernel(const BurstArgs bp) {
+    burst_tile<FMT, BL, MB, NB, WAVES, KPW, BF16>(bp, blockIdx.x % bp.n_tiles, blockIdx.x / bp.n_tiles, blockIdx.y,
+                                                  gridDim.y);
+}
+
+// ---- grouped launch: several decode GEMMs (own N, K, operands, scales and
+// output; M <= 64 each) in one grid over one list of work items ----
+// Problem j owns items [item_begin[j], item_begin[j + 1]): its n_tiles *
+// splitk (tile, K slice) pairs, tile-major within a slice, as one problem's
+// own launch would number its workgroups.  Workgroup b takes items b,
+// b + gridDim.x, ... (gridDim.x = the item count for one workgroup per item,
+// or fewer for a persistent grid).  Every problem carries its own counter
+// block and partial planes (batch 1), all under the launch's one epoch.
+constexpr int kGroupMax = 16;
+struct BurstGroup {
+    BurstArgs p[kGroupMax];
+    int item_begin[kGroupMax + 1];    // item_begin[count] = items in total
+    int count;
+};
+static_assert(sizeof(BurstGroup) <= 4096, "a grouped launch passes its problems as kernel arguments");
+
+template <int FMT, BLay BL, int MB, int NB, int WAVES, int KPW, bool BF16>
+__global__ __launch_bounds__(WAVES * 64) void burst_grouped_kernel(const BurstGroup g) {
+    const int items = g.item_begin[g.count];
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        int j = 0;    // the problem of the item (uniform: a scalar scan of at most 16 bounds)
+        while (j + 1 < g.count && item >= g.item_begin[j + 1]) ++j;
+        const int local = item - g.item_begin[j];
+        burst_tile<FMT, BL, MB, NB, WAVES, KPW, BF16>(g.p[j], local % g.p[j].n_tiles, local / g.p[j].n_tiles, 0, 1);
+        __syncthreads();    // the next item's slot writes reuse the LDS the reduction just read
+    }
 }
 
 }  // namespace qg

@@ -85,6 +85,20 @@ __device__ __forceinline__ float load_partial1(__amdgpu_buffer_rsrc_t r, int ele
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, elem * 4, 0, kCoherent));
 }
 
+// The launch's claim on a tile's counter word, issued by every slice when it
+// starts, long before any slice arrives: an atomic max with (epoch << 8)
+// turns the re-armed word (zero, or an earlier epoch's count) into "this
+// epoch, no arrivals" and leaves a word that already carries this epoch as
+// it is, so the arrivals take split_arrive's one-atomic path.  Its result is
+// not waited for.  A word above the tag (a wrapped epoch, garbage) keeps its
+// value and the arrivals claim it by compare-and-swap instead.  Without the
+// claim every slice of a tile arriving close together found an untagged word
+// and went through the compare-and-swap loop: configs[0]'s five slices per
+// tile measured 13.6 us a launch against 9.1 us.
+__device__ __forceinline__ void split_claim(unsigned* ctr, unsigned epoch) {
+    __hip_atomic_fetch_max(ctr, epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Split-K arrival counter of one output tile, tagged with the launch's
 // epoch: bits 8..31 hold the epoch (a 24-bit number the host takes from a
 // process-wide sequence, a new one per launch), bits 0..7 the slices of

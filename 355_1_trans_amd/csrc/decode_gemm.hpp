@@ -118,6 +118,7 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
 
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
     const int q = L >> 4, l16 = L & 15;
+    if (dp.splitk > 1 && tid == 0) split_claim(dp.counters + (long long)bz * dp.n_tiles + nt, dp.epoch);
     const int nw0 = n0 + 16 * w;                     // the wave's first column
 
     const uint8_t* A = p.a + bz * p.a_batch;

@@ -1,5 +1,6 @@
-// Instantiations and launcher of the burst kernel for fp8 with fp32 block
-// scales (M <= 64, K-panel B' or fragment-order B'').
+// Instantiations and launchers of the burst kernel for fp8 with fp32 block
+// scales (M <= 64, K-panel B' or fragment-order B''); the grouped kernel's
+// are in kernels_burst_grouped.hip.
 #include "burst_launch.hpp"
 
 namespace qg {

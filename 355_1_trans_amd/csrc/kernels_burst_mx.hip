@@ -1,5 +1,6 @@
-// Instantiations and launcher of the burst kernel for MXFP8 / MXFP4 with
-// row-major B and row-major E8M0 scales (M <= 64).
+// Instantiations and launchers of the burst kernel for MXFP8 / MXFP4 with
+// row-major B and row-major E8M0 scales (M <= 64); the grouped kernel's are
+// in kernels_burst_mx_grouped.hip.
 #include "burst_launch.hpp"
 
 namespace qg {

@@ -77,6 +77,14 @@ hipError_t launch_burst(const BurstArgs& a, bool frag, int mb, int nb, int waves
 // kernels_burst_mx.hip: the same for MXFP8 / MXFP4 (fp4) with row-major B and E8M0 scales
 hipError_t launch_burst_mx(const BurstArgs& a, bool fp4, int mb, int nb, int waves, int batch, bool bf16,
                            hipStream_t s);
+// kernels_burst_grouped.hip / kernels_burst_mx_grouped.hip: the grouped form
+// (several decode GEMMs, one grid over their work items; grid = the item
+// count, or fewer workgroups for a persistent walk)
+struct BurstGroup;
+hipError_t launch_burst_grouped(const BurstGroup& g, bool frag, int mb, int nb, int waves, int grid, bool bf16,
+                                hipStream_t s);
+hipError_t launch_burst_mx_grouped(const BurstGroup& g, bool fp4, int mb, int nb, int waves, int grid, bool bf16,
+                                   hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);
@@ -99,6 +107,25 @@ hipError_t launch_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int k
 // order with w16; X and K multiples of 64
 hipError_t launch_transpose(bool w16, const uint8_t* src, uint8_t* dst, int x_len, int k_len, long long ld,
                             int batch, long long src_batch, long long dst_batch, hipStream_t st);
+
+// ref_gemm.hip: the whole-output reference GEMM (fp64 sums of decoded,
+// scaled products; row-major A [M][K] and B [N][K] codes, lda / ldb in
+// bytes; fp32 C [M][N] with pitch ldc).  Scales: MX8 / MX4 sfa(m, g) =
+// sfa[m * sfa_sm + g] (E8M0 per 32 K), sfb(n, g) = sfb[n * sfb_sm + g];
+// BSF32 (fp32) / BS8 (E8M0) sfa(m, kg) = sfa[m * sfa_sm + kg * sfa_sk],
+// sfb(nb, kg) = sfb[nb * sfb_sm + kg] per 128 K.
+enum class RefFam : int { BSF32 = 0, BS8 = 1, MX8 = 2, MX4 = 3 };
+struct RefArgs {
+    const uint8_t* a;
+    const uint8_t* b;
+    const uint8_t* sfa;
+    const uint8_t* sfb;
+    float* c;
+    int m, n, k;
+    long long lda, ldb, ldc;
+    long long sfa_sm, sfa_sk, sfb_sm;
+};
+hipError_t launch_ref_gemm(const RefArgs& a, RefFam fam, hipStream_t s);
 
 // probe.hip
 hipError_t launch_probe(int32_t* dev_out, hipStream_t s);

@@ -190,6 +190,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     // the wave index is uniform: keep it (and every K-tile index) in SGPRs
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
     const int q = L >> 4, l16 = L & 15;
+    if (sp.splitk > 1 && tid == 0)
+        split_claim(sp.counters + ((long long)bz * sp.m_tiles + mt) * sp.n_tiles + nt, sp.epoch);
 
     const uint8_t* A = p.a + bz * p.a_batch;
     const uint8_t* B = p.b + bz * p.b_batch;

@@ -141,6 +141,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_gemm_kernel(const
     const int li = L & 15, lq = L >> 4;
     const int lr = li / CH, lc = li % CH;        // the lane's operand row: (row of its group, chunk)
     const int bz = blockIdx.y, z = blockIdx.z;
+    if (sa.splitk > 1 && tid == 0) split_claim(sa.counters + (long long)bz * gridDim.x + blockIdx.x, sa.epoch);
     const int r0 = blockIdx.x * sa.rows_per_wg;
     const int R = min(sa.rows_per_wg, p.n - r0);
     const int M = p.m, KB = p.kbytes, ldb = p.ldb, lds = p.sfb_sn;

@@ -66,6 +66,10 @@ WORKLOADS = {
     "bs_e8m0_8192": ("bs8", 8192, 8192, 8192, None),
 }
 
+# the other BASELINE configs the default run measures after the headline:
+# (workload, M override)
+EXTRA_WORKLOADS = (("mxfp4_8192", None), ("bs_c0", None), ("mxfp4_c4", 32))
+
 NAMES = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
          "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
          "mx4a": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K, aiter gemm_a4w4 bpreshuffle formats "
@@ -90,6 +94,8 @@ def parse():
                    help="mxfp4_8192_aiter: persistent grid of this many workgroups (0 = one per tile)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-check", action="store_true", help="skip the output check against the oracle")
+    p.add_argument("--no-extra", action="store_true",
+                   help="default run only: skip the extra records (configs[3], configs[0], configs[4] M = 32)")
     p.add_argument("--sfa-km", action="store_true",
                    help="block-scale fp32 workloads: pass A's scales column-major [K/128][M] (the reference's "
                         "layout) instead of BASELINE's row-major [M][K/128]")
@@ -98,6 +104,10 @@ def parse():
                    help="time a block-scale shape sweep (bpreshuffle and ldsbypass), one JSON line per shape: "
                         "configs2 = BASELINE configs[2] (default), dsv4 = the 125 traced DeepSeek-V4 a8w8 shapes "
                         "(355_1_trans_amd/configs/dsv4_a8w8_shapes.csv)")
+    p.add_argument("--grouped", default=None, choices=["bpreshuffle", "ldsbypass", "mxfp8", "mxfp4"],
+                   help="time configs[2]'s decode shapes (N, K) = (2112, 7168), (4096, 7168), (7168, 2048) at M = "
+                        "--m (default 16) as ONE grouped launch and as three single launches; one JSON line")
+    p.add_argument("--group-grid", type=int, default=0, help="--grouped: persistent grid (0 = one per item)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run only a plain 256 MiB device copy 5 times (PMC byte-counter calibration)")
     return p.parse_args()
@@ -435,6 +445,174 @@ def sweep(args):
         torch.cuda.empty_cache()
 
 
+# ------------------------------------------------------------------ grouped decode
+GROUP_NK = ((2112, 7168), (4096, 7168), (7168, 2048))
+
+
+def grouped(args):
+    """configs[2]'s decode shapes at one M as one grouped launch against
+    the same three GEMMs launched one by one (each with the library plan):
+    both as HIP graphs over rotating weight copies (> 512 MB, past the last
+    level cache), algorithmic bytes = every A, B, scale and C byte once."""
+    import torch
+    q = importlib.import_module("355_1_trans_amd")
+    L = q.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    kind = args.grouped
+    fam = {"bpreshuffle": "bs", "ldsbypass": "lbp", "mxfp8": "mx8", "mxfp4": "mx4"}[kind]
+    m = args.m or 16
+    probs, alg = [], 0
+    for i, (n, k) in enumerate(GROUP_NK):
+        ops = make_operands(q, fam, m, n, k, dev)
+        ops["C"] = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        probs.append((n, k, ops))
+        alg += (ops["A"].numel() + ops["SA"].numel() * ops["SA"].element_size() + ops["B"].numel()
+                + ops["SB"].numel() * ops["SB"].element_size() + m * n * 2)
+    b_bytes = sum(o["B"].numel() + o["SB"].numel() * o["SB"].element_size() for _, _, o in probs)
+    copies = max(2, ROTATE_BYTES // b_bytes + 1)
+    rot = [[(o["B"], o["SB"]) if c == 0 else (o["B"].clone(), o["SB"].clone()) for _, _, o in probs]
+           for c in range(copies)]
+    name, ktype = q._GROUPED[kind]
+    single_fn, single_q = entry_for(L, fam)
+    group_calls, single_calls = [], []
+    for c in range(copies):
+        ks = [kargs_for(q, fam, m, n, k, o["A"], rot[c][j][0], o["C"], o["SA"], rot[c][j][1], False)
+              for j, (n, k, o) in enumerate(probs)]
+        group_calls.append((ktype * len(ks))(*ks))
+        single_calls.append(ks)
+    gws_b = max(256, getattr(L, name + "_workspace_bytes")(group_calls[0], len(probs)))
+    gws = torch.zeros(gws_b, dtype=torch.uint8, device=dev)
+    sws_b = [max(256, single_q(ctypes.byref(k))) for k in single_calls[0]]
+    sws = [torch.zeros(b, dtype=torch.uint8, device=dev) for b in sws_b]
+    torch.cuda.synchronize()
+
+    def launch_group(i):
+        st = getattr(L, name)(group_calls[i % copies], len(probs), 1, args.group_grid, gws.data_ptr(), gws.numel(),
+                              sptr)
+        if st:
+            raise RuntimeError(f"{name} failed: HIP error {st}")
+
+    kern = {}
+
+    def launch_single(i):
+        for j, ka in enumerate(single_calls[i % copies]):
+            st = single_fn(ctypes.byref(ka), sws[j].data_ptr(), sws[j].numel(), sptr)
+            if st:
+                raise RuntimeError(f"single launch {j} failed: HIP error {st}")
+            kern[j] = q.last_launch()
+
+    with torch.cuda.stream(stream):
+        launch_group(0)
+    gkern = q.last_launch()
+    steps = args.steps
+    ms_g, t_g = run_timed(launch_group, copies, stream, True, steps, args.warmup // 4, args.settle_s / 2)
+    ms_s, t_s = run_timed(launch_single, copies, stream, True, steps, args.warmup // 4, args.settle_s / 2)
+    check = None
+    if not args.no_check:
+        import oracle as O
+        launch_group(0)
+        torch.cuda.synchronize()
+        bad, worst = 0, 0.0
+        for n, k, o in probs:
+            h = host_copies(fam, o, False)
+            r = check_points(O, fam, m, n, k, h, o["C"], False)
+            bad += r["violations"]
+            worst = max(worst, r["max_err_over_bound"])
+        check = {"points": CHECK_POINTS * len(probs), "violations": bad, "max_err_over_bound": worst, "ok": bad == 0}
+    gb_g, gb_s = alg / (ms_g * 1e-3) / 1e9, alg / (ms_s * 1e-3) / 1e9
+    print(json.dumps({
+        "grouped": kind, "M": m, "shapes_NK": [list(x) for x in GROUP_NK], "algorithmic_bytes": int(alg),
+        "grouped_us": round(ms_g * 1e3, 2), "grouped_GBps": round(gb_g, 1), "grouped_hbm_frac": round(gb_g / HBM_GBPS, 4),
+        "singles_us": round(ms_s * 1e3, 2), "singles_GBps": round(gb_s, 1), "singles_hbm_frac": round(gb_s / HBM_GBPS, 4),
+        "speedup": round(ms_s / ms_g, 3), "grouped_kernel": gkern, "single_kernels": [kern[j] for j in sorted(kern)],
+        "spread_us": {"grouped": t_g.get("replay_us"), "singles": t_s.get("replay_us")}, "check": check}), flush=True)
+    if check is not None and not check["ok"]:
+        sys.exit(1)
+
+
+def measure(args, workload, m_over, n_over, k_over, with_cpu):
+    """Time one workload (settle, warm up, `--steps` launches) and return its
+    JSON record: throughput, roofline block of the dominant kernel, the
+    4096-point check and, with_cpu, the CPU baseline."""
+    import torch
+    q = importlib.import_module("355_1_trans_amd")
+    L = q.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    fam, M, N, K, cfg = WORKLOADS[workload]
+    M, N, K = m_over or M, n_over or N, k_over or K
+    hbm_bound = M <= 256
+    ops = make_operands(q, fam, M, N, K, dev, args.sfa_km)
+    A, SA, B0, SB0 = ops["A"], ops["SA"], ops["B"], ops["SB"]
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    b_bytes = B0.numel() * B0.element_size() + SB0.numel() * SB0.element_size()
+    copies = max(2, ROTATE_BYTES // b_bytes + 1) if hbm_bound else 1
+    Bs = [B0] + [B0.clone() for _ in range(copies - 1)]
+    SBs = [SB0] + [SB0.clone() for _ in range(copies - 1)]
+
+    launch_fn, wq = entry_for(L, fam)
+    calls = [kargs_for(q, fam, M, N, K, A, B, C, SA, SB, args.sfa_km, args.grid_blocks) for B, SB in zip(Bs, SBs)]
+    ws_bytes = max(1, wq(ctypes.byref(calls[0])))
+    ws = torch.zeros((ws_bytes + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream(dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    def launch(i):
+        st = launch_fn(ctypes.byref(calls[i % len(calls)]), ws.data_ptr(), ws.numel(), sptr)
+        if st:
+            raise RuntimeError(f"{workload} launch failed: HIP error {st}")
+
+    with torch.cuda.stream(stream):
+        launch(0)
+    kernel = q.last_launch()
+    ms, timing = run_timed(launch, len(calls), stream, hbm_bound, args.steps, args.warmup, args.settle_s)
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    kind = "fp4" if fam in ("mx4", "mx4a") else "fp8"
+    tag = workload + (f"_m{M}" if m_over else "") + (f"_n{N}" if n_over else "") + (f"_k{K}" if k_over else "")
+    if hbm_bound:
+        # algorithmic bytes: A, B and both scale arrays read once, C written once
+        alg = A.numel() * A.element_size() + SA.numel() * SA.element_size() + b_bytes + C.numel() * 2
+        gbps = alg / (ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_GBPS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_GBPS, 4), "traffic": traffic_from_profiles(tag),
+                    "algorithmic_bytes": int(alg)}
+    else:
+        peak = PEAK_TFLOPS[kind]
+        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                    "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(tag)}
+
+    check, cpu = None, None
+    if not (args.no_check and not with_cpu):
+        import oracle as O
+        h = host_copies(fam, ops, args.sfa_km)
+        if not args.no_check:
+            torch.cuda.synchronize()
+            check = check_points(O, fam, M, N, K, h, C, args.sfa_km)
+        if with_cpu:
+            cpu = cpu_baseline(O, fam, M, N, K, h, args.sfa_km, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": kind,
+        "data": "synthetic N(0,1) (torch GPU generator, seeds 0 / 1), quantized on the GPU per the BASELINE recipe",
+        "config": {"workload": f"{NAMES[fam]} M={M} N={N} K={K}, bf16 out " +
+                               (f"(BASELINE configs[{cfg}])" if cfg is not None
+                                else "(the reference's headline block-scale kernel, BASELINE.md)"),
+                   "M": M, "N": N, "K": K, "out": "bf16", "kernel": kernel},
+        "timing": timing, "roofline": roofline, "cpu_baseline": cpu, "check": check,
+    }
+    del Bs, SBs, calls, ws, ops
+    torch.cuda.empty_cache()
+    return line
+
+
 # ------------------------------------------------------------------ main
 def main():
     args = parse()
@@ -461,81 +639,27 @@ def main():
     if args.sweep:
         sweep(args)
         return
+    if args.grouped:
+        grouped(args)
+        return
 
-    q = importlib.import_module("355_1_trans_amd")
-    L = q.lib()
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-
-    fam, M, N, K, cfg = WORKLOADS[args.workload]
-    M, N, K = args.m or M, args.n or N, args.k or K
-    hbm_bound = M <= 256
-    ops = make_operands(q, fam, M, N, K, dev, args.sfa_km)
-    A, SA, B0, SB0 = ops["A"], ops["SA"], ops["B"], ops["SB"]
-    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    b_bytes = B0.numel() * B0.element_size() + SB0.numel() * SB0.element_size()
-    copies = max(2, ROTATE_BYTES // b_bytes + 1) if hbm_bound else 1
-    Bs = [B0] + [B0.clone() for _ in range(copies - 1)]
-    SBs = [SB0] + [SB0.clone() for _ in range(copies - 1)]
-
-    launch_fn, wq = entry_for(L, fam)
-    calls = [kargs_for(q, fam, M, N, K, A, B, C, SA, SB, args.sfa_km, args.grid_blocks) for B, SB in zip(Bs, SBs)]
-    ws_bytes = max(1, wq(ctypes.byref(calls[0])))
-    ws = torch.zeros((ws_bytes + 255) // 256 * 256, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.Stream(dev)
-    sptr = ctypes.c_void_p(stream.cuda_stream)
-
-    def launch(i):
-        st = launch_fn(ctypes.byref(calls[i % len(calls)]), ws.data_ptr(), ws.numel(), sptr)
-        if st:
-            raise RuntimeError(f"{args.workload} launch failed: HIP error {st}")
-
-    with torch.cuda.stream(stream):
-        launch(0)
-    kernel = q.last_launch()
-    ms, timing = run_timed(launch, len(calls), stream, hbm_bound, args.steps, args.warmup, args.settle_s)
-    flops = 2.0 * M * N * K
-    tflops = flops / (ms * 1e-3) / 1e12
-
-    kind = "fp4" if fam in ("mx4", "mx4a") else "fp8"
-    tag = args.workload + (f"_m{M}" if args.m else "") + (f"_n{N}" if args.n else "") + (f"_k{K}" if args.k else "")
-    if hbm_bound:
-        # algorithmic bytes: A, B and both scale arrays read once, C written once
-        alg = A.numel() * A.element_size() + SA.numel() * SA.element_size() + b_bytes + C.numel() * 2
-        gbps = alg / (ms * 1e-3) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_GBPS, "unit": "GB/s",
-                    "frac": round(gbps / HBM_GBPS, 4), "traffic": traffic_from_profiles(tag),
-                    "algorithmic_bytes": int(alg)}
-    else:
-        peak = PEAK_TFLOPS[kind]
-        roofline = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
-                    "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(tag)}
-
-    check, cpu = None, None
-    if not (args.no_check and args.no_cpu):
-        import oracle as O
-        h = host_copies(fam, ops, args.sfa_km)
-        if not args.no_check:
-            torch.cuda.synchronize()
-            check = check_points(O, fam, M, N, K, h, C, args.sfa_km)
-        if not args.no_cpu:
-            cpu = cpu_baseline(O, fam, M, N, K, h, args.sfa_km, args.cpu_seconds)
-
-    line = {
-        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": kind,
-        "data": "synthetic N(0,1) (torch GPU generator, seeds 0 / 1), quantized on the GPU per the BASELINE recipe",
-        "config": {"workload": f"{NAMES[fam]} M={M} N={N} K={K}, bf16 out " +
-                               (f"(BASELINE configs[{cfg}])" if cfg is not None
-                                else "(the reference's headline block-scale kernel, BASELINE.md)"),
-                   "M": M, "N": N, "K": K, "out": "bf16", "kernel": kernel},
-        "timing": timing, "roofline": roofline, "cpu_baseline": cpu, "check": check,
-    }
+    line = measure(args, args.workload, args.m, args.n, args.k, with_cpu=not args.no_cpu)
+    failed = [line] if line["check"] is not None and not line["check"]["ok"] else []
+    if not args.no_extra and args.workload == "mxfp8_8192" and not (args.m or args.n or args.k):
+        # the other BASELINE configs from the same run, so that the driver's
+        # record carries them too (GPU time, roofline, kernel, 4096-point check)
+        line["extra"] = []
+        for wl, m in EXTRA_WORKLOADS:
+            x = measure(args, wl, m, None, None, with_cpu=False)
+            line["extra"].append({k: x[k] for k in ("value", "unit", "ms_per_step", "dtype", "config", "roofline",
+                                                   "check", "timing")})
+            if x["check"] is not None and not x["check"]["ok"]:
+                failed.append(x)
     print(json.dumps(line), flush=True)
-    if check is not None and not check["ok"]:
-        print(f"bench.py: output check FAILED ({check['violations']} of {CHECK_POINTS} points out of tolerance)",
-              file=sys.stderr)
+    for x in failed:
+        print(f"bench.py: output check FAILED for {x['config']['workload']} ({x['check']['violations']} of "
+              f"{CHECK_POINTS} points out of tolerance)", file=sys.stderr)
+    if failed:
         sys.exit(1)
 
 

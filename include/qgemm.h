@@ -281,6 +281,62 @@ hipError_t gemm_a4w4_mxfp4_noalloc(const opus_gemm_scale_kargs* args, int out_dt
 size_t gemm_a4w4_mxfp4_noalloc_max_workspace_bytes(void);
 
 /* ------------------------------------------------------------------ */
+/* Grouped decode GEMMs: several problems in one launch.                */
+/* ------------------------------------------------------------------ */
+/* The persistent scheduling across mixed decode batches that the
+ * reference's split-K plan names next to its fused split-K reduce
+ * (R/opus_gemm_splitk_and_interface_refactor.md:41-45; persistent tile walk
+ * MX4/MULTITILE_DESIGN.md:78); the reference has no symbol for it.  `args`
+ * points to `group_count` (1..16) kargs blocks, each a complete problem as
+ * the family's single-problem entry takes it (same layouts, strides and
+ * checks), with batch = 1 and 1 <= M <= 64; problems differ in M, N, K,
+ * operands, scales and output.  No output may overlap any operand or output
+ * of the call.  One grid walks every problem's (output tile, K slice) work
+ * items; each split problem sums its slices in its own counters and fp32
+ * planes inside the workspace (query: *_grouped_workspace_bytes; rules as
+ * the single-problem workspace).  NULL runs every problem unsplit and is
+ * refused (hipErrorInvalidValue) when a problem's K is past one workgroup's
+ * reach (16 waves x 4-8 K-tiles of 128 bytes, 8 waves x 4 for M > 32).
+ * grid_blocks: 0 = one workgroup per item; > 0 = a persistent grid of
+ * min(grid_blocks, items) workgroups.  out_dtype applies to every problem. */
+hipError_t gemm_a8w8_blockscale_bpreshuffle_grouped(const opus_gemm_kargs* args, int group_count, int out_dtype,
+                                                    int grid_blocks, void* workspace, size_t workspace_bytes,
+                                                    hipStream_t stream);
+size_t gemm_a8w8_blockscale_bpreshuffle_grouped_workspace_bytes(const opus_gemm_kargs* args, int group_count);
+hipError_t gemm_a8w8_blockscale_ldsbypass_grouped(const opus_gemm_ldsbypass_kargs* args, int group_count,
+                                                  int out_dtype, int grid_blocks, void* workspace,
+                                                  size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_blockscale_ldsbypass_grouped_workspace_bytes(const opus_gemm_ldsbypass_kargs* args,
+                                                              int group_count);
+hipError_t gemm_a8w8_mxfp8_grouped(const opus_gemm_scale_kargs* args, int group_count, int out_dtype, int grid_blocks,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a8w8_mxfp8_grouped_workspace_bytes(const opus_gemm_scale_kargs* args, int group_count);
+hipError_t gemm_a4w4_mxfp4_grouped(const opus_gemm_scale_kargs* args, int group_count, int out_dtype, int grid_blocks,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a4w4_mxfp4_grouped_workspace_bytes(const opus_gemm_scale_kargs* args, int group_count);
+
+/* ------------------------------------------------------------------ */
+/* Whole-output verification.                                           */
+/* ------------------------------------------------------------------ */
+/* An independent GPU reference GEMM for checking every output of a
+ * full-size launch: the role of the reference's gemm_ref_gpu
+ * (MX4/gemm_a4w4_mxfp4_4wave_host.cc:66-94, used at :219-257).  Each code
+ * is decoded and multiplied by its scale in fp64, the products are summed
+ * in fp64 in K order and rounded once into fp32 C [M][N] (stride_c >= N).
+ * No MFMA, no shuffled layouts: A [M][K] and B [N][K] row-major codes
+ * (fp4: K/2 bytes, even k in the low nibble; strides in bytes), batch 1.
+ * Scales: QGEMM_REF_BS_FP32 fp32, QGEMM_REF_BS_E8M0 E8M0 bytes, A per
+ * (row, 128 K) row-major (stride_sfa = 1) or column-major [K/128][M]
+ * (stride_sfa >= M), B per (128 rows, 128 K) [ceil(N/128)][stride_sfb];
+ * QGEMM_REF_MXFP8 / _MXFP4 E8M0 per (row, 32 K), [rows][stride_sfa / _sfb].
+ * K a multiple of 128 (block scales) or 32 (MX). */
+#define QGEMM_REF_BS_FP32 0
+#define QGEMM_REF_BS_E8M0 1
+#define QGEMM_REF_MXFP8 2
+#define QGEMM_REF_MXFP4 3
+hipError_t qgemm_reference_gemm(int family, const opus_gemm_scale_kargs* args, hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* Offline layout helpers (host, CPU).                                  */
 /* ------------------------------------------------------------------ */
 /* K-panel pre-shuffle, BPS host.cc:92-111: dst[kt][n][ki] = src[n][kt*128+ki]. */

@@ -49,3 +49,22 @@ def make_bs(m, n, k, seed=0):
     qa, sa = O.quant_bs_act(a)
     qb, sb = O.quant_bs_wgt(b)
     return qa, qb, sa, sb
+
+
+def assert_close_all(ref, got, what=""):
+    """Every element of two GPU tensors against the BASELINE tolerance,
+    |got - ref| <= 2^-7 |ref| + 1e-3 rms(ref) (rms over all of ref), computed
+    on the GPU; NaN or Inf in either counts as a violation."""
+    ref, got = ref.float(), got.float()
+    rms = float(torch.sqrt(torch.mean(ref.double() ** 2)))
+    bound = ref.abs() * 2.0 ** -7 + 1e-3 * rms
+    err = (got - ref).abs()
+    ok = err <= bound
+    bad = int((~ok).sum())
+    ratio = float(torch.nan_to_num(err / bound, nan=float("inf")).max())
+    if bad:
+        idx = int(torch.nonzero(~ok.reshape(-1))[0])
+        raise AssertionError(f"{what}: {bad} of {ref.numel()} elements out of tolerance, worst ratio {ratio:.3f}; "
+                             f"first at flat index {idx} (ref={float(ref.reshape(-1)[idx])}, "
+                             f"got={float(got.reshape(-1)[idx])})")
+    return ratio

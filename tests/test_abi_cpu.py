@@ -346,3 +346,58 @@ def test_noalloc_plans_as_the_query(qgemm):
     assert 2 * 129 * 18432 * 4 < need <= cap                # two fp32 planes + panels
     if not torch.cuda.is_available():
         assert L.gemm_a4w4_mxfp4_noalloc(ctypes.byref(fit), 1, None) != HIP_INVALID_VALUE
+
+
+# ----------------------------------------------------------------- grouped entries
+def _group(qgemm, shapes, fp4=False, bs=False):
+    """An array of far-apart fake kargs blocks (never dereferenced)."""
+    ks = []
+    for i, (m, n, k) in enumerate(shapes):
+        base = [(1 << 44) + ((5 * i + j) << 36) for j in range(5)]
+        if bs:
+            kg = k // 128
+            ks.append(qgemm.Kargs(base[0], base[1], base[2], m, n, k, 1, k, 128, n, m * k, n * k, m * n, base[3],
+                                  base[4], 1, kg, m * kg, ((n + 127) // 128) * kg))
+        else:
+            kb = k // 2 if fp4 else k
+            ks.append(qgemm.Kargs(base[0], base[1], base[2], m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n, base[3],
+                                  base[4], k // 32, k // 32, m * (k // 32), n * (k // 32)))
+    return (qgemm.Kargs * len(ks))(*ks)
+
+
+def test_grouped_validation_and_workspace(qgemm):
+    """Grouped calls: 1..16 problems of M <= 64 and batch 1; outputs must not
+    overlap another problem's operands; the workspace query is 0 unless a
+    problem splits K, and a split plan's workspace rule is the single
+    entries' (too small / misaligned / overlapping rejected)."""
+    L = qgemm.lib()
+    fn, query = L.gemm_a8w8_blockscale_bpreshuffle_grouped, L.gemm_a8w8_blockscale_bpreshuffle_grouped_workspace_bytes
+    ok = _group(qgemm, [(16, 2112, 7168), (16, 4096, 7168), (16, 7168, 2048)], bs=True)
+    assert query(ok, 3) == 0                                             # one slice each: no workspace
+    split = _group(qgemm, [(64, 2112, 16384), (8, 512, 2048)], bs=True)
+    need = query(split, 2)
+    assert need >= 256 + 4 * 64 * 2112 * 4                               # counters + >= 4 planes of problem 0
+    for bad in (0, 17, -1):
+        assert fn(ok, bad, 1, 0, None, 0, None) == HIP_INVALID_VALUE
+        assert query(ok, bad) == 0
+    assert fn(None, 1, 1, 0, None, 0, None) == HIP_INVALID_VALUE
+    assert fn(ok, 3, 1, -1, None, 0, None) == HIP_INVALID_VALUE          # grid_blocks < 0
+    big = _group(qgemm, [(16, 2112, 7168), (65, 512, 2048)], bs=True)
+    assert fn(big, 2, 1, 0, None, 0, None) == HIP_INVALID_VALUE          # M > 64
+    b2 = _group(qgemm, [(16, 2112, 7168)], bs=True)
+    b2[0].batch = 2
+    assert fn(b2, 1, 1, 0, None, 0, None) == HIP_INVALID_VALUE           # batch > 1
+    ov = _group(qgemm, [(16, 2112, 7168), (16, 512, 2048)], bs=True)
+    ov[1].ptr_c = ov[0].ptr_a                                            # C of problem 1 on A of problem 0
+    assert fn(ov, 2, 1, 0, None, 0, None) == HIP_INVALID_VALUE
+    ws = (1 << 44) + (90 << 36)
+    assert fn(split, 2, 1, 0, ws, need - 1, None) == HIP_INVALID_VALUE   # too small
+    assert fn(split, 2, 1, 0, ws + 16, need, None) == HIP_INVALID_VALUE  # misaligned
+    assert fn(split, 2, 1, 0, split[0].ptr_b, need, None) == HIP_INVALID_VALUE
+    mx = _group(qgemm, [(1, 7168, 16384), (32, 4096, 8192)], fp4=True)
+    assert L.gemm_a4w4_mxfp4_grouped(mx, 2, 1, 0, None, 0, None) != HIP_INVALID_VALUE or torch.cuda.is_available()
+    mx[1].k = 8000                                                      # K % 256 for fp4
+    assert L.gemm_a4w4_mxfp4_grouped(mx, 2, 1, 0, None, 0, None) == HIP_INVALID_VALUE
+    if not torch.cuda.is_available():
+        assert fn(ok, 3, 1, 0, None, 0, None) != HIP_INVALID_VALUE       # valid: stops at the device check
+        assert fn(split, 2, 1, 256, ws, need, None) != HIP_INVALID_VALUE

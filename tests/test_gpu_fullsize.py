@@ -4,19 +4,22 @@ Each test builds the benchmark's own inputs (BASELINE recipe: N(0,1) from
 seed 0, stream 0 for A and 1 for B, quantized on the host), calls the entry
 point the way bench.py does (bf16 output, the queried workspace), asserts
 which kernel instantiations ran (qgemm_last_launch) and checks the output
-against the CPU oracle at 4096 random points plus one whole band of rows
-that straddles a 256-row tile boundary -- the way the reference verifies
-its full-size runs (MX4 gemm_a4w4_mxfp4_4wave_host.cc:219-257 compares
-every 8192^3 output with gemm_ref_gpu; here the oracle is on the CPU, so
-the check is sampled).  Tolerance: |y - y_ref| <= 2^-7 |y_ref| + 1e-3
-rms(y_ref), rms taken over the checked elements.
+two ways: against the CPU oracle at 4096 random points plus one whole band
+of rows that straddles a 256-row tile boundary, and -- the way the
+reference verifies its full-size runs (MX4
+gemm_a4w4_mxfp4_4wave_host.cc:219-257 compares every 8192^3 output with
+gemm_ref_gpu) -- every output element against the whole-output GPU
+reference GEMM (qgemm_reference_gemm, pinned to the oracle in
+test_gpu_reference.py).  Tolerance: |y - y_ref| <= 2^-7 |y_ref| + 1e-3
+rms(y_ref), rms over the checked elements (the sampled check) or over the
+whole output (the full check).
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle as O
-from helpers import assert_close
+from helpers import assert_close, assert_close_all
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +71,9 @@ def test_mxfp8_bench_kernel_full_size(qgemm, gpu, m, n, k, kernel):
     torch.cuda.synchronize()
     _check(y, lambda r, c: O.gemm_mx8_points(qa, qb, sa, sb, r, c),
            lambda band: O.gemm_mx8(qa[band], qb, sa[band], sb), m, n, 256, f"mxfp8 {m}x{n}x{k}")
+    ref = qgemm.reference_gemm("mxfp8", dev(qa).view(torch.float8_e4m3fn), dev(qb).view(torch.float8_e4m3fn), dev(sa),
+                               dev(sb))
+    assert_close_all(ref, y, f"mxfp8 {m}x{n}x{k}, every output")
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
@@ -85,6 +91,8 @@ def test_mxfp4_bench_kernel_full_size(qgemm, gpu, m, n, k, kernel):
     torch.cuda.synchronize()
     _check(y, lambda r, c: O.gemm_mx4_points(qa, qb, sa, sb, r, c),
            lambda band: O.gemm_mx4(qa[band], qb, sa[band], sb), m, n, 256, f"mxfp4 {m}x{n}x{k}")
+    ref = qgemm.reference_gemm("mxfp4", dev(qa), dev(qb), dev(sa), dev(sb))
+    assert_close_all(ref, y, f"mxfp4 {m}x{n}x{k}, every output")
 
 
 @pytest.mark.parametrize("grid_blocks,kernel", [
@@ -106,6 +114,8 @@ def test_mxfp4_aiter_bench_kernel_full_size(qgemm, gpu, grid_blocks, kernel):
     torch.cuda.synchronize()
     _check(y, lambda r, c: O.gemm_mx4_points(qa, qb, sa, sb, r, c),
            lambda band: O.gemm_mx4(qa[band], qb, sa[band], sb), m, n, 256, f"mxfp4 aiter {m}x{n}x{k}")
+    ref = qgemm.reference_gemm("mxfp4", dev(qa), dev(qb), dev(sa), dev(sb))
+    assert_close_all(ref, y, f"mxfp4 aiter {m}x{n}x{k}, every output")
 
 
 def test_blockscale_fp32_bench_kernel_full_size(qgemm, gpu):
@@ -122,6 +132,9 @@ def test_blockscale_fp32_bench_kernel_full_size(qgemm, gpu):
     torch.cuda.synchronize()
     _check(y, lambda r, c: O.gemm_bs_fp32_points(qa, qb, sa, sb, r, c),
            lambda band: O.gemm_bs_fp32(qa[band], qb, sa[band], sb), m, n, 128, "bs-fp32 8192^3")
+    ref = qgemm.reference_gemm("bs_fp32", dev(qa).view(torch.float8_e4m3fn), dev(qb).view(torch.float8_e4m3fn),
+                               dev(sa), dev(sb))
+    assert_close_all(ref, y, "bs-fp32 8192^3, every output")
 
 
 def test_blockscale_e8m0_bench_kernel_full_size(qgemm, gpu):
@@ -143,6 +156,9 @@ def test_blockscale_e8m0_bench_kernel_full_size(qgemm, gpu):
     _check(y, lambda r, c: O.gemm_bs_e8m0_points(qa, qb, sfa_km, eb, r, c),
            lambda band: O.gemm_bs_e8m0(qa[band], qb, np.ascontiguousarray(sfa_km[:, band]), eb),
            m, n, 64, "bs-e8m0 8192^3")
+    ref = qgemm.reference_gemm("bs_e8m0", dev(qa).view(torch.float8_e4m3fn), dev(qb).view(torch.float8_e4m3fn),
+                               A_scale, dev(eb))
+    assert_close_all(ref, y, "bs-e8m0 8192^3, every output")
 
 
 SWEEP_NK = [(24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168)]
