@@ -107,6 +107,8 @@ EXPORTS = {
                                            ctypes.c_size_t, ctypes.c_void_p]),
     "gemm_a4w4_mxfp4_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), ctypes.c_int]),
     "gemm_a4w4_mxfp4_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_void_p]),
+    "gemm_a4w4_mxfp4_bpreshuffle_kid": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_int,
+                                                       ctypes.c_void_p]),
     "gemm_a8w8_mxfp8": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),
     "gemm_a8w8_mxfp8_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
@@ -310,7 +312,7 @@ def _shuffled_scale(e, rows, kg, name):
 
 
 def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, bpreshuffle=True, *,
-              dtype=None, grid_blocks=0):
+              dtype=None, grid_blocks=0, kernel_id=0):
     """MXFP4 GEMM with aiter's gemm_a4w4 operand formats.
 
     A [M, K/2] packed e2m1 (row-major); B [N, K/2] bytes in
@@ -318,7 +320,9 @@ def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, 
     A_scale / B_scale: E8M0 in e8m0_shuffle order (``e8m0_shuffle``, or
     ``quant_mxfp4(x, shuffle=True)``), rows padded to 32; out [M, N], bf16
     unless ``dtype`` (or a given ``out``) says fp32.  ``grid_blocks`` > 0 runs a persistent grid of that
-    many workgroups.  The epilogue has no bias or alpha/beta: anything but
+    many workgroups.  ``kernel_id``: 0 = the library's choice, 1 = the
+    two-by-two wave 256x256 kernel, 8 = the one-by-four wave kernel (no
+    persistent grid).  The epilogue has no bias or alpha/beta: anything but
     the defaults raises, and so does bpreshuffle=False (row-major B goes
     through gemm_a4w4_mxfp4)."""
     if bias is not None or alpha != 1.0 or beta != 0.0:
@@ -343,7 +347,8 @@ def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, 
                       int(grid_blocks))
     with torch.cuda.device(dev):
         s = _stream(dev)
-        st = lib().gemm_a4w4_mxfp4_bpreshuffle(ctypes.byref(args), _out_code(dtype), ctypes.c_void_p(s.cuda_stream))
+        st = lib().gemm_a4w4_mxfp4_bpreshuffle_kid(ctypes.byref(args), _out_code(dtype), int(kernel_id),
+                                                   ctypes.c_void_p(s.cuda_stream))
         _record(s, A, B, A_scale, B_scale, out)
     _check(st, "gemm_a4w4_mxfp4_bpreshuffle")
     return out

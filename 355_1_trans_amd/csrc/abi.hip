@@ -839,6 +839,48 @@ hipError_t copy_scale_panels(TileArgs& t, const opus_gemm_scale_kargs& a, int pb
     return hipSuccess;
 }
 
+// The one-by-four wave MXFP4 kernel reads its scales in e8m0_shuffle order
+// (per 32-row block and K-tile 256 contiguous bytes): the row-major entry
+// shuffles both operands' scales into the workspace, [A: batch x
+// ceil(M/32) x 32 x K/32][B: batch x ceil(N/32) x 32 x K/32] (each part
+// 256-byte aligned), and the kernel reads them from there.
+size_t quad_plane_bytes(int rows, int k) { return (size_t)ceil_div(rows, 32) * 32 * (size_t)(k / 32); }
+size_t quad_scale_bytes(const opus_gemm_scale_kargs& a) {
+    return round256((size_t)a.batch * quad_plane_bytes(a.m, a.k)) + round256((size_t)a.batch * quad_plane_bytes(a.n, a.k));
+}
+// Both operands' scales into the workspace's shuffled planes: one launch.
+qg::ShuffleArgs quad_shuffle_args(const opus_gemm_scale_kargs& a, const uint8_t* sfa, const uint8_t* sfb, void* ws) {
+    qg::ShuffleArgs sh{};
+    const int kg = a.k / 32, chunks = ceil_div(ceil_div(kg, 8), 16);
+    sh.src[0] = sfa;
+    sh.src[1] = sfb;
+    sh.dst[0] = static_cast<uint8_t*>(ws);
+    sh.dst[1] = sh.dst[0] + round256((size_t)a.batch * quad_plane_bytes(a.m, a.k));
+    sh.rows[0] = a.m;
+    sh.rows[1] = a.n;
+    sh.ld[0] = a.stride_sfa;
+    sh.ld[1] = a.stride_sfb;
+    sh.src_batch[0] = a.stride_sfa_batch;
+    sh.src_batch[1] = a.stride_sfb_batch;
+    sh.dst_batch[0] = (long long)quad_plane_bytes(a.m, a.k);
+    sh.dst_batch[1] = (long long)quad_plane_bytes(a.n, a.k);
+    sh.kg = kg;
+    sh.units[0] = ceil_div(a.m, 32) * chunks;
+    sh.units[1] = ceil_div(a.n, 32) * chunks;
+    return sh;
+}
+hipError_t run_quad(TileArgs t, const opus_gemm_scale_kargs& a, bool bf16, void* ws, hipStream_t stream) {
+    const qg::ShuffleArgs sh = quad_shuffle_args(a, t.sfa, t.sfb, ws);
+    const hipError_t st = qg::launch_e8m0_shuffle_blocks(sh, a.batch, stream);
+    if (st != hipSuccess) return st;
+    t.sfa = sh.dst[0];
+    t.sfb = sh.dst[1];
+    t.sfa_sm = t.sfb_sn = a.k;    // 32 rows x K/32 groups per 32-row block
+    t.sfa_batch = sh.dst_batch[0];
+    t.sfb_batch = sh.dst_batch[1];
+    return qg::launch_quad_mx4(t, a.batch, false, bf16, stream);
+}
+
 hipError_t run_wide_mx(TileArgs t, const opus_gemm_scale_kargs& a, bool fp4, int pb, bool bf16, void* ws,
                        size_t ws_bytes, hipStream_t stream) {
     const int kt_bytes = fp4 ? 8 : 4;
@@ -1198,6 +1240,11 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = r.bd.ws_bytes;
             if (r.bd.splitk > 1 && !have_ws) return r;    // its K slices need the workspace
             break;
+        case QGEMM_KID_QUAD:
+            if (!fp4) return r;
+            r.ws_bytes = quad_scale_bytes(a);
+            if (!have_ws) return r;    // the shuffled scales live in the workspace
+            break;
         default:
             return r;
     }
@@ -1234,6 +1281,8 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
             return run_skinny(sk, t, a.batch, r.pl, bf16, ws, ws_bytes, kt, stream);
         case QGEMM_KID_BAND:
             return run_band(r.bd, t, a.batch, fp4, bf16, ws, stream);
+        case QGEMM_KID_QUAD:
+            return run_quad(t, a, bf16, ws, stream);
         case QGEMM_KID_MID:
             t.sfa_sk = t.sfb_sk = fp4 ? 8 : 4;
             return run_mid(t, a.batch, r.pl, bf16, fp4 ? qg::MidKind::MX4 : qg::MidKind::MX8, ws, ws_bytes, kt,
@@ -1446,11 +1495,15 @@ size_t gemm_a4w4_mxfp4_kid_workspace_bytes(const opus_gemm_scale_kargs* args, in
 }
 
 // ------------------------------------------------ MXFP4, aiter bpreshuffle operands
-hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream) {
+hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, int kernel_id,
+                                           hipStream_t stream) {
     qg::trace_reset();
     if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
         !flag01(out_dtype) || args->grid_blocks < 0)
         return hipErrorInvalidValue;
+    if (kernel_id != QGEMM_KID_AUTO && kernel_id != QGEMM_KID_TILE256 && kernel_id != QGEMM_KID_QUAD)
+        return hipErrorInvalidValue;
+    if (kernel_id == QGEMM_KID_QUAD && args->grid_blocks > 0) return hipErrorInvalidValue;    // one tile per workgroup
     const auto& x = *args;
     if (x.m <= 0 || x.n <= 0 || x.k <= 0 || x.batch <= 0 || x.k % 256 || x.n % 16) return hipErrorInvalidValue;
     const int kb = x.k / 2, rows32a = ceil_div(x.m, 32), rows32b = ceil_div(x.n, 32);
@@ -1489,10 +1542,19 @@ hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, 
     t.sfa_sm = x.stride_sfa;
     t.sfb_sn = x.stride_sfb;
     t.sfa_sk = t.sfb_sk = 256;
+    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
     const long long tiles = (long long)t.tiles_m * t.tiles_n * x.batch;
     const int blocks = x.grid_blocks > 0 ? (int)std::min<long long>(x.grid_blocks, tiles) : 0;
+    // AUTO: the one-by-four wave kernel unless a persistent grid is asked
+    // for (B straight into registers: 8192^3 1.13x over the two-by-two wave
+    // kernel, M = 512-16384 at N, K = 2048-8192 1.0-1.13x, same bits)
+    if (kernel_id == QGEMM_KID_QUAD || (kernel_id == QGEMM_KID_AUTO && blocks == 0))
+        return qg::launch_quad_mx4(t, x.batch, true, bf16, stream);
     // 4 K-tiles of scales per DMA when they come whole (K % 1024 == 0)
     return qg::launch_wide_mx4_w16s(t, x.batch, out_dtype == QGEMM_OUT_BF16, x.k % 1024 == 0 ? 32 : 8, blocks, stream);
+}
+hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream) {
+    return gemm_a4w4_mxfp4_bpreshuffle_kid(args, out_dtype, QGEMM_KID_AUTO, stream);
 }
 
 }  // extern "C"
@@ -2007,6 +2069,16 @@ hipError_t qgemm_e8m0_shuffle_device(const uint8_t* src, uint8_t* dst, int rows,
         return hipErrorInvalidValue;
     hipError_t st = check_arch();
     if (st != hipSuccess) return st;
+    if (aligned(dst, 16) && aligned(src, 4) && ld_src % 4 == 0) {
+        qg::ShuffleArgs sh{};
+        sh.src[0] = src;
+        sh.dst[0] = dst;
+        sh.rows[0] = rows;
+        sh.ld[0] = ld_src;
+        sh.kg = groups_k;
+        sh.units[0] = ceil_div(rows, 32) * ceil_div(ceil_div(groups_k, 8), 16);
+        return qg::launch_e8m0_shuffle_blocks(sh, 1, stream);
+    }
     return qg::launch_e8m0_shuffle(src, dst, rows, groups_k, ld_src, stream);
 }
 

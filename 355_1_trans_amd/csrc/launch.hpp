@@ -33,6 +33,10 @@ hipError_t launch_wide_mx4_raw(const TileArgs& a, int batch, bool bf16, int pane
 hipError_t launch_wide_mx4_w16s(const TileArgs& a, int batch, bool bf16, int panel_bytes, int persist_blocks,
                                 hipStream_t s);
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+// kernels_quad.hip: one-by-four wave 256 x 256 MXFP4 tiles, B straight into
+// registers (W16 or row-major), scales in e8m0_shuffle order (sfa_sm / sfb_sn =
+// bytes per 32-row block); every operand's bytes per batch entry below 2^31
+hipError_t launch_quad_mx4(const TileArgs& a, int batch, bool w16, bool bf16, hipStream_t s);
 // E8M0 block scales with row-major [N][K] B
 hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // E8M0 scales of A and B into the wide kernel's panel-major layout
@@ -103,6 +107,21 @@ hipError_t launch_quant_wgt_blocks(int fmt, bool bf16in, const void* w, long lon
 hipError_t launch_relayout(int layout, const uint8_t* src, uint8_t* dst, int n, int kbytes, long long ld,
                            hipStream_t st);
 hipError_t launch_e8m0_shuffle(const uint8_t* src, uint8_t* dst, int rows, int kg, long long ld, hipStream_t st);
+// e8m0_shuffle of one or two operands over a batch in one launch (quant.hip):
+// operand i: rows[i] x kg row-major bytes at src[i] (pitch ld[i]; src and
+// ld dword aligned) -> dst[i] (16-byte aligned, ceil(rows/32) * 32 *
+// ceil(kg/8) * 8 bytes); units[i] = ceil(rows[i]/32) * ceil(ceil(kg/8)/16)
+// workgroups per batch entry (units[1] = 0: one operand)
+struct ShuffleArgs {
+    const uint8_t* src[2];
+    uint8_t* dst[2];
+    int rows[2];
+    long long ld[2];
+    long long src_batch[2], dst_batch[2];
+    int kg;
+    int units[2];
+};
+hipError_t launch_e8m0_shuffle_blocks(const ShuffleArgs& a, int batch, hipStream_t st);
 // MN-major [K][X] bytes (pitch ld) -> [X][K] row-major, or shuffle_weight(16,16)
 // order with w16; X and K multiples of 64
 hipError_t launch_transpose(bool w16, const uint8_t* src, uint8_t* dst, int x_len, int k_len, long long ld,

@@ -273,6 +273,55 @@ __global__ __launch_bounds__(256) void e8m0_shuffle_kernel(const uint8_t* __rest
     }
 }
 
+// e8m0_shuffle of one or two operands (all batch entries) in one launch: a
+// workgroup turns one 32-row block x 16 K-tiles (128 groups) of row-major
+// E8M0 into 16 contiguous 256-byte shuffled blocks.  Each row's 128-byte run
+// is read with dword loads (8 threads per row) into LDS, and every thread
+// then gathers and writes 16 contiguous destination bytes.  Rows past
+// `rows` and groups past kg read as 0x7F.  Source rows and pitches are
+// dword aligned, destinations 16-byte aligned.
+__global__ __launch_bounds__(256) void e8m0_shuffle_blocks_kernel(const ShuffleArgs a) {
+    __shared__ uint8_t run[32][132];    // 33 dwords per row: the gathers spread over the banks
+    int u = blockIdx.x, op = 0;
+    if (u >= a.units[0]) {
+        u -= a.units[0];
+        op = 1;
+    }
+    const int kg = a.kg, kt8 = (kg + 7) / 8, chunks = (kt8 + 15) / 16;
+    const int rb = u / chunks, ch = u - rb * chunks;
+    const int rows = a.rows[op];
+    const uint8_t* src = a.src[op] + (long long)blockIdx.y * a.src_batch[op];
+    uint8_t* dst = a.dst[op] + (long long)blockIdx.y * a.dst_batch[op];
+    const int t = threadIdx.x, rl = t >> 3, seg = t & 7, row = rb * 32 + rl;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const int g = ch * 128 + seg * 16 + 4 * d;
+        uint32_t v = 0x7F7F7F7Fu;
+        if (row < rows) {
+            const uint8_t* q = src + (long long)row * a.ld[op] + g;
+            if (g + 3 < kg) {
+                v = *(const uint32_t*)q;
+            } else {
+                v = 0;
+                for (int e = 0; e < 4; ++e) v |= (uint32_t)(g + e < kg ? q[e] : 0x7Fu) << (8 * e);
+            }
+        }
+        *(uint32_t*)&run[rl][seg * 16 + 4 * d] = v;
+    }
+    __syncthreads();
+    const int j = t >> 4, kt = ch * 16 + j, w0 = (t & 15) * 16;
+    if (kt >= kt8) return;
+    uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int w = w0 + e;
+        const int r = (w & 1) * 16 + ((w & 63) >> 2), g = j * 8 + ((w & 3) >> 1) * 4 + (w >> 6);
+        o[e >> 2] |= (uint32_t)run[r][g] << (8 * (e & 3));
+    }
+    *(i32x4*)(dst + (long long)rb * 32 * (kt8 * 8) + (long long)kt * 256 + w0) =
+        i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+}
+
 unsigned grid_for(long long units) {
     const long long b = (units + 255) / 256;
     return (unsigned)(b < 8192 ? (b > 0 ? b : 1) : 8192);
@@ -394,6 +443,13 @@ hipError_t launch_relayout(int layout, const uint8_t* src, uint8_t* dst, int n, 
         case 2: relayout_kernel<Lay::FRAG><<<grid, 256, 0, st>>>(src, dst, n, kbytes, ld); trace_launch("relayout<FRAG>"); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_e8m0_shuffle_blocks(const ShuffleArgs& a, int batch, hipStream_t st) {
+    const dim3 grid(a.units[0] + a.units[1], batch);
+    e8m0_shuffle_blocks_kernel<<<grid, 256, 0, st>>>(a);
+    trace_launch("e8m0_shuffle_blocks<%d>", a.units[1] ? 2 : 1);
     return hipGetLastError();
 }
 

@@ -180,6 +180,8 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
 #define QGEMM_KID_BURST   5  /* burst kernel: every load issued up front */
 #define QGEMM_KID_STREAM  6  /* MX only: row-streaming kernel (M <= 8, N >= 256) */
 #define QGEMM_KID_BAND    7  /* MX only: band kernel (M <= 64): 128-256 columns x a K slice, A in LDS */
+#define QGEMM_KID_QUAD    8  /* MXFP4 only: one-by-four wave 256x256 tiles, B straight into registers
+                                (row-major entries: the scales are shuffled into the workspace first) */
 hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
                                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);
@@ -266,6 +268,12 @@ typedef struct opus_gemm_mxfp4_scale_kargs {
  * Needs no workspace. Every shape runs the 256x256 tile kernel (decode
  * shapes run faster through gemm_a4w4_mxfp4 with row-major operands). */
 hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream);
+/* The same with a kernel id: QGEMM_KID_AUTO (the library's choice),
+ * QGEMM_KID_TILE256 (the two-by-two wave 256x256 tile kernel, the only one
+ * that takes grid_blocks > 0) or QGEMM_KID_QUAD (one-by-four waves, B
+ * straight from memory into registers); other ids are rejected. */
+hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, int kernel_id,
+                                           hipStream_t stream);
 
 /* No counterpart in the reference.  gemm_a4w4_mxfp4 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving

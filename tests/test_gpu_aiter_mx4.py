@@ -35,13 +35,18 @@ SHAPES = [(256, 256, 512), (512, 512, 1024), (300, 272, 2048), (1, 1024, 1024), 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_gemm_a4w4_bpreshuffle(qgemm, gpu, m, n, k, dtype):
+@pytest.mark.parametrize("kernel_id", [0, 1])
+def test_gemm_a4w4_bpreshuffle(qgemm, gpu, m, n, k, dtype, kernel_id):
+    """kernel_id 0: the library's choice, the one-by-four wave kernel;
+    1: the two-by-two wave kernel."""
     qa, qb, ea, eb = make_mx4(m, n, k, seed=m + 3 * n + k)
     A, B, SA, SB = _aiter_operands(qa, qb, ea, eb, gpu)
-    y = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype)
+    y = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=kernel_id)
     pb = 32 if k % 1024 == 0 else 8
-    assert qgemm.last_launch() == f"wide_gemm<fp4,MXS,W16,{'bf16' if dtype == torch.bfloat16 else 'fp32'},pb{pb}>"
-    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"a4w4 bpreshuffle {m}x{n}x{k}")
+    f = "bf16" if dtype == torch.bfloat16 else "fp32"
+    want = f"quad_gemm<fp4,MXS,W16,{f}>" if kernel_id == 0 else f"wide_gemm<fp4,MXS,W16,{f},pb{pb}>"
+    assert qgemm.last_launch() == want, qgemm.last_launch()
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"a4w4 bpreshuffle {m}x{n}x{k} ({want})")
 
 
 @pytest.mark.parametrize("m,n,k", [(768, 1280, 1536), (1024, 1024, 2048), (2048, 1024, 7168)])

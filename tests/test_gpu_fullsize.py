@@ -96,7 +96,7 @@ def test_mxfp4_bench_kernel_full_size(qgemm, gpu, m, n, k, kernel):
 
 
 @pytest.mark.parametrize("grid_blocks,kernel", [
-    (0, "wide_gemm<fp4,MXS,W16,bf16,pb32>"),
+    (0, "quad_gemm<fp4,MXS,W16,bf16>"),
     (256, "wide_gemm<fp4,MXS,W16,bf16,pb32,persist256>"),
 ])
 def test_mxfp4_aiter_bench_kernel_full_size(qgemm, gpu, grid_blocks, kernel):

@@ -183,10 +183,13 @@ def test_device_layouts_match_host(qgemm, gpu, n, k):
     assert torch.equal(qgemm.shuffle_b_kpanel(wide[:, :k]), qgemm.shuffle_b_kpanel(B))
 
 
-@pytest.mark.parametrize("rows,kg", [(64, 24), (100, 13), (32, 8), (1, 256)])
+# dword-aligned rows take the block kernel (one 32-row block x 16 K-tiles per
+# workgroup; partial last chunk, padded groups), odd pitches the byte kernel
+@pytest.mark.parametrize("rows,kg", [(64, 24), (100, 13), (32, 8), (1, 256), (300, 1040), (77, 36), (33, 2048)])
 def test_device_e8m0_shuffle(qgemm, gpu, rows, kg):
     e = np.random.default_rng(rows * kg).integers(100, 150, (rows, kg), dtype=np.uint8)
     got = qgemm.e8m0_shuffle(torch.from_numpy(e).to(gpu)).cpu().numpy()
+    assert qgemm.last_launch() == ("e8m0_shuffle" if kg % 4 else "e8m0_shuffle_blocks<1>")
     assert np.array_equal(got, O.e8m0_shuffle(e))
 
 
