@@ -108,7 +108,8 @@ EXPORTS = {
     "gemm_a4w4_mxfp4_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs), ctypes.c_int]),
     "gemm_a4w4_mxfp4_bpreshuffle": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_void_p]),
     "gemm_a4w4_mxfp4_bpreshuffle_kid": (ctypes.c_int, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int, ctypes.c_int,
-                                                       ctypes.c_void_p]),
+                                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Mxfp4Kargs), ctypes.c_int]),
     "gemm_a8w8_mxfp8": (ctypes.c_int, [ctypes.POINTER(Kargs), ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
                                        ctypes.c_void_p]),
     "gemm_a8w8_mxfp8_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Kargs)]),
@@ -312,7 +313,7 @@ def _shuffled_scale(e, rows, kg, name):
 
 
 def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, bpreshuffle=True, *,
-              dtype=None, grid_blocks=0, kernel_id=0):
+              dtype=None, grid_blocks=0, kernel_id=0, workspace=None):
     """MXFP4 GEMM with aiter's gemm_a4w4 operand formats.
 
     A [M, K/2] packed e2m1 (row-major); B [N, K/2] bytes in
@@ -320,9 +321,12 @@ def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, 
     A_scale / B_scale: E8M0 in e8m0_shuffle order (``e8m0_shuffle``, or
     ``quant_mxfp4(x, shuffle=True)``), rows padded to 32; out [M, N], bf16
     unless ``dtype`` (or a given ``out``) says fp32.  ``grid_blocks`` > 0 runs a persistent grid of that
-    many workgroups.  ``kernel_id``: 0 = the library's choice, 1 = the
-    two-by-two wave 256x256 kernel, 8 = the one-by-four wave kernel (no
-    persistent grid).  The epilogue has no bias or alpha/beta: anything but
+    many workgroups.  ``kernel_id``: 0 = the library's choice (M <= 64 on
+    the burst kernel, else the one-by-four wave kernel), 1 = the two-by-two
+    wave 256x256 kernel, 5 = the burst kernel (M <= 64), 8 = the one-by-four
+    wave kernel (no persistent grid).  ``workspace``: as for the other
+    entries (None: a cached buffer when a burst plan splits K; False: none,
+    so only unsplit plans).  The epilogue has no bias or alpha/beta: anything but
     the defaults raises, and so does bpreshuffle=False (row-major B goes
     through gemm_a4w4_mxfp4)."""
     if bias is not None or alpha != 1.0 or beta != 0.0:
@@ -345,11 +349,14 @@ def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, 
     args = Mxfp4Kargs(A.data_ptr(), B.data_ptr(), out.data_ptr(), m, n, k, 1, kb, kb, n, m * kb, n * kb, m * n,
                       A_scale.data_ptr(), B_scale.data_ptr(), sfa, sfb, A_scale.numel(), B_scale.numel(),
                       int(grid_blocks))
+    kid = int(kernel_id)
     with torch.cuda.device(dev):
         s = _stream(dev)
-        st = lib().gemm_a4w4_mxfp4_bpreshuffle_kid(ctypes.byref(args), _out_code(dtype), int(kernel_id),
+        query = lambda a: lib().gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(a, kid)
+        ws_ptr, ws_bytes = _workspace(query, args, workspace, dev, s)
+        st = lib().gemm_a4w4_mxfp4_bpreshuffle_kid(ctypes.byref(args), _out_code(dtype), kid, ws_ptr, ws_bytes,
                                                    ctypes.c_void_p(s.cuda_stream))
-        _record(s, A, B, A_scale, B_scale, out)
+        _record(s, A, B, A_scale, B_scale, out, _ws_tensor(workspace))
     _check(st, "gemm_a4w4_mxfp4_bpreshuffle")
     return out
 

@@ -1495,15 +1495,75 @@ size_t gemm_a4w4_mxfp4_kid_workspace_bytes(const opus_gemm_scale_kargs* args, in
 }
 
 // ------------------------------------------------ MXFP4, aiter bpreshuffle operands
-hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, int kernel_id,
-                                           hipStream_t stream) {
-    qg::trace_reset();
+}  // extern "C"
+
+namespace {
+
+// Route of the aiter-format MXFP4 entry.  AUTO: M <= 64 runs the burst
+// kernel (B in shuffle_weight(16,16) order is the 16x16x128 MFMA's operand
+// order, streamed as whole 1 KB loads; a K split needs the workspace, so
+// without one only unsplit plans) -- its gated plan, else, for M = 33-64,
+// the ungated one: the 256-row tiles of the one-by-four wave kernel leave
+// most CUs idle at these M (graph-replayed, N = 7168, K = 16384: M = 1-32
+// 13-22 us against 68; M = 64 32.8 against 69; N = 2112, K = 7168, M = 64:
+// 12.4 against 33.6).  The one-by-four wave kernel takes the rest, and the
+// decode shapes whose 256-column tiles fill half the CUs over at most 4
+// K-tiles (M = 64, N = 32768, K = 512: 9.7 us against 11.5); a persistent
+// grid (grid_blocks > 0) the two-by-two wave kernel.  A forced id runs that
+// kernel or fails.
+struct Mx4sRoute {
+    int kid = QGEMM_KID_AUTO;
+    bool ok = false;
+    qg::BurstPlan bp;
+    size_t ws_bytes = 0;
+};
+Mx4sRoute route_mx4s(const opus_gemm_mxfp4_scale_kargs& x, int kid, bool have_ws) {
+    Mx4sRoute r;
+    const int kt = x.k / 256;
+    const int cus = device_cus();
+    auto burst = [&](bool gate) {
+        r.bp = qg::burst_plan(x.m, x.n, kt, x.batch, cus, kMaxCounters, gate, 16, true);
+        if (r.bp.ok && r.bp.splitk > 1 && !have_ws) r.bp = qg::burst_plan(x.m, x.n, kt, x.batch, cus, kMaxCounters, gate, 1, true);
+        r.ws_bytes = burst_ws_bytes(r.bp, x.m, x.n, x.batch);
+        return r.bp.ok;
+    };
+    switch (kid) {
+        case QGEMM_KID_AUTO: {
+            r.ok = true;
+            const bool quad_short = 2LL * ceil_div(x.n, 256) * x.batch >= cus && kt <= 4;
+            if (x.grid_blocks > 0) r.kid = QGEMM_KID_TILE256;
+            else if (x.m <= 64 && !quad_short && (burst(true) || (x.m > 32 && burst(false)))) r.kid = QGEMM_KID_BURST;
+            else {
+                r.kid = QGEMM_KID_QUAD;
+                r.bp = qg::BurstPlan{};
+                r.ws_bytes = 0;
+            }
+            return r;
+        }
+        case QGEMM_KID_TILE256:
+            r.kid = kid;
+            r.ok = true;
+            return r;
+        case QGEMM_KID_QUAD:
+            r.kid = kid;
+            r.ok = x.grid_blocks == 0;    // one tile per workgroup
+            return r;
+        case QGEMM_KID_BURST:
+            r.kid = kid;
+            r.ok = x.grid_blocks == 0 && burst(false);
+            return r;
+        default:
+            return r;
+    }
+}
+
+// Validation of the aiter-format MXFP4 operands (MX4 candidate_m10
+// gemm_a4w4_mxfp4_4wave_host.cc:194-250); fills the shared argument block.
+hipError_t validate_mx4s(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, opus_gemm_scale_kargs* common,
+                         Spans* sp) {
     if (!args || !args->ptr_a || !args->ptr_b || !args->ptr_c || !args->ptr_sfa || !args->ptr_sfb ||
         !flag01(out_dtype) || args->grid_blocks < 0)
         return hipErrorInvalidValue;
-    if (kernel_id != QGEMM_KID_AUTO && kernel_id != QGEMM_KID_TILE256 && kernel_id != QGEMM_KID_QUAD)
-        return hipErrorInvalidValue;
-    if (kernel_id == QGEMM_KID_QUAD && args->grid_blocks > 0) return hipErrorInvalidValue;    // one tile per workgroup
     const auto& x = *args;
     if (x.m <= 0 || x.n <= 0 || x.k <= 0 || x.batch <= 0 || x.k % 256 || x.n % 16) return hipErrorInvalidValue;
     const int kb = x.k / 2, rows32a = ceil_div(x.m, 32), rows32b = ceil_div(x.n, 32);
@@ -1526,35 +1586,73 @@ hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* ar
         !bounded_count(x.m, x.stride_c, 1, outb) || !bounded_count(rows32a, x.stride_sfa, 1, 1) ||
         !bounded_count(rows32b, x.stride_sfb, 1, 1))
         return hipErrorInvalidValue;
+    sp->add(x.ptr_c, span(x.batch, x.stride_c_batch, x.m, x.stride_c, x.n, outb));
+    sp->add(x.ptr_a, span(x.batch, x.stride_a_batch, x.m, x.stride_a, kb, 1));
+    sp->add(x.ptr_b, span(x.batch, x.stride_b_batch, 1, 0, (long long)x.n * kb, 1));
+    sp->add(x.ptr_sfa, span(x.batch, x.stride_sfa_batch, rows32a, x.stride_sfa, x.k, 1));
+    sp->add(x.ptr_sfb, span(x.batch, x.stride_sfb_batch, rows32b, x.stride_sfb, x.k, 1));
+    if (sp->overlap_any(sp->p[0], sp->bytes[0], 1)) return hipErrorInvalidValue;
+    std::memcpy(common, &x, sizeof(*common));    // the leading 96 bytes are the common block
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, int kernel_id,
+                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    qg::trace_reset();
     Spans sp;
-    sp.add(x.ptr_c, span(x.batch, x.stride_c_batch, x.m, x.stride_c, x.n, outb));
-    sp.add(x.ptr_a, span(x.batch, x.stride_a_batch, x.m, x.stride_a, kb, 1));
-    sp.add(x.ptr_b, span(x.batch, x.stride_b_batch, 1, 0, (long long)x.n * kb, 1));
-    sp.add(x.ptr_sfa, span(x.batch, x.stride_sfa_batch, rows32a, x.stride_sfa, x.k, 1));
-    sp.add(x.ptr_sfb, span(x.batch, x.stride_sfb_batch, rows32b, x.stride_sfb, x.k, 1));
-    if (sp.overlap_any(sp.p[0], sp.bytes[0], 1)) return hipErrorInvalidValue;
-    hipError_t st = check_arch();
-    if (st != hipSuccess) return st;
     opus_gemm_scale_kargs a{};
-    std::memcpy(&a, &x, sizeof(a));    // the leading 96 bytes are the common block
+    hipError_t st = validate_mx4s(args, out_dtype, &a, &sp);
+    if (st != hipSuccess) return st;
+    const auto& x = *args;
+    const Mx4sRoute r = route_mx4s(x, kernel_id, workspace != nullptr);
+    if (!r.ok) return hipErrorInvalidValue;
+    st = check_workspace(workspace, workspace_bytes, r.ws_bytes, sp);
+    if (st != hipSuccess) return st;
+    st = check_arch();
+    if (st != hipSuccess) return st;
+    const int kb = x.k / 2;
+    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
     TileArgs t{};
-    fill_common(t, a, kb, (int)outb);
+    fill_common(t, a, kb, bf16 ? 2 : 4);
     t.sfa_sm = x.stride_sfa;
     t.sfb_sn = x.stride_sfb;
     t.sfa_sk = t.sfb_sk = 256;
-    const bool bf16 = out_dtype == QGEMM_OUT_BF16;
-    const long long tiles = (long long)t.tiles_m * t.tiles_n * x.batch;
-    const int blocks = x.grid_blocks > 0 ? (int)std::min<long long>(x.grid_blocks, tiles) : 0;
-    // AUTO: the one-by-four wave kernel unless a persistent grid is asked
-    // for (B straight into registers: 8192^3 1.13x over the two-by-two wave
-    // kernel, M = 512-16384 at N, K = 2048-8192 1.0-1.13x, same bits)
-    if (kernel_id == QGEMM_KID_QUAD || (kernel_id == QGEMM_KID_AUTO && blocks == 0))
-        return qg::launch_quad_mx4(t, x.batch, true, bf16, stream);
-    // 4 K-tiles of scales per DMA when they come whole (K % 1024 == 0)
-    return qg::launch_wide_mx4_w16s(t, x.batch, out_dtype == QGEMM_OUT_BF16, x.k % 1024 == 0 ? 32 : 8, blocks, stream);
+    switch (r.kid) {
+        case QGEMM_KID_QUAD:
+            return qg::launch_quad_mx4(t, x.batch, true, bf16, stream);
+        case QGEMM_KID_BURST: {
+            qg::BurstArgs b{};
+            b.t = t;
+            b.splitk = r.bp.splitk;
+            b.kt_per_split = r.bp.kt_per_split;
+            b.n_tiles = r.bp.n_tiles;
+            b.b_bytes = (long long)x.n * kb;
+            if (r.bp.splitk > 1) {
+                b.counters = static_cast<unsigned*>(workspace);
+                b.epoch = next_epoch();
+                b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes);
+            }
+            return qg::launch_burst_mx4s(b, r.bp.mb, r.bp.nb, r.bp.waves, x.batch, bf16, stream);
+        }
+        default: {
+            const long long tiles = (long long)t.tiles_m * t.tiles_n * x.batch;
+            const int blocks = x.grid_blocks > 0 ? (int)std::min<long long>(x.grid_blocks, tiles) : 0;
+            // 4 K-tiles of scales per DMA when they come whole (K % 1024 == 0)
+            return qg::launch_wide_mx4_w16s(t, x.batch, bf16, x.k % 1024 == 0 ? 32 : 8, blocks, stream);
+        }
+    }
+}
+size_t gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(const opus_gemm_mxfp4_scale_kargs* args, int kernel_id) {
+    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->k % 256 || args->batch <= 0) return 0;
+    const Mx4sRoute r = route_mx4s(*args, kernel_id, true);
+    return r.ok ? r.ws_bytes : 0;
 }
 hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream) {
-    return gemm_a4w4_mxfp4_bpreshuffle_kid(args, out_dtype, QGEMM_KID_AUTO, stream);
+    return gemm_a4w4_mxfp4_bpreshuffle_kid(args, out_dtype, QGEMM_KID_AUTO, nullptr, 0, stream);
 }
 
 }  // extern "C"

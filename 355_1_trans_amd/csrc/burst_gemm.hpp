@@ -1,7 +1,10 @@
 // Burst GEMM for decode shapes (M <= 64) on gfx950: every global load of a
 // workgroup's K slice is issued in one burst.  fp8 with fp32 block scales
-// (K-panel B' or fragment-order B''), or MXFP8 / MXFP4 with row-major B and
-// row-major E8M0 scales.
+// (K-panel B' or fragment-order B''), MXFP8 / MXFP4 with row-major B and
+// row-major E8M0 scales, or MXFP4 in aiter's bpreshuffle formats: B in
+// shuffle_weight(16,16) order (for fp4 the same bytes as B'': a 16-row
+// block's K-tile is the two 1 KB operands of the 16x16x128 MFMA) and both
+// scale tensors in e8m0_shuffle order.
 //
 // A decode GEMM streams B once; at configs[0] size (11 MB) the whole launch
 // lasts a few microseconds, so what bounds it is how many bytes are in flight
@@ -152,10 +155,12 @@ template <int FMT, BLay BL, int MB, int NB, int WAVES, int KPW, bool BF16>
 __device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, const int sk, const int bz,
                                            const int batch) {
     constexpr int kBurstWaves = WAVES;
-    // RAW: MXFP8 / MXFP4 with row-major B and E8M0 scales; else fp8 with
-    // fp32 block scales on B' (K-panel) or B'' (fragment order)
-    constexpr bool MX = BL == BLay::RAW;
+    // RAW: MXFP8 / MXFP4 with row-major B and E8M0 scales; fp4 FRAG: MXFP4
+    // with W16 B and e8m0_shuffle scales (MXS); else fp8 with fp32 block
+    // scales on B' (K-panel) or B'' (fragment order)
     constexpr bool FP4 = FMT == kFmtFp4;
+    constexpr bool MXS = FP4 && BL == BLay::FRAG;
+    constexpr bool MX = BL == BLay::RAW || MXS;
     static_assert(BL == BLay::KPANEL || BL == BLay::FRAG || BL == BLay::RAW, "B layout");
     static_assert(MX || !FP4, "fp4 comes with E8M0 scales");
     static_assert((MB == 1 || MB == 2 || MB == 4) && (NB == 1 || NB == 2), "tile shape");
@@ -201,8 +206,10 @@ __device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, co
     // lane L taking row 8h + L/8, 16-byte chunk L%8
     i32x4 av[KPW][MB][2], bv[KPW][NB][2];
     float sa[KPW][MB], sb[KPW];
-    // MX: the row's scale bytes of the K-tile (fp8 one dword, fp4 two)
-    using SX = std::conditional_t<FP4, u32x2, uint32_t>;
+    // MX: the row's scale bytes of the K-tile (fp8 one dword, fp4 two); MXS:
+    // the e8m0_shuffle dword holding the lane's two groups (q and q + 4) for
+    // both 16-row halves of its 32-row block
+    using SX = std::conditional_t<FP4 && !MXS, u32x2, uint32_t>;
     SX xa[KPW][MB], xb[KPW][NB];
     int a_off[MB][2], b_off[NB][2];
 #pragma unroll
@@ -214,10 +221,15 @@ __device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, co
 #pragma unroll
         for (int h = 0; h < 2; ++h) b_off[b][h] = min(n0 + 16 * b + 8 * h + (L >> 3), N - 1) * LDB + (L & 7) * 16;
     int sa_off[MB], xb_off[NB];
+    // MXS dword of row r, lane group q: 32-row block r / 32 (SFA_SM / SFB_SN
+    // bytes each), q * 64 + (r % 16) * 4 within its 256-byte K-tile
+    auto mxs_off = [&](int r, int sm) __attribute__((always_inline)) { return (r >> 5) * sm + q * 64 + (r & 15) * 4; };
 #pragma unroll
-    for (int i = 0; i < MB; ++i) sa_off[i] = min(16 * i + l16, M - 1) * SFA_SM * (MX ? 1 : 4);
+    for (int i = 0; i < MB; ++i)
+        sa_off[i] = MXS ? mxs_off(min(16 * i + l16, M - 1), SFA_SM) : min(16 * i + l16, M - 1) * SFA_SM * (MX ? 1 : 4);
 #pragma unroll
-    for (int b = 0; b < NB; ++b) xb_off[b] = min(n0 + 16 * b + l16, N - 1) * SFB_SN;
+    for (int b = 0; b < NB; ++b)
+        xb_off[b] = MXS ? mxs_off(min(n0 + 16 * b + l16, N - 1), SFB_SN) : min(n0 + 16 * b + l16, N - 1) * SFB_SN;
     const int sb_off = ((min(n0, N - 1) >> 7) * SFB_SN) * 4;
 #pragma unroll
     for (int j = 0; j < KPW; ++j) {
@@ -247,7 +259,13 @@ __device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, co
             for (int h = 0; h < 2; ++h)
                 av[j][i][h] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[i][h],
                                                                                               kt * BKB, 0));
-        if constexpr (MX) {
+        if constexpr (MXS) {
+            // lane (q, r): the dword of its row's block for this K-tile
+#pragma unroll
+            for (int i = 0; i < MB; ++i) xa[j][i] = __builtin_amdgcn_raw_buffer_load_b32(rSA, sa_off[i], kt * 256, 0);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) xb[j][b] = __builtin_amdgcn_raw_buffer_load_b32(rSB, xb_off[b], kt * 256, 0);
+        } else if constexpr (MX) {
             // lane (q, r): the KT_SC scale bytes of its row for this K-tile
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
@@ -321,10 +339,16 @@ __device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, co
         if constexpr (MX) {
             // the lane group's scale byte in byte 0: fp8 byte q of the
             // row's 4; fp4 bytes q (chunk q) and q + 4 (chunk q + 4)
+            // MXS: byte (r % 32) / 16 of the dword for group q, 2 + that
+            // for group q + 4 (rows of B block b: (n0 / 16 + b) % 2)
             int sxb[NB][2];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                if constexpr (FP4) {
+                if constexpr (MXS) {
+                    const int hb = 8 * (((n0 >> 4) + b) & 1);
+                    sxb[b][0] = (int)(xb[j][b] >> hb);
+                    sxb[b][1] = (int)(xb[j][b] >> (hb + 16));
+                } else if constexpr (FP4) {
                     sxb[b][0] = (int)(xb[j][b][0] >> (8 * q));
                     sxb[b][1] = (int)(xb[j][b][1] >> (8 * q));
                 } else {
@@ -336,7 +360,14 @@ __device__ __forceinline__ void burst_tile(const BurstArgs& bp, const int nt, co
                 const QG_LDS uint8_t* as = slot + i * 2048;
                 const i32x4 a0 = *(const QG_LDS i32x4*)(as + frag0), a1 = *(const QG_LDS i32x4*)(as + frag1);
                 if constexpr (FP4) {
-                    const int s0 = (int)(xa[j][i][0] >> (8 * q)), s1 = (int)(xa[j][i][1] >> (8 * q));
+                    int s0, s1;
+                    if constexpr (MXS) {
+                        s0 = (int)(xa[j][i] >> (8 * (i & 1)));
+                        s1 = (int)(xa[j][i] >> (8 * (i & 1) + 16));
+                    } else {
+                        s0 = (int)(xa[j][i][0] >> (8 * q));
+                        s1 = (int)(xa[j][i][1] >> (8 * q));
+                    }
                     const i32x8 a0w = i32x8{a0[0], a0[1], a0[2], a0[3], 0, 0, 0, 0};
                     const i32x8 a1w = i32x8{a1[0], a1[1], a1[2], a1[3], 0, 0, 0, 0};
 #pragma unroll

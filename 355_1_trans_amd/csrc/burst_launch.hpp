@@ -26,13 +26,24 @@ inline bool valid(const BurstGroup& g) {
     return true;
 }
 
+// scale policy of an instantiation: row-major E8M0 (RAW B), e8m0_shuffle
+// (fp4 with W16 = B'' bytes), or fp32 block scales
+template <int FMT, BLay BL>
+constexpr const char* scale_tag() {
+    return BL == BLay::RAW ? "MX" : (FMT == kFmtFp4 && BL == BLay::FRAG) ? "MXS" : "BSF32";
+}
+template <int FMT, BLay BL>
+constexpr bool is_mx() {
+    return BL == BLay::RAW || (FMT == kFmtFp4 && BL == BLay::FRAG);
+}
+
 template <int FMT, BLay BL, int MB, int NB, int W, int KPW>
 hipError_t launch_kpw(const BurstArgs& a, int batch, bool bf16, hipStream_t s) {
     const dim3 grid(a.n_tiles * a.splitk, batch);
     if (bf16) burst_gemm_kernel<FMT, BL, MB, NB, W, KPW, true><<<grid, W * 64, 0, s>>>(a);
     else burst_gemm_kernel<FMT, BL, MB, NB, W, KPW, false><<<grid, W * 64, 0, s>>>(a);
     trace_launch("burst_gemm<%s,%s,%s,mb%d,nb%d,w%d,kpw%d,%s,splitk%d>", FMT == kFmtFp4 ? "fp4" : "fp8",
-                 BL == BLay::RAW ? "MX" : "BSF32", layout_name(BL), MB, NB, W, KPW, bf16 ? "bf16" : "fp32", a.splitk);
+                 scale_tag<FMT, BL>(), layout_name(BL), MB, NB, W, KPW, bf16 ? "bf16" : "fp32", a.splitk);
     return hipGetLastError();
 }
 
@@ -42,7 +53,7 @@ hipError_t launch_kpw(const BurstGroup& g, int grid, bool bf16, hipStream_t s) {
     if (bf16) burst_grouped_kernel<FMT, BL, MB, NB, W, KPW, true><<<grid, W * 64, 0, s>>>(g);
     else burst_grouped_kernel<FMT, BL, MB, NB, W, KPW, false><<<grid, W * 64, 0, s>>>(g);
     trace_launch("burst_grouped<%s,%s,%s,mb%d,nb%d,w%d,kpw%d,%s,g%d,items%d,grid%d>", FMT == kFmtFp4 ? "fp4" : "fp8",
-                 BL == BLay::RAW ? "MX" : "BSF32", layout_name(BL), MB, NB, W, KPW, bf16 ? "bf16" : "fp32", g.count,
+                 scale_tag<FMT, BL>(), layout_name(BL), MB, NB, W, KPW, bf16 ? "bf16" : "fp32", g.count,
                  g.item_begin[g.count], grid);
     return hipGetLastError();
 }
@@ -50,8 +61,7 @@ hipError_t launch_kpw(const BurstGroup& g, int grid, bool bf16, hipStream_t s) {
 // `extent`: the batch count (BurstArgs) or the grid (BurstGroup)
 template <int FMT, BLay BL, int MB, int NB, int W, class Args>
 hipError_t launch_waves(const Args& a, int extent, bool bf16, hipStream_t s) {
-    constexpr bool MX = BL == BLay::RAW;
-    constexpr int KMAX = burst_max_kpw(MB, NB, W, MX);
+    constexpr int KMAX = burst_max_kpw(MB, NB, W, is_mx<FMT, BL>());
     constexpr bool fits = burst_lds_bytes(MB, NB, W, BL != BLay::FRAG) <= kBurstLdsMax && KMAX > 0;
     if constexpr (!fits) {
         return hipErrorInvalidValue;

@@ -79,6 +79,9 @@ struct BurstArgs;
 hipError_t launch_burst(const BurstArgs& a, bool frag, int mb, int nb, int waves, int batch, bool bf16,
                         hipStream_t s);
 // kernels_burst_mx.hip: the same for MXFP8 / MXFP4 (fp4) with row-major B and E8M0 scales
+// kernels_burst_mx4s.hip: MXFP4 with W16 B (= B'' bytes) and e8m0_shuffle
+// scales (sfa_sm / sfb_sn = bytes per 32-row block)
+hipError_t launch_burst_mx4s(const BurstArgs& a, int mb, int nb, int waves, int batch, bool bf16, hipStream_t s);
 hipError_t launch_burst_mx(const BurstArgs& a, bool fp4, int mb, int nb, int waves, int batch, bool bf16,
                            hipStream_t s);
 // kernels_burst_grouped.hip / kernels_burst_mx_grouped.hip: the grouped form

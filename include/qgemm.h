@@ -268,12 +268,21 @@ typedef struct opus_gemm_mxfp4_scale_kargs {
  * Needs no workspace. Every shape runs the 256x256 tile kernel (decode
  * shapes run faster through gemm_a4w4_mxfp4 with row-major operands). */
 hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream);
-/* The same with a kernel id: QGEMM_KID_AUTO (the library's choice),
- * QGEMM_KID_TILE256 (the two-by-two wave 256x256 tile kernel, the only one
- * that takes grid_blocks > 0) or QGEMM_KID_QUAD (one-by-four waves, B
- * straight from memory into registers); other ids are rejected. */
+/* The same with a kernel id and an optional workspace: QGEMM_KID_AUTO (the
+ * library's choice: M <= 64 on the burst kernel where its plan takes the
+ * shape -- B's 16-row blocks are the 16x16x128 MFMA's operand order,
+ * streamed as whole 1 KB loads -- with a K split only when the workspace is
+ * given; otherwise the one-by-four wave kernel, or the two-by-two wave
+ * kernel for grid_blocks > 0), QGEMM_KID_TILE256 (the two-by-two wave 256x256
+ * tile kernel, the only one that takes grid_blocks > 0), QGEMM_KID_QUAD (one-by-
+ * four waves, B straight from memory into registers) or QGEMM_KID_BURST
+ * (M <= 64); other ids, and shapes a forced id cannot take, are rejected.
+ * The workspace (size from the query below, 256-byte aligned, any
+ * contents) carries a burst plan's split-K counters and fp32 partials; the
+ * plain entry above runs without one. */
 hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, int kernel_id,
-                                           hipStream_t stream);
+                                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(const opus_gemm_mxfp4_scale_kargs* args, int kernel_id);
 
 /* No counterpart in the reference.  gemm_a4w4_mxfp4 for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving

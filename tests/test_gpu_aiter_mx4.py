@@ -37,16 +37,71 @@ SHAPES = [(256, 256, 512), (512, 512, 1024), (300, 272, 2048), (1, 1024, 1024), 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("kernel_id", [0, 1])
 def test_gemm_a4w4_bpreshuffle(qgemm, gpu, m, n, k, dtype, kernel_id):
-    """kernel_id 0: the library's choice, the one-by-four wave kernel;
-    1: the two-by-two wave kernel."""
+    """kernel_id 0: the library's choice (the burst kernel for decode M,
+    else the one-by-four wave kernel); 1: the two-by-two wave kernel."""
     qa, qb, ea, eb = make_mx4(m, n, k, seed=m + 3 * n + k)
     A, B, SA, SB = _aiter_operands(qa, qb, ea, eb, gpu)
     y = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=kernel_id)
     pb = 32 if k % 1024 == 0 else 8
     f = "bf16" if dtype == torch.bfloat16 else "fp32"
-    want = f"quad_gemm<fp4,MXS,W16,{f}>" if kernel_id == 0 else f"wide_gemm<fp4,MXS,W16,{f},pb{pb}>"
-    assert qgemm.last_launch() == want, qgemm.last_launch()
-    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"a4w4 bpreshuffle {m}x{n}x{k} ({want})")
+    trace = qgemm.last_launch()
+    if kernel_id == 1:
+        assert trace == f"wide_gemm<fp4,MXS,W16,{f},pb{pb}>", trace
+    elif m <= 64:
+        assert trace.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,")), trace
+    else:
+        assert trace == f"quad_gemm<fp4,MXS,W16,{f}>", trace
+    assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"a4w4 bpreshuffle {m}x{n}x{k} ({trace})")
+
+
+# decode shapes on the burst kernel (W16 B streamed as the 16x16x128 MFMA's
+# 1 KB operands, e8m0_shuffle scales picked by byte): row counts across the
+# 16 / 32 / 64-row tiles, unsplit and K split over workgroups (configs[4]'s
+# N = 7168, K = 16384), a workspace of garbage, and no workspace
+DECODE = [(1, 1024, 1024), (8, 512, 8192), (16, 7168, 2048), (17, 2112, 7168), (32, 4096, 4096),
+          (33, 4096, 256), (48, 1536, 7168), (64, 7168, 2048), (32, 7168, 16384), (1, 7168, 16384)]
+
+
+@pytest.mark.parametrize("m,n,k", DECODE)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_a4w4_decode_burst(qgemm, gpu, m, n, k, dtype):
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=5 * m + n + k)
+    A, B, SA, SB = _aiter_operands(qa, qb, ea, eb, gpu)
+    ref = O.gemm_mx4(qa, qb, ea, eb)
+    args = qgemm.Mxfp4Kargs(A.data_ptr(), B.data_ptr(), 0, m, n, k, 1, k // 2, k // 2, n, 0, 0, 0, SA.data_ptr(),
+                            SB.data_ptr(), k, k, 0, 0, 0)
+    need = qgemm.lib().gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(ctypes.byref(args), 5)
+    junk = torch.full((max(need, 256),), 0xFF, dtype=torch.uint8, device=gpu)
+    y = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=5, workspace=junk)
+    trace = qgemm.last_launch()
+    assert trace.startswith("burst_gemm<fp4,MXS,FRAG,"), trace
+    assert_close(ref, out_to_f32(y), f"a4w4 decode {m}x{n}x{k} ({trace})")
+    y2 = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=5, workspace=junk)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), f"two calls differ ({trace})"
+    # the library's choice: the burst kernel where its plan gate accepts the shape
+    y0 = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype)
+    trace0 = qgemm.last_launch()
+    assert trace0.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,")), trace0
+    assert_close(ref, out_to_f32(y0), f"a4w4 decode auto {m}x{n}x{k} ({trace0})")
+    # no workspace: an unsplit plan, or refused when K needs a split
+    try:
+        yn = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=5, workspace=False)
+    except RuntimeError as e:
+        assert "HIP error 1" in str(e) and need > 0, (trace, str(e))
+    else:
+        tn = qgemm.last_launch()
+        assert tn.endswith(",splitk1>"), tn
+        assert_close(ref, out_to_f32(yn), f"a4w4 decode unsplit {m}x{n}x{k} ({tn})")
+    # the plain entry (no workspace) always answers: burst unsplit or the tile kernel
+    yp = torch.empty_like(y)
+    st = qgemm.lib().gemm_a4w4_mxfp4_bpreshuffle(ctypes.byref(qgemm.Mxfp4Kargs(
+        A.data_ptr(), B.data_ptr(), yp.data_ptr(), m, n, k, 1, k // 2, k // 2, n, 0, 0, 0, SA.data_ptr(),
+        SB.data_ptr(), k, k, 0, 0, 0)), 1 if dtype == torch.bfloat16 else 0,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert_close(ref, out_to_f32(yp), f"a4w4 decode plain entry {m}x{n}x{k} ({qgemm.last_launch()})")
 
 
 @pytest.mark.parametrize("m,n,k", [(768, 1280, 1536), (1024, 1024, 2048), (2048, 1024, 7168)])
