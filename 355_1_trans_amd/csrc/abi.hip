@@ -1515,8 +1515,28 @@ struct Mx4sRoute {
     int kid = QGEMM_KID_AUTO;
     bool ok = false;
     qg::BurstPlan bp;
+    int qsplit = 1;    // QUAD: K slices (batch 1), fp32 partial planes + splitk_reduce
     size_t ws_bytes = 0;
 };
+// K split of the one-by-four wave kernel where its 256 x 256 tiles leave
+// more than half of the CUs idle (middle M, batch 1): equal slices of at
+// least 4 K-tiles, as many as the CUs take while the partial planes (4 bytes
+// per output and slice) stay within twice B's bytes (s <= K / 4M), run as
+// batch entries of the unchanged kernel into fp32 partial planes that
+// splitk_reduce_kernel sums in slice order.  Graph-replayed, us, split /
+// unsplit: N = 7168, K = 16384, M = 128 / 256 / 512: 32.6 / 44.1 / 54.0
+// against 71.3 / 73.3 / 72.7; N = 2112, K = 7168, M = 128 / 256: 19.7 / 27.0
+// against 35.4 / 39.6; M = 1024, N = 4096, K = 7168 split 4 ways (planes 4.6x
+// B's bytes) 59.2 against 36.2, hence the bound.
+int plan_quad_split(const opus_gemm_mxfp4_scale_kargs& x, int cus) {
+    if (x.batch != 1 || (long long)x.m * x.n >= (1LL << 29)) return 1;
+    const int kt = x.k / 256;
+    const long long tiles = (long long)ceil_div(x.m, 256) * ceil_div(x.n, 256);
+    if (2 * tiles >= cus) return 1;
+    int s = (int)std::min<long long>({cus / tiles, kt / 4, x.k / (4LL * x.m)});
+    while (s > 1 && kt % s) --s;
+    return std::max(s, 1);
+}
 Mx4sRoute route_mx4s(const opus_gemm_mxfp4_scale_kargs& x, int kid, bool have_ws) {
     Mx4sRoute r;
     const int kt = x.k / 256;
@@ -1537,6 +1557,10 @@ Mx4sRoute route_mx4s(const opus_gemm_mxfp4_scale_kargs& x, int kid, bool have_ws
                 r.kid = QGEMM_KID_QUAD;
                 r.bp = qg::BurstPlan{};
                 r.ws_bytes = 0;
+                if (have_ws) {
+                    r.qsplit = plan_quad_split(x, cus);
+                    if (r.qsplit > 1) r.ws_bytes = (size_t)r.qsplit * x.m * x.n * 4;
+                }
             }
             return r;
         }
@@ -1622,8 +1646,35 @@ hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* ar
     t.sfb_sn = x.stride_sfb;
     t.sfa_sk = t.sfb_sk = 256;
     switch (r.kid) {
-        case QGEMM_KID_QUAD:
-            return qg::launch_quad_mx4(t, x.batch, true, bf16, stream);
+        case QGEMM_KID_QUAD: {
+            if (r.qsplit <= 1) return qg::launch_quad_mx4(t, x.batch, true, bf16, stream);
+            // K slices as batch entries: A / B / scale offsets of one slice
+            // along K, fp32 output into the partial planes
+            const int slice_kt = x.k / 256 / r.qsplit;
+            TileArgs w = t;
+            w.kbytes = slice_kt * 128;
+            w.a_batch = w.kbytes;
+            w.b_batch = (long long)slice_kt * 2048;    // within each 16-row block
+            w.sfa_batch = w.sfb_batch = (long long)slice_kt * 256;
+            float* part = static_cast<float*>(workspace);
+            w.c = part;
+            w.ldc = x.n;
+            w.c_batch = (long long)x.m * x.n;
+            w.c_vec = x.n % 4 == 0 ? 4 : x.n % 2 == 0 ? 2 : 1;
+            st = qg::launch_quad_mx4(w, r.qsplit, true, false, stream);
+            if (st != hipSuccess) return st;
+            qg::SplitReduceArgs red{};
+            red.ws = part;
+            red.c = t.c;
+            red.m = x.m;
+            red.n = x.n;
+            red.ldc = t.ldc;
+            red.c_vec = t.c_vec;
+            red.splitk = r.qsplit;
+            red.batch = 1;
+            red.c_batch = t.c_batch;
+            return qg::launch_splitk_reduce(red, bf16, stream);
+        }
         case QGEMM_KID_BURST: {
             qg::BurstArgs b{};
             b.t = t;

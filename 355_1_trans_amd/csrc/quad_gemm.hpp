@@ -100,7 +100,9 @@ __device__ __forceinline__ void mfma(f32x16& acc, const i32x4& b, const i32x4& a
 }  // namespace quad
 
 // p: TileArgs with sfa_sm / sfb_sn = e8m0_shuffle bytes per 32-row block
-// (the K-tile step is 256 bytes), tiles_m / tiles_n / group_m set by the host.
+// (the K-tile step is 256 bytes), tiles_m / tiles_n / group_m set by the host;
+// W16 B: ldb = the bytes of K per row (16-row blocks 16 * ldb apart), which
+// exceeds kbytes when batch entries are K slices of one GEMM.
 // (A persistent form of this kernel -- each workgroup walking the tile list
 // and issuing the next tile's first K-tiles during this one's last -- ran
 // 1.1-1.4x slower: the C stores of one tile sit in the in-order vmcnt queue
@@ -146,8 +148,12 @@ __global__ __launch_bounds__(256, 1) void quad_gemm_kernel(const TileArgs p) {
     const uint8_t* B;
     int b_bytes;
     if constexpr (BL == BLay::W16) {
-        B = p.b + bz * p.b_batch + (long long)(n0 >> 4) * 16 * KB;
-        b_bytes = min(((N + 15) >> 4) - (n0 >> 4), BM / 16) * 16 * KB;
+        // 16-row blocks 16 * LDB bytes apart (LDB = the whole row's K bytes;
+        // a K slice of a split launch covers the first KB of each block
+        // from its batch offset on); the range ends with the last block's
+        // slice
+        B = p.b + bz * p.b_batch + (long long)(n0 >> 4) * 16 * LDB;
+        b_bytes = (min(((N + 15) >> 4) - (n0 >> 4), BM / 16) - 1) * 16 * LDB + 16 * KB;
     } else {
         B = p.b + bz * p.b_batch + (long long)n0 * LDB;
         b_bytes = min(N - n0, BM) * LDB;
@@ -192,7 +198,7 @@ __global__ __launch_bounds__(256, 1) void quad_gemm_kernel(const TileArgs p) {
     int boff[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        if constexpr (BL == BLay::W16) boff[h] = (4 * w + 2 * rhi + h) * 16 * KB + g * 256 + rlo * 16;
+        if constexpr (BL == BLay::W16) boff[h] = (4 * w + 2 * rhi + h) * 16 * LDB + g * 256 + rlo * 16;
         else boff[h] = (64 * w + 32 * rhi + 16 * h + rlo) * LDB + g * 16;
     }
     // scale DMA of wave w (one per K-tile): waves 0-1 A's blocks 4(w&1) + L/16,

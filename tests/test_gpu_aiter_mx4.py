@@ -49,8 +49,9 @@ def test_gemm_a4w4_bpreshuffle(qgemm, gpu, m, n, k, dtype, kernel_id):
         assert trace == f"wide_gemm<fp4,MXS,W16,{f},pb{pb}>", trace
     elif m <= 64:
         assert trace.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,")), trace
-    else:
-        assert trace == f"quad_gemm<fp4,MXS,W16,{f}>", trace
+    else:    # (split over K into fp32 planes where the tiles leave most CUs idle)
+        assert trace == f"quad_gemm<fp4,MXS,W16,{f}>" or \
+            trace.startswith(f"quad_gemm<fp4,MXS,W16,fp32>+splitk_reduce<{f},"), trace
     assert_close(O.gemm_mx4(qa, qb, ea, eb), out_to_f32(y), f"a4w4 bpreshuffle {m}x{n}x{k} ({trace})")
 
 
@@ -183,3 +184,26 @@ def test_gemm_a4w4_rejects(qgemm, gpu):
     assert call(stride_sf=256) == 1      # scale block smaller than 32 rows x K/32
     assert call(grid=-1) == 1
     assert call(c=A.data_ptr()) == 1     # C overlapping A
+
+
+# middle M: the one-by-four wave kernel split over K (slices as batch
+# entries into fp32 partial planes, summed by the split-K reduce) where its
+# 256 x 256 tiles would leave most CUs idle
+MIDDLE = [(128, 7168, 16384), (96, 2112, 7168), (256, 4096, 7168), (200, 1536, 2048), (256, 2112, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", MIDDLE)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_a4w4_middle_m_split(qgemm, gpu, m, n, k, dtype):
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=3 * m + n + 7 * k)
+    A, B, SA, SB = _aiter_operands(qa, qb, ea, eb, gpu)
+    ref = O.gemm_mx4(qa, qb, ea, eb)
+    y = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype)
+    trace = qgemm.last_launch()
+    assert trace.startswith("quad_gemm<fp4,MXS,W16,fp32>+splitk_reduce"), trace
+    assert_close(ref, out_to_f32(y), f"a4w4 middle {m}x{n}x{k} ({trace})")
+    # without a workspace the unsplit kernel, the same sums in another order
+    y0 = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, workspace=False)
+    t0 = qgemm.last_launch()
+    assert t0.startswith("quad_gemm<fp4,MXS,W16,") and "splitk" not in t0, t0
+    assert_close(ref, out_to_f32(y0), f"a4w4 middle unsplit {m}x{n}x{k} ({t0})")
