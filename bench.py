@@ -61,6 +61,8 @@ WORKLOADS = {
     "bs_c0": ("bs", 32, 1536, 7168, 0),
     "ldsbypass_c0": ("lbp", 32, 1536, 7168, 0),
     "mxfp4_c4": ("mx4", 32, 7168, 16384, 4),
+    # configs[4] in aiter's formats (W16 weight, e8m0_shuffle scales)
+    "mxfp4_c4_aiter": ("mx4a", 32, 7168, 16384, 4),
     # the reference's headline block-scale kernel (E8M0 1x128 / 128x128 scales,
     # shuffle_weight(16,16) B: 3.31 PFLOPS at 8192^3)
     "bs_e8m0_8192": ("bs8", 8192, 8192, 8192, None),
@@ -68,7 +70,7 @@ WORKLOADS = {
 
 # the other BASELINE configs the default run measures after the headline:
 # (workload, M override)
-EXTRA_WORKLOADS = (("mxfp4_8192", None), ("bs_c0", None), ("mxfp4_c4", 32))
+EXTRA_WORKLOADS = (("mxfp4_8192", None), ("mxfp4_8192_aiter", None), ("bs_c0", None), ("mxfp4_c4", 32))
 
 NAMES = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
          "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
@@ -95,7 +97,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-check", action="store_true", help="skip the output check against the oracle")
     p.add_argument("--no-extra", action="store_true",
-                   help="default run only: skip the extra records (configs[3], configs[0], configs[4] M = 32)")
+                   help="default run only: skip the extra records (configs[3] row-major and in aiter's "
+                        "formats, configs[0], configs[4] M = 32)")
     p.add_argument("--sfa-km", action="store_true",
                    help="block-scale fp32 workloads: pass A's scales column-major [K/128][M] (the reference's "
                         "layout) instead of BASELINE's row-major [M][K/128]")
@@ -205,8 +208,9 @@ def entry_for(L, fam):
     """(launch(kargs_ptr, ws_ptr, ws_bytes, stream), workspace query) of a family."""
     if fam == "bs8":
         return (lambda ka, wp, wb, s: L.launch_blockscale_bpreshuffle(ka, 1, 0, s)), (lambda ka: 0)
-    if fam == "mx4a":
-        return (lambda ka, wp, wb, s: L.gemm_a4w4_mxfp4_bpreshuffle(ka, 1, s)), (lambda ka: 0)
+    if fam == "mx4a":    # the library's choice, with the workspace its decode plans split K in
+        return ((lambda ka, wp, wb, s: L.gemm_a4w4_mxfp4_bpreshuffle_kid(ka, 1, 0, wp, wb, s)),
+                (lambda ka: L.gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(ka, 0)))
     name = {"mx8": "gemm_a8w8_mxfp8", "mx4": "gemm_a4w4_mxfp4", "bs": "gemm_a8w8_blockscale_bpreshuffle",
             "lbp": "gemm_a8w8_blockscale_ldsbypass"}[fam]
     fn = getattr(L, name)
