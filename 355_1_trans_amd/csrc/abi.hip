@@ -1821,18 +1821,10 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
 }
 
 // ------------------------------------------------ E8M0 block scales, NN / TT / TN
-// Each M- or N-contiguous operand is first brought into the NT kernel's
-// operand layout (A [M][K]; B shuffle_weight(16,16) of [N][K]) in the
-// workspace by one transpose pass, and the NT mainloop runs unchanged
-// (TT keeps its row-major [N][K] B and reads it as is).
-size_t gemm_a8w8_blockscale_layout_workspace_bytes(const opus_gemm_scale_kargs* args, int layout) {
-    if (!args || args->m <= 0 || args->n <= 0 || args->k <= 0 || args->batch <= 0 || layout < 0 || layout > 3)
-        return 0;
-    const bool at = layout == QGEMM_LAYOUT_TT || layout == QGEMM_LAYOUT_TN;
-    const bool bn = layout == QGEMM_LAYOUT_NN || layout == QGEMM_LAYOUT_TN;
-    const size_t per_a = (size_t)args->m * args->k, per_b = (size_t)args->n * args->k;
-    return (at ? round256(per_a * args->batch) : 0) + (bn ? round256(per_b * args->batch) : 0);
-}
+// The four-wave tile kernel reads M- or N-contiguous operands as they lie:
+// K-major LDS stages, transposed by ds_read_b64_tr_b8 into the same MFMA
+// operands as the NT path (TT keeps its row-major [N][K] B).  No workspace.
+size_t gemm_a8w8_blockscale_layout_workspace_bytes(const opus_gemm_scale_kargs*, int) { return 0; }
 
 hipError_t gemm_a8w8_blockscale_layout(const opus_gemm_scale_kargs* args, int layout, int output_bf16,
                                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -1862,35 +1854,15 @@ hipError_t gemm_a8w8_blockscale_layout(const opus_gemm_scale_kargs* args, int la
     sp.add(a.ptr_sfa, uint64_t(a.stride_sfa_batch) * a.batch);
     sp.add(a.ptr_sfb, uint64_t(a.stride_sfb_batch) * a.batch);
     if (sp.overlap_any(sp.p[0], sp.bytes[0], 1)) return hipErrorInvalidValue;
-    // the canonical copies need the workspace: NULL is an error here
-    const size_t need = gemm_a8w8_blockscale_layout_workspace_bytes(args, layout);
-    if (!workspace || workspace_bytes < need || !aligned(workspace, 256) || sp.overlap_any(workspace, need, 0))
-        return hipErrorInvalidValue;
+    (void)workspace;
+    (void)workspace_bytes;
     hipError_t st = check_arch();
     if (st != hipSuccess) return st;
-    opus_gemm_scale_kargs c = a;    // the NT view
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    if (at) {
-        st = qg::launch_transpose(false, static_cast<const uint8_t*>(a.ptr_a), ws, a.m, a.k, a.m, a.batch,
-                                  (long long)a.m * a.k, (long long)a.m * a.k, stream);
-        if (st != hipSuccess) return st;
-        c.ptr_a = ws;
-        c.stride_a = a.k;
-        ws += round256((size_t)a.batch * a.m * a.k);
-    }
-    if (bn) {
-        st = qg::launch_transpose(true, static_cast<const uint8_t*>(a.ptr_b), ws, a.n, a.k, a.n, a.batch,
-                                  (long long)a.n * a.k, (long long)a.n * a.k, stream);
-        if (st != hipSuccess) return st;
-        c.ptr_b = ws;
-        c.stride_b = a.k;
-    }
     TileArgs t{};
-    fill_common(t, c, a.k, output_bf16 ? 2 : 4);
+    fill_common(t, a, a.k, output_bf16 ? 2 : 4);
     t.sfa_sk = a.stride_sfa;
     t.sfb_sn = a.stride_sfb;
-    return bn ? qg::launch_wide_bs8_w16(t, a.batch, output_bf16 == 1, stream)
-              : qg::launch_wide_bs8_raw(t, a.batch, output_bf16 == 1, stream);
+    return qg::launch_wide_bs8_kmajor(t, a.batch, output_bf16 == 1, at, bn, stream);
 }
 
 // ------------------------------------------------ block-scale FP8, fp32 scales

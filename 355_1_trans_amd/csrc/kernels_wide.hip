@@ -5,14 +5,14 @@
 namespace qg {
 
 namespace {
-template <int FMT, ScaleKind SK, BLay BL, int PB = 16>
+template <int FMT, ScaleKind SK, BLay BL, int PB = 16, bool AKM = false>
 hipError_t launch_wide(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     const dim3 grid(a.tiles_m * a.tiles_n, 1, batch);
     const dim3 block(256);
-    if (bf16) wide_gemm_kernel<FMT, SK, BL, true, PB><<<grid, block, 0, s>>>(a);
-    else wide_gemm_kernel<FMT, SK, BL, false, PB><<<grid, block, 0, s>>>(a);
-    trace_launch("wide_gemm<%s,%s,%s,%s,pb%d>", FMT == kFmtFp4 ? "fp4" : "fp8", scale_name(SK), layout_name(BL),
-                 bf16 ? "bf16" : "fp32", PB);
+    if (bf16) wide_gemm_kernel<FMT, SK, BL, true, PB, false, AKM><<<grid, block, 0, s>>>(a);
+    else wide_gemm_kernel<FMT, SK, BL, false, PB, false, AKM><<<grid, block, 0, s>>>(a);
+    trace_launch("wide_gemm<%s,%s,%s,%s,pb%d%s>", FMT == kFmtFp4 ? "fp4" : "fp8", scale_name(SK), layout_name(BL),
+                 bf16 ? "bf16" : "fp32", PB, AKM ? ",akm" : "");
     return hipGetLastError();
 }
 // persistent grid of `blocks` workgroups (a.persist = 1, a.batch set)
@@ -55,6 +55,12 @@ hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStrea
 }
 hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::RAW>(a, batch, bf16, s);
+}
+hipError_t launch_wide_bs8_kmajor(const TileArgs& a, int batch, bool bf16, bool a_km, bool b_kn, hipStream_t s) {
+    if (a_km && b_kn) return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::KN, 16, true>(a, batch, bf16, s);
+    if (a_km) return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::RAW, 16, true>(a, batch, bf16, s);
+    if (b_kn) return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::KN>(a, batch, bf16, s);
+    return hipErrorInvalidValue;
 }
 
 // E8M0 scales [rows][ngroups] (row pitch ld) -> panel-major [ngroups/pb][rows][pb]

@@ -39,6 +39,9 @@ hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStrea
 hipError_t launch_quad_mx4(const TileArgs& a, int batch, bool w16, bool bf16, hipStream_t s);
 // E8M0 block scales with row-major [N][K] B
 hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s);
+// K-major operands: A [K][M] (a_km, lda = row pitch >= M) and/or B [K][N]
+// (b_kn, ldb >= N); M and N multiples of 256
+hipError_t launch_wide_bs8_kmajor(const TileArgs& a, int batch, bool bf16, bool a_km, bool b_kn, hipStream_t s);
 // E8M0 scales of A and B into the wide kernel's panel-major layout
 // [ngroups/pb][rows][pb] (pb = 16 or 32 bytes, ngroups % pb == 0)
 struct ScalePanelArgs {
@@ -125,10 +128,6 @@ struct ShuffleArgs {
     int units[2];
 };
 hipError_t launch_e8m0_shuffle_blocks(const ShuffleArgs& a, int batch, hipStream_t st);
-// MN-major [K][X] bytes (pitch ld) -> [X][K] row-major, or shuffle_weight(16,16)
-// order with w16; X and K multiples of 64
-hipError_t launch_transpose(bool w16, const uint8_t* src, uint8_t* dst, int x_len, int k_len, long long ld,
-                            int batch, long long src_batch, long long dst_batch, hipStream_t st);
 
 // ref_gemm.hip: the whole-output reference GEMM (fp64 sums of decoded,
 // scaled products; row-major A [M][K] and B [N][K] codes, lda / ldb in

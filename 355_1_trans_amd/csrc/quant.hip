@@ -327,52 +327,9 @@ unsigned grid_for(long long units) {
     return (unsigned)(b < 8192 ? (b > 0 ? b : 1) : 8192);
 }
 
-// MN-major operand [K][X] (X contiguous, row pitch ld bytes) -> K-contiguous
-// [X][K]: row-major (pitch K) or, with W16, shuffle_weight(16,16) order.
-// 64 x 64-byte tiles through LDS: a thread loads 16 bytes of one K row, then
-// gathers 16 K bytes of one X row (LDS row pitch 68: the four K segments a
-// wave reads at once fall in different banks).  X, K multiples of 64.
-template <bool W16>
-__global__ __launch_bounds__(256) void transpose_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
-                                                        int k_len, long long ld, long long src_batch,
-                                                        long long dst_batch) {
-    constexpr int P = 68;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[64 * P];
-    const int x0 = blockIdx.x * 64, k0 = blockIdx.y * 64, t = threadIdx.x;
-    src += (long long)blockIdx.z * src_batch;
-    dst += (long long)blockIdx.z * dst_batch;
-    {
-        const int k = t >> 2, xs = (t & 3) * 16;
-        const i32x4 v = *(const i32x4*)(src + (long long)(k0 + k) * ld + x0 + xs);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *(int*)(tile + k * P + xs + 4 * j) = v[j];
-    }
-    __syncthreads();
-    const int x = t >> 2, ks = (t & 3) * 16;
-    i32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint8_t* c = tile + (ks + 4 * j) * P + x;
-        o[j] = (int)((uint32_t)c[0] | (uint32_t)c[P] << 8 | (uint32_t)c[2 * P] << 16 | (uint32_t)c[3 * P] << 24);
-    }
-    const long long n = x0 + x, kb = k0 + ks;
-    uint8_t* d = W16 ? dst + (n >> 4) * 16 * k_len + (kb >> 4) * 256 + (n & 15) * 16 : dst + n * k_len + kb;
-    *(i32x4*)d = o;
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
-hipError_t launch_transpose(bool w16, const uint8_t* src, uint8_t* dst, int x_len, int k_len, long long ld,
-                            int batch, long long src_batch, long long dst_batch, hipStream_t st) {
-    if (x_len % 64 || k_len % 64 || ld % 16) return hipErrorInvalidValue;
-    const dim3 grid(x_len / 64, k_len / 64, batch);
-    if (w16) transpose_kernel<true><<<grid, 256, 0, st>>>(src, dst, k_len, ld, src_batch, dst_batch);
-    else transpose_kernel<false><<<grid, 256, 0, st>>>(src, dst, k_len, ld, src_batch, dst_batch);
-    trace_launch("transpose<%s>", w16 ? "W16" : "ROW");
-    return hipGetLastError();
-}
-
 hipError_t launch_quant_rows(int fmt, int group, bool bf16in, bool shuffle, const void* x, long long ldx,
                              uint8_t* q, long long ldq, void* s, long long s_sm, long long s_sk, int rows, int k,
                              hipStream_t st) {

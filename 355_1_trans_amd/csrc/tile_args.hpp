@@ -23,20 +23,23 @@
 // B layouts: RAW [N][Kbytes]; KPANEL [Kbytes/128][N][128] (BPS host.cc:92-111);
 //            W16 shuffle_weight(16,16) [N/16][Kbytes/16][16][16] (SNAP host.cc:161-179);
 //            FRAG this library's B'' for the LDS-bypass entry: per 16-row block and
-//            128-byte K-tile, 2048 contiguous bytes in 16x16x128 operand order.
+//            128-byte K-tile, 2048 contiguous bytes in 16x16x128 operand order;
+//            KN  [K][N] N-contiguous (row pitch ldb >= N): aiter's NN / TN B
+//            (opus_mxfp8_layouts_trace_8192_20261027T005846Z/capture.py:42-62), fp8
+//            only, read from LDS with the transposing ds_read_b64_tr_b8.
 #pragma once
 #include "common.hpp"
 
 namespace qg {
 
 enum class ScaleKind : int { MX = 0, BS8 = 1, BSF32 = 2, MXS = 3 };
-enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2, FRAG = 3 };
+enum class BLay : int { RAW = 0, KPANEL = 1, W16 = 2, FRAG = 3, KN = 4 };
 
 constexpr const char* scale_name(ScaleKind k) {
     return k == ScaleKind::MX ? "MX" : k == ScaleKind::BS8 ? "BS8" : k == ScaleKind::MXS ? "MXS" : "BSF32";
 }
 constexpr const char* layout_name(BLay l) {
-    return l == BLay::RAW ? "RAW" : l == BLay::KPANEL ? "KPANEL" : l == BLay::W16 ? "W16" : "FRAG";
+    return l == BLay::RAW ? "RAW" : l == BLay::KPANEL ? "KPANEL" : l == BLay::W16 ? "W16" : l == BLay::FRAG ? "FRAG" : "KN";
 }
 
 struct TileArgs {

@@ -41,6 +41,19 @@
 // (fp8: r & 7; fp4: (r >> 1) & 7) so both the DMA writes and the fragment
 // reads are conflict free.  Scale policies (MX panels, BS8) and B layouts:
 // tile_args.hpp.
+//
+// K-major operands (fp8 only): B in [K][N] (BL = KN) and, with AKM, A in
+// [K][M] are staged as they lie -- a K-tile is 128 K-rows of the tile's 256
+// columns, rows of 256 bytes in LDS, the 16 chunks of 16 columns swizzled by
+// chunk ^ kn_swz(k) -- and transposed on the way out of LDS by
+// ds_read_b64_tr_b8: within each 16-lane group, output lane i receives byte
+// (i % 8) of the 8-byte pieces addressed by lanes 2j + (i / 8), j = 0..7, as
+// its bytes j.  Lane 2j + h of group q addresses K-row k0 + j, columns
+// 8h..8h+7 of the 16-column block, so lane 16q + r ends up with the eight K
+// values k0..k0+7 of column r; four such reads (k0 = 16q, 16q + 8, 64 + 16q,
+// 72 + 16q) build the same 16x16x128 operand the row-major path reads with
+// two ds_read_b128.  The swizzle puts the 16 rows that half a wave touches
+// (k0 + 0..7 of groups q and q + 1) on 16 different chunks: all 64 banks.
 #pragma once
 #include <type_traits>
 #include <utility>
@@ -100,9 +113,16 @@ __device__ __forceinline__ void mfma_fp4(f32x16& acc, const i32x4& b, const i32x
 }
 }  // namespace wide
 
-template <int FMT, ScaleKind SK, BLay BL, bool BF16, int PB = 16, bool PERSIST = false>
+// physical 16-byte chunk of logical chunk c in K-row k of a K-major stage: c ^ kn_swz(k)
+__device__ __forceinline__ int kn_swz(int k) { return (k & 7) | (((k >> 4) & 1) << 3); }
+
+// AKM: A in [K][M] (row pitch lda >= M), for aiter's TT / TN layouts.
+// K-major operands cover whole 256-column tiles (M, N multiples of 256).
+template <int FMT, ScaleKind SK, BLay BL, bool BF16, int PB = 16, bool PERSIST = false, bool AKM = false>
 __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
     constexpr bool FP4 = (FMT == kFmtFp4);
+    constexpr bool BKN = (BL == BLay::KN);
+    static_assert(!FP4 || (!BKN && !AKM), "K-major operands: fp8");
     // MXS (e8m0_shuffle scales) goes with fp4 and shuffle_weight(16,16) B:
     // aiter's gemm_a4w4 bpreshuffle operands
     constexpr bool MXS = (SK == ScaleKind::MXS);
@@ -178,10 +198,12 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         const int w = __builtin_amdgcn_readfirstlane(tid >> 6), L = tid & 63;
         const int wm = w >> 1, wn = w & 1;
 
-        const uint8_t* A = p.a + bz * p.a_batch + (long long)m0 * LDA;
+        const uint8_t* A = p.a + bz * p.a_batch + (AKM ? (long long)m0 : (long long)m0 * LDA);
         const uint8_t* B = p.b + bz * p.b_batch +
                            (BL == BLay::RAW ? (long long)n0 * LDB
-                                            : BL == BLay::KPANEL ? (long long)n0 * BKB : (long long)(n0 >> 4) * 16 * KB);
+                            : BL == BLay::KPANEL ? (long long)n0 * BKB
+                            : BKN                ? (long long)n0
+                                                 : (long long)(n0 >> 4) * 16 * KB);
         const uint8_t* SFA = p.sfa + bz * p.sfa_batch;
         const uint8_t* SFB = p.sfb + bz * p.sfb_batch;
 
@@ -192,15 +214,21 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         // contiguous ([8 chunks][16 rows][16 B], already the 16x16x128 operand
         // order), two linear 1 KB DMAs, read back linearly.  (Gathering W16 into
         // 128-byte rows made every lane of a DMA hit a different cache line:
-        // 18% more cycles per K-tile.) ----
+        // 18% more cycles per K-tile.)  A K-major operand's K-tile is 128 K-rows
+        // of 256 bytes: wave w's DMA t fills K-rows 32w + 4t .. +3, lane L K-row
+        // +L/16, physical chunk L%16. ----
         int aoff[8], boff[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int r = (w * 8 + t) * 8 + (L >> 3);
             const int c = (L & 7) ^ (FP4 ? ((r >> 1) & 7) : (r & 7));
-            aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
+            const int kr = (w * 8 + t) * 4 + (L >> 4);
+            const int kc = ((L & 15) ^ kn_swz(kr)) << 4;
+            if constexpr (AKM) aoff[t] = kr * LDA + kc;
+            else aoff[t] = (min(m0 + r, M - 1) - m0) * LDA + c * 16;
             const int gn = min(n0 + r, N - 1) - n0;
-            if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
+            if constexpr (BKN) boff[t] = kr * LDB + kc;
+            else if constexpr (BL == BLay::RAW) boff[t] = gn * LDB + c * 16;
             else if constexpr (BL == BLay::KPANEL) boff[t] = gn * BKB + c * 16;
             else {
                 const int blk = min((n0 >> 4) + w * 4 + (t >> 1), ((N + 15) >> 4) - 1) - (n0 >> 4);
@@ -252,13 +280,18 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, valid ? 0x7FFFFFFFu : 0u,
                                                      0x00020000);
         };
+        auto a_ktile = [&](int kt) __attribute__((always_inline)) -> const uint8_t* {
+            if constexpr (AKM) return A + (long long)kt * BKB * LDA;
+            else return A + kt * BKB;
+        };
         auto b_ktile = [&](int kt) __attribute__((always_inline)) -> const uint8_t* {
-            if constexpr (BL == BLay::RAW) return B + kt * BKB;
+            if constexpr (BKN) return B + (long long)kt * BKB * LDB;
+            else if constexpr (BL == BLay::RAW) return B + kt * BKB;
             else if constexpr (BL == BLay::KPANEL) return B + (long long)kt * N * BKB;
             else return B + kt * 2048;
         };
         auto dma_a = [&](int kt, bool valid, QG_LDS uint8_t* sA) __attribute__((always_inline)) {
-            const auto r = rsrc(A + kt * BKB, valid);
+            const auto r = rsrc(a_ktile(kt), valid);
 #pragma unroll
             for (int t = 0; t < 8; ++t) dma16_buf(r, sA + (w * 8 + t) * 8 * BKB, aoff[t], 0);
         };
@@ -392,6 +425,15 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
         // hit and put a vmcnt(0) (wait for every DMA in flight) before them.
         int rdw = (l32 >> 4) * 2048 + g * 256 + (l32 & 15) * 16;
         asm("" : "+v"(rdw));
+        // K-major stages: lane 2j + h of group q addresses K-row 16q + j (+8,
+        // +64, +72 for the other three reads), bytes 8h..8h+7 of the logical
+        // chunk wsel * 8 + (16-column block of the wave): chunk bits XOR in
+        // kn_swz(row) = j | (q & 1) << 3 and the wave's column half
+        const int kfl = (l16 >> 1) | ((q & 1) << 3);
+        const int krow = (16 * q + (l16 >> 1)) * 256 + (l16 & 1) * 8;
+        int tra = krow | (((wm * 8) ^ kfl) << 4), trb = krow | (((wn * 8) ^ kfl) << 4);
+        asm("" : "+v"(tra));
+        asm("" : "+v"(trb));
 
         Acc acc[NBLK][NBLK];
 #pragma unroll
@@ -420,6 +462,13 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
                     dst[h][4 * (x >> 1) + s0] = *(const QG_LDS i32x4*)(blk + rd4(s0));
                     dst[h][4 * (x >> 1) + s0 + 1] = *(const QG_LDS i32x4*)(blk + rd4(s0 + 1));
                 }
+            } else if ((is_a && AKM) || (!is_a && BKN)) {
+                const QG_LDS uint8_t* stg = (is_a ? sA : sB) + ((is_a ? tra : trb) ^ ((4 * h + x) << 4));
+                const i32x2 r0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((QG_LDS i32x2*)stg);
+                const i32x2 r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((QG_LDS i32x2*)(stg + 8 * 256));
+                const i32x2 r2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((QG_LDS i32x2*)(stg + 64 * 256));
+                const i32x2 r3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((QG_LDS i32x2*)(stg + 72 * 256));
+                dst[h][x] = i32x8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
             } else {
                 const QG_LDS uint8_t* blk = base + (4 * h + x) * 16 * BKB;
                 const bool lin = BL == BLay::W16 && !is_a;    // W16 blocks: operand order
@@ -486,7 +535,7 @@ __global__ __launch_bounds__(256, 1) void wide_gemm_kernel(const TileArgs p) {
             // the scale DMAs go first, so B2's vmcnt covers them
             const bool more = t + 2 < nk;
             if constexpr ((P + 2) % SPAN == 0) dma_scales(t + 2, more);
-            const auto rA = rsrc(A + (t + 2) * BKB, more);
+            const auto rA = rsrc(a_ktile(t + 2), more);
             const auto rB = rsrc(b_ktile(t + 2), more);
             auto dma_op = [&](int d) __attribute__((always_inline)) {
                 if (d < 8) dma16_buf(rA, sA + (w * 8 + d) * 8 * BKB, aoff[d], 0);

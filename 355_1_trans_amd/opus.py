@@ -40,9 +40,8 @@ _WS = {}
 
 def _scratch(tag, need, dev, stream):
     """A cached device buffer of at least `need` bytes per (tag, device,
-    stream), zero-filled on allocation.  Split-K workspaces (whose counter
-    words every call leaves zero) and the layout entry's transpose copies
-    use different tags, so a copy never lands on counter words."""
+    stream), zero-filled on allocation; the tag separates workspaces of
+    different entries.  A query of zero bytes gives no buffer."""
     if need == 0:
         return None, 0
     key = (tag, dev.index, stream.cuda_stream)

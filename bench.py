@@ -66,7 +66,14 @@ WORKLOADS = {
     # the reference's headline block-scale kernel (E8M0 1x128 / 128x128 scales,
     # shuffle_weight(16,16) B: 3.31 PFLOPS at 8192^3)
     "bs_e8m0_8192": ("bs8", 8192, 8192, 8192, None),
+    # the same GEMM in aiter's other physical layouts (opus_gemm_mxfp8_{nn,tt,tn}):
+    # B [K][N] (NN, TN), A [K][M] (TT, TN), read in place by the tile kernel
+    "bs_e8m0_8192_nn": ("bs8nn", 8192, 8192, 8192, None),
+    "bs_e8m0_8192_tt": ("bs8tt", 8192, 8192, 8192, None),
+    "bs_e8m0_8192_tn": ("bs8tn", 8192, 8192, 8192, None),
 }
+BS8_FAMS = ("bs8", "bs8nn", "bs8tt", "bs8tn")
+LAYOUT_CODE = {"bs8nn": 1, "bs8tt": 2, "bs8tn": 3}   # QGEMM_LAYOUT_*
 
 # the other BASELINE configs the default run measures after the headline:
 # (workload, M override)
@@ -78,7 +85,10 @@ NAMES = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
                  "(shuffle_weight(16,16) B, e8m0_shuffle scales)",
          "bs": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, K-panel B (bpreshuffle)",
          "lbp": "block-scale FP8 GEMM, fp32 1x128 / 128x128 scales, fragment-order B'' (ldsbypass)",
-         "bs8": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, shuffle_weight(16,16) B"}
+         "bs8": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, shuffle_weight(16,16) B",
+         "bs8nn": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, NN layout (B [K][N] N-contiguous)",
+         "bs8tt": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, TT layout (A [K][M] M-contiguous, B [N][K])",
+         "bs8tn": "block-scale FP8 GEMM, E8M0 1x128 / 128x128 scales, TN layout (A [K][M], B [K][N])"}
 
 
 def parse():
@@ -159,7 +169,7 @@ def make_operands(q, fam, M, N, K, dev, sfa_km=False):
         A, SA = q.quant_mxfp4(a)
         B, SB = q.quant_mxfp4(b)
         ops.update(A=A, SA=SA, B=B, SB=SB)
-    elif fam == "bs8":
+    elif fam in BS8_FAMS:
         A, SA = q.quant_fp8_e8m0_blockscale(a, "1x128")          # SA: [M, K/128] view of [K/128][M] bytes
         B, SB = q.quant_fp8_e8m0_blockscale(b, "128x128")
         ops.update(A=A.view(torch.uint8), SA=SA, B=B.view(torch.uint8), SB=SB)
@@ -175,6 +185,11 @@ def make_operands(q, fam, M, N, K, dev, sfa_km=False):
         ops["B"] = q.ldsbypass_pack_b(ops["B"])
     elif fam == "bs8":
         ops["B"] = q.shuffle_weight_16x16(ops["B"])
+    elif fam in ("bs8nn", "bs8tn"):
+        ops["B"] = ops["B"].t().contiguous()                      # [K][N]
+    if fam in ("bs8tt", "bs8tn"):
+        ops["A_raw"] = ops["A"]
+        ops["A"] = ops["A"].t().contiguous()                      # [K][M]
     elif fam == "mx4a":
         ops["B"] = q.shuffle_weight_16x16(ops["B"])
         ops["SA_raw"], ops["SB_raw"] = ops["SA"], ops["SB"]
@@ -193,8 +208,9 @@ def kargs_for(q, fam, M, N, K, A, B, C, SA, SB, sfa_km, grid_blocks=0):
     if fam in ("mx8", "mx4"):
         return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, kb, kb, N, M * kb, N * kb, M * N,
                        SA.data_ptr(), SB.data_ptr(), kg32, kg32, M * kg32, N * kg32)
-    if fam == "bs8":
-        return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, K, K, N, M * K, N * K, M * N,
+    if fam in BS8_FAMS:
+        return q.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, 1, M if fam in ("bs8tt", "bs8tn") else K,
+                       N if fam in ("bs8nn", "bs8tn") else K, N, M * K, N * K, M * N,
                        SA.data_ptr(), SB.data_ptr(), M, kg128, M * kg128, SB.numel())
     sfa_stride = M if sfa_km else (1 if M > 1 else M)
     if fam == "bs":
@@ -208,6 +224,10 @@ def entry_for(L, fam):
     """(launch(kargs_ptr, ws_ptr, ws_bytes, stream), workspace query) of a family."""
     if fam == "bs8":
         return (lambda ka, wp, wb, s: L.launch_blockscale_bpreshuffle(ka, 1, 0, s)), (lambda ka: 0)
+    if fam in LAYOUT_CODE:
+        code = LAYOUT_CODE[fam]
+        return ((lambda ka, wp, wb, s: L.gemm_a8w8_blockscale_layout(ka, code, 1, None, 0, s)),
+                (lambda ka: L.gemm_a8w8_blockscale_layout_workspace_bytes(ka, code)))
     if fam == "mx4a":    # the library's choice, with the workspace its decode plans split K in
         return ((lambda ka, wp, wb, s: L.gemm_a4w4_mxfp4_bpreshuffle_kid(ka, 1, 0, wp, wb, s)),
                 (lambda ka: L.gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(ka, 0)))
@@ -314,7 +334,7 @@ def check_points(O, fam, M, N, K, host, C, sfa_km):
         ref = O.gemm_mx8_points(A, B, SA, SB, rows, cols)
     elif fam in ("mx4", "mx4a"):
         ref = O.gemm_mx4_points(A, B, SA, SB, rows, cols)
-    elif fam == "bs8":
+    elif fam in BS8_FAMS:
         ref = O.gemm_bs_e8m0_points(A, B, SA, SB, rows, cols)     # SA physical [K/128][M]
     else:
         ref = O.gemm_bs_fp32_points(A, B, SA, SB, rows, cols, sfa_layout="km" if sfa_km else "mk")
@@ -325,12 +345,13 @@ def check_points(O, fam, M, N, K, host, C, sfa_km):
 
 def host_copies(fam, ops, sfa_km):
     """Host arrays of the quantized operands in the oracle's layouts."""
-    h = {k: ops[k].cpu().numpy() for k in ("A", "B_raw", "SB")}
+    h = {k: ops[k].cpu().numpy() for k in ("B_raw", "SB")}
+    h["A"] = ops.get("A_raw", ops["A"]).cpu().numpy()           # [M][K] for the oracle
     sa = ops["SA"]
     if fam == "mx4a":                                           # the row-major scales
         h["SB"] = ops["SB_raw"].cpu().numpy()
         sa = ops["SA_raw"]
-    if fam == "bs8":
+    if fam in BS8_FAMS:
         h["SA"] = sa.t().contiguous().cpu().numpy()               # physical [K/128][M]
     elif fam in ("bs", "lbp") and sfa_km:
         h["SA"] = sa.t().contiguous().cpu().numpy()
@@ -350,7 +371,7 @@ def cpu_baseline(O, fam, M, N, K, h, sfa_km, seconds):
     elif fam in ("mx4", "mx4a"):
         fn = lambda r: O.gemm_mx4(A[r], B, SA[r], SB)
         which = "MX4 gemm_ref_gpu grouped form (gemm_a4w4_mxfp4_4wave_host.cc:66-94)"
-    elif fam == "bs8":
+    elif fam in BS8_FAMS:
         fn = lambda r: O.gemm_bs_e8m0(A[r], B, np.ascontiguousarray(SA[:, r]), SB)
         which = "SNAP gemm_ref (gemm_a8w8_blockscale_bpreshuffle_host.cc:219-248)"
     else:

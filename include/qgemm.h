@@ -118,10 +118,12 @@ hipError_t launch_blockscale_bpreshuffle(const opus_gemm_scale_kargs* args, int 
  *   TT  A [K,M] M-contiguous (stride_a = M); B [N,K] row-major (stride_b = K)
  *   TN  A [K,M]; B [K,N]
  * Scales, C, shape and density rules as launch_blockscale_bpreshuffle
- * (stride_a_batch = M*K, stride_b_batch = N*K). NN / TT / TN bring each
- * M- or N-contiguous operand into the NT operand layout inside `workspace`
- * (gemm_a8w8_blockscale_layout_workspace_bytes; required, 256-byte aligned,
- * no overlap) and run the NT kernel. */
+ * (stride_a_batch = M*K, stride_b_batch = N*K). NN / TT / TN read the M- or
+ * N-contiguous operands in place (K-major LDS stages, transposed on the
+ * LDS read into the NT kernel's MFMA operands; results bit-identical to NT
+ * on the same data). `workspace` is not used (may be NULL):
+ * gemm_a8w8_blockscale_layout_workspace_bytes returns 0, kept so callers
+ * written against a workspace-taking form keep working. */
 #define QGEMM_LAYOUT_NT 0
 #define QGEMM_LAYOUT_NN 1
 #define QGEMM_LAYOUT_TT 2

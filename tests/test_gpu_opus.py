@@ -113,7 +113,8 @@ def _e8m0_inputs(m, n, k, seed):
     return a, b, sfa_km, sfb
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 512, 384), (512, 256, 1024), (768, 512, 2048)])
+@pytest.mark.parametrize("m,n,k", [(256, 512, 384), (512, 256, 1024), (768, 512, 2048), (256, 256, 128),
+                                   (512, 768, 640), (1024, 1280, 256)])
 @pytest.mark.parametrize("layout", ["nt", "nn", "tt", "tn"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_e8m0_layouts(qgemm, gpu, m, n, k, layout, dtype):
@@ -128,9 +129,12 @@ def test_e8m0_layouts(qgemm, gpu, m, n, k, layout, dtype):
     out = torch.empty(m, n, dtype=dtype, device=gpu)
     getattr(qgemm, f"opus_gemm_mxfp8_{layout}")(A, B, sfa, torch.from_numpy(sfb).to(gpu), out)
     launched = qgemm.last_launch()
-    want = {"nt": "wide_gemm<fp8,BS8,W16", "nn": "transpose<W16>+wide_gemm<fp8,BS8,W16",
-            "tt": "transpose<ROW>+wide_gemm<fp8,BS8,RAW", "tn": "transpose<ROW>+transpose<W16>+wide_gemm<fp8,BS8,W16"}
-    assert launched.startswith(want[layout]), launched
+    f = "bf16" if dtype == torch.bfloat16 else "fp32"
+    # NN / TT / TN: the M- or N-contiguous operands go through the kernel's
+    # K-major LDS stages (transposing LDS reads), no transpose pass
+    want = {"nt": f"wide_gemm<fp8,BS8,W16,{f},pb16>", "nn": f"wide_gemm<fp8,BS8,KN,{f},pb16>",
+            "tt": f"wide_gemm<fp8,BS8,RAW,{f},pb16,akm>", "tn": f"wide_gemm<fp8,BS8,KN,{f},pb16,akm>"}
+    assert launched == want[layout], launched
     assert_close(ref, out_to_f32(out), f"{layout} {m}x{n}x{k}")
 
 
@@ -143,14 +147,36 @@ def test_layout_entry_rejects(qgemm, gpu):
     L = qgemm.lib()
     args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, 1, k, n, n, m * k, n * k, m * n,
                        SA.data_ptr(), SB.data_ptr(), m, k // 128, m * (k // 128), SB.numel())
-    need = L.gemm_a8w8_blockscale_layout_workspace_bytes(ctypes.byref(args), 1)
-    assert need == n * k
-    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    assert L.gemm_a8w8_blockscale_layout_workspace_bytes(ctypes.byref(args), 1) == 0   # no copies
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 1, 1, None, 0, s) == 1          # workspace required
-    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 1, 1, ws.data_ptr(), need - 256, s) == 1
-    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 4, 1, ws.data_ptr(), need, s) == 1   # layout code
-    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 2, 1, ws.data_ptr(), need, s) == 1   # TT strides
-    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 1, 1, ws.data_ptr(), need, s) == 0
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 4, 1, None, 0, s) == 1   # layout code
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 2, 1, None, 0, s) == 1   # TT strides
+    bad = qgemm.Kargs(*[getattr(args, f) for f, _ in qgemm.Kargs._fields_])
+    bad.n = 384                                                                         # N % 256
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(bad), 1, 1, None, 0, s) == 1
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(args), 1, 1, None, 0, s) == 0
+    assert qgemm.last_launch() == "wide_gemm<fp8,BS8,KN,bf16,pb16>"
     torch.cuda.synchronize()
     assert_close(O.gemm_bs_e8m0(a, b, sfa_km, sfb), out_to_f32(C), "NN through the C ABI")
+
+
+@pytest.mark.parametrize("layout", [1, 2, 3])
+def test_layout_entry_batch2(qgemm, gpu, layout):
+    """Batched K-major operands through the C ABI: each batch entry of A
+    [K][M] (TT, TN) and B [K][N] (NN, TN) at its dense batch stride."""
+    m, n, k, batch = 512, 256, 768, 2
+    at, bn = layout in (2, 3), layout in (1, 3)
+    data = [_e8m0_inputs(m, n, k, seed=40 + i) for i in range(batch)]
+    A = _fp8(np.stack([d[0].T if at else d[0] for d in data]), gpu)
+    B = _fp8(np.stack([d[1].T if bn else d[1] for d in data]), gpu)
+    SA = torch.from_numpy(np.stack([d[2] for d in data])).to(gpu)
+    SB = torch.from_numpy(np.stack([d[3] for d in data])).to(gpu)
+    C = torch.full((batch, m, n), float("nan"), dtype=torch.float32, device=gpu)
+    kg = k // 128
+    args = qgemm.Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, m if at else k, n if bn else k, n,
+                       m * k, n * k, m * n, SA.data_ptr(), SB.data_ptr(), m, kg, m * kg, (n // 128) * kg)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert qgemm.lib().gemm_a8w8_blockscale_layout(ctypes.byref(args), layout, 0, None, 0, s) == 0
+    torch.cuda.synchronize()
+    for i, d in enumerate(data):
+        assert_close(O.gemm_bs_e8m0(*d), out_to_f32(C[i]), f"layout {layout} batch {i}")
