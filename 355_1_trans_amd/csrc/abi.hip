@@ -21,6 +21,7 @@
 #include "burst_gemm.hpp"
 #include "decode_gemm.hpp"
 #include "mid_gemm.hpp"
+#include "runs_gemm.hpp"
 #include "stream_gemm.hpp"
 
 static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
@@ -1063,6 +1064,45 @@ hipError_t run_bsf32(const BsfRoute& r, const TileArgs& t, int batch, bool frag,
 // above (row-streaming kernel for M <= 8, burst kernel where its gate
 // accepts, skinny / decode, 128 x 128, 256 x 256 tiles); a forced id runs
 // that family with its own plan or fails for shapes it cannot take.
+// Row-run kernel (runs_gemm.hpp): M <= 64, row-major MX B read in 512-byte
+// runs of each row.  32 columns per workgroup; K slices of at most 64
+// K-tiles (16 stages), more slices while a round of workgroups leaves more
+// than a quarter of the CUs idle and each slice keeps >= 16 K-tiles; a split
+// needs the workspace (counters + fp32 partial planes).
+struct RunsPlan {
+    bool ok = false;
+    int mb = 1, splitk = 1, kt_per_split = 1, n_tiles = 1;
+    size_t ws_bytes = 0;
+};
+RunsPlan plan_runs(int m, int n, int kt, int batch, int cus, bool have_ws) {
+    RunsPlan r;
+    if (m < 1 || m > 64 || n < 1 || kt < 1 || batch < 1) return r;
+    r.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    r.n_tiles = ceil_div(n, qg::kRunsCols);
+    const long long tiles = (long long)r.n_tiles * batch;
+    constexpr int kMaxSlice = 16 * qg::kRunsStage;
+    int split = ceil_div(kt, kMaxSlice);
+    if (have_ws)
+        while (tiles * split * 4 < 3LL * cus && ceil_div(kt, split + 1) >= 16) ++split;
+    const int kps = ceil_div(ceil_div(kt, split), qg::kRunsStage) * qg::kRunsStage;
+    split = ceil_div(kt, kps);
+    if (split > 1) {
+        if (!have_ws || tiles > kMaxCounters || (long long)m * n >= (1LL << 29)) return r;
+        r.ws_bytes = kCounterBytes + (size_t)split * batch * m * n * 4;
+    }
+    r.splitk = split;
+    r.kt_per_split = kps;
+    r.ok = true;
+    return r;
+}
+// its loads take 16 bytes of A / B rows and of scale rows per lane
+bool runs_ok(const opus_gemm_scale_kargs& a) {
+    if (!dma_aligned(a, false) || a.stride_b % 16 || !aligned(a.ptr_sfa, 16) || !aligned(a.ptr_sfb, 16) ||
+        a.stride_sfa % 16 || a.stride_sfb % 16)
+        return false;
+    return a.batch == 1 || (a.stride_sfa_batch % 16 == 0 && a.stride_sfb_batch % 16 == 0);
+}
+
 struct MxRoute {
     int kid = QGEMM_KID_AUTO;
     bool ok = false;
@@ -1070,6 +1110,7 @@ struct MxRoute {
     StreamPlan sp;
     qg::BurstPlan bp;
     BandPlan bd;
+    RunsPlan rn;
     int wsplit = 1;    // K slices of the four-wave kernel (plan_wide_split)
     size_t ws_bytes = 0;
 };
@@ -1165,6 +1206,23 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
                                    r.pl.skinny || r.pl.mid ? 0 : r.ws_bytes});
             r.ok = true;
+            if (a.m > 40 && a.m <= 64 && kt >= 64 && (long long)ceil_div(a.n, qg::kRunsCols) * a.batch <= 128 &&
+                have_ws && runs_ok(a)) {
+                // the row-run kernel at narrow N and long K, M = 41-64: its
+                // 32-column tiles split K to fill the CUs while reading B in
+                // 512-byte row runs (graph-replayed, M = 48 / 56 / 64, N =
+                // 2112 / 4096, K = 16384: MXFP4 1.04-1.26x, MXFP8 1.14-1.38x
+                // over the skinny plans, e.g. MXFP8 M = 64, N = 2112 36.8 ->
+                // 26.6 us; at N = 7168 it is within 4% either way, at N =
+                // 16384 or K <= 7168 up to 1.5x slower: not taken there)
+                const RunsPlan rn = plan_runs(a.m, a.n, kt, a.batch, cus, true);
+                if (rn.ok) {
+                    r.rn = rn;
+                    r.kid = QGEMM_KID_RUNS;
+                    r.ws_bytes = std::max(r.ws_bytes, rn.ws_bytes);
+                    return r;
+                }
+            }
             if (a.m > 16 && band_ok(a)) {
                 // the band kernel when one unsplit round of bands covers
                 // three quarters of the CUs: it reads each B row once with
@@ -1245,6 +1303,12 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = quad_scale_bytes(a);
             if (!have_ws) return r;    // the shuffled scales live in the workspace
             break;
+        case QGEMM_KID_RUNS:
+            if (!runs_ok(a)) return r;
+            r.rn = plan_runs(a.m, a.n, kt, a.batch, cus, have_ws);
+            if (!r.rn.ok) return r;
+            r.ws_bytes = r.rn.ws_bytes;
+            break;
         default:
             return r;
     }
@@ -1275,6 +1339,20 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
                 b.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
             }
             return qg::launch_burst_mx(b, fp4, r.bp.mb, r.bp.nb, r.bp.waves, a.batch, bf16, stream);
+        }
+        case QGEMM_KID_RUNS: {
+            qg::RunsArgs x{};
+            x.t = t;
+            x.splitk = r.rn.splitk;
+            x.kt_per_split = r.rn.kt_per_split;
+            x.n_tiles = r.rn.n_tiles;
+            x.b_bytes = (long long)(a.n - 1) * a.stride_b + (fp4 ? a.k / 2 : a.k);
+            if (r.rn.splitk > 1) {
+                x.counters = static_cast<unsigned*>(ws);
+                x.epoch = next_epoch();
+                x.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
+            }
+            return qg::launch_runs(x, fp4, r.rn.mb, a.batch, bf16, stream);
         }
         case QGEMM_KID_SKINNY:
         case QGEMM_KID_DECODE:

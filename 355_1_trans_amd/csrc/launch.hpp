@@ -95,6 +95,10 @@ hipError_t launch_burst_grouped(const BurstGroup& g, bool frag, int mb, int nb, 
                                 hipStream_t s);
 hipError_t launch_burst_mx_grouped(const BurstGroup& g, bool fp4, int mb, int nb, int waves, int grid, bool bf16,
                                    hipStream_t s);
+// kernels_runs.hip: row-run decode kernel (MXFP8 / MXFP4, row-major B, M <= 16 mb,
+// 32 columns per workgroup; 16-byte aligned rows and scale rows)
+struct RunsArgs;
+hipError_t launch_runs(const RunsArgs& a, bool fp4, int mb, int batch, bool bf16, hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);

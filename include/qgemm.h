@@ -184,6 +184,8 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
 #define QGEMM_KID_BAND    7  /* MX only: band kernel (M <= 64): 128-256 columns x a K slice, A in LDS */
 #define QGEMM_KID_QUAD    8  /* MXFP4 only: one-by-four wave 256x256 tiles, B straight into registers
                                 (row-major entries: the scales are shuffled into the workspace first) */
+#define QGEMM_KID_RUNS    9  /* MX only: row-run decode kernel (M <= 64): B rows read in 512-byte runs,
+                                32 columns per workgroup; 16-byte aligned A / B rows and scale rows */
 hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
                                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);

@@ -73,7 +73,7 @@ def test_mx_random_shapes(qgemm, gpu, family, case):
     name = "gemm_a4w4_mxfp4_kid" if fp4 else "gemm_a8w8_mxfp8_kid"
     dt = torch.bfloat16 if bf16 else torch.float32
     launched = 0
-    for kid, C, trace in _run_ids(qgemm, gpu, name, args, range(9), dt, m, n, batch):
+    for kid, C, trace in _run_ids(qgemm, gpu, name, args, range(10), dt, m, n, batch):
         launched += 1
         for i in range(batch):
             assert_close(refs[i], out_to_f32(C[i]), f"{family} {m}x{n}x{k} b{i} kid {kid} ({trace})")
