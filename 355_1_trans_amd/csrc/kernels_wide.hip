@@ -53,9 +53,6 @@ hipError_t launch_wide_mx4_w16s(const TileArgs& a, int batch, bool bf16, int pan
 hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
     return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::W16>(a, batch, bf16, s);
 }
-hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s) {
-    return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::RAW>(a, batch, bf16, s);
-}
 hipError_t launch_wide_bs8_kmajor(const TileArgs& a, int batch, bool bf16, bool a_km, bool b_kn, hipStream_t s) {
     if (a_km && b_kn) return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::KN, 16, true>(a, batch, bf16, s);
     if (a_km) return launch_wide<kFmtFp8, ScaleKind::BS8, BLay::RAW, 16, true>(a, batch, bf16, s);

@@ -37,8 +37,6 @@ hipError_t launch_wide_bs8_w16(const TileArgs& a, int batch, bool bf16, hipStrea
 // registers (W16 or row-major), scales in e8m0_shuffle order (sfa_sm / sfb_sn =
 // bytes per 32-row block); every operand's bytes per batch entry below 2^31
 hipError_t launch_quad_mx4(const TileArgs& a, int batch, bool w16, bool bf16, hipStream_t s);
-// E8M0 block scales with row-major [N][K] B
-hipError_t launch_wide_bs8_raw(const TileArgs& a, int batch, bool bf16, hipStream_t s);
 // K-major operands: A [K][M] (a_km, lda = row pitch >= M) and/or B [K][N]
 // (b_kn, ldb >= N); M and N multiples of 256
 hipError_t launch_wide_bs8_kmajor(const TileArgs& a, int batch, bool bf16, bool a_km, bool b_kn, hipStream_t s);
