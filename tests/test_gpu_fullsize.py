@@ -160,6 +160,21 @@ def test_blockscale_e8m0_bench_kernel_full_size(qgemm, gpu):
                                A_scale, dev(eb))
     assert_close_all(ref, y, "bs-e8m0 8192^3, every output")
 
+    # the same GEMM in the NN / TT / TN layouts (bench.py --workload
+    # bs_e8m0_8192_{nn,tt,tn}): the K-major operands feed the same MFMAs in
+    # the same K order, so every output equals the NT result bit for bit
+    A_km = dev(qa).t().contiguous().view(torch.float8_e4m3fn)          # [K, M]
+    B_kn = dev(qb).t().contiguous().view(torch.float8_e4m3fn)          # [K, N]
+    B_nk = dev(qb).view(torch.float8_e4m3fn)                           # [N, K]
+    for layout, A_op, B_op, kern in (("nn", dev(qa).view(torch.float8_e4m3fn), B_kn, "wide_gemm<fp8,BS8,KN,bf16,pb16>"),
+                                     ("tt", A_km, B_nk, "wide_gemm<fp8,BS8,RAW,bf16,pb16,akm>"),
+                                     ("tn", A_km, B_kn, "wide_gemm<fp8,BS8,KN,bf16,pb16,akm>")):
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        getattr(qgemm, f"opus_gemm_mxfp8_{layout}")(A_op, B_op, A_scale, dev(eb), out)
+        assert qgemm.last_launch() == kern, (layout, qgemm.last_launch())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), y.view(torch.int16)), f"{layout.upper()} 8192^3 differs from NT"
+
 
 SWEEP_NK = [(24576, 1536), (32768, 512), (7168, 16384), (4096, 7168), (7168, 2048), (2112, 7168)]
 SWEEP_M = [1, 16, 64, 256, 1024, 4096, 16384]
