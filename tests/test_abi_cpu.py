@@ -401,3 +401,53 @@ def test_grouped_validation_and_workspace(qgemm):
     if not torch.cuda.is_available():
         assert fn(ok, 3, 1, 0, None, 0, None) != HIP_INVALID_VALUE       # valid: stops at the device check
         assert fn(split, 2, 1, 256, ws, need, None) != HIP_INVALID_VALUE
+
+
+def test_layout_entry_contract(qgemm):
+    """NN / TT / TN read their operands in place: the workspace query is 0
+    for every layout, and the entry refuses (before any device work) a
+    layout code out of range, strides that do not match the layout, and
+    M or N not a multiple of 256."""
+    L = qgemm.lib()
+    m, n, k = 512, 768, 1024
+    base = [(1 << 44) + (i << 38) for i in range(5)]
+
+    def kargs(layout, **over):
+        at, bn = layout in (2, 3), layout in (1, 3)
+        a = qgemm.Kargs(base[0], base[1], base[2], m, n, k, 1, m if at else k, n if bn else k, n, m * k, n * k,
+                        m * n, base[3], base[4], m, k // 128, m * (k // 128), (n // 128) * (k // 128))
+        for f, v in over.items():
+            setattr(a, f, v)
+        return a
+
+    for layout in range(4):
+        assert L.gemm_a8w8_blockscale_layout_workspace_bytes(ctypes.byref(kargs(layout)), layout) == 0
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(kargs(1)), 4, 1, None, 0, None) == HIP_INVALID_VALUE
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(kargs(1)), 2, 1, None, 0, None) == HIP_INVALID_VALUE
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(kargs(3, stride_b=k)), 3, 1, None, 0, None) == HIP_INVALID_VALUE
+    assert L.gemm_a8w8_blockscale_layout(ctypes.byref(kargs(1, n=640, stride_c=640, stride_b=640)), 1, 1, None, 0,
+                                         None) == HIP_INVALID_VALUE
+    if not torch.cuda.is_available():
+        # conforming arguments pass validation and stop at the device check
+        for layout in (1, 2, 3):
+            assert L.gemm_a8w8_blockscale_layout(ctypes.byref(kargs(layout)), layout, 1, None, 0, None) \
+                != HIP_INVALID_VALUE
+
+
+def test_runs_kernel_id_contract(qgemm):
+    """QGEMM_KID_RUNS (9): M <= 64, 16-byte aligned scale rows; a K split
+    (more than 64 K-tiles, or narrow N) sizes its workspace as counters +
+    fp32 planes; other shapes answer 0 / hipErrorInvalidValue."""
+    L = qgemm.lib()
+    kid = 9
+    q = lambda a: L.gemm_a4w4_mxfp4_kid_workspace_bytes(ctypes.byref(a), kid)
+    assert q(_far_kargs(qgemm, 65, 7168, 16384, fp4=True)) == 0                  # M > 64
+    assert q(_far_kargs(qgemm, 32, 7168, 256, fp4=True)) == 0                    # 8-byte scale rows
+    assert q(_far_kargs(qgemm, 32, 7168, 16384, fp4=True)) == 0                  # unsplit: no workspace
+    m, n, k = 40, 256, 32768                                                     # 128 K-tiles: split
+    need = q(_far_kargs(qgemm, m, n, k, fp4=True))
+    assert need > 2048 and (need - 2048) % (m * n * 4) == 0
+    a = _far_kargs(qgemm, 32, 7168, 256, fp4=True)
+    assert L.gemm_a4w4_mxfp4_kid(ctypes.byref(a), 1, kid, None, 0, None) == HIP_INVALID_VALUE
+    a = _far_kargs(qgemm, m, n, k, fp4=True)
+    assert L.gemm_a4w4_mxfp4_kid(ctypes.byref(a), 1, kid, None, 0, None) == HIP_INVALID_VALUE   # split needs ws
