@@ -81,7 +81,8 @@ __host__ __device__ constexpr int burst_lds_bytes(int mb, int nb, int waves, boo
 // a cost model fitted to MI355X measurements (graph-replayed launches,
 // M <= 64, K <= 8192, B' and B''): a launch costs ~2.5 us, plus ~25 ns per
 // KB that one CU streams (B and A bytes of a workgroup times the workgroups
-// per CU), plus ~3.4 us when K is split over workgroups (device-coherent
+// per CU), plus ~3.4 us when K is split over workgroups (and, for MX, 0.6
+// us per slice past 4; device-coherent
 // partial stores, counter and loads, one after the other).  ok == false:
 // no burst plan (M > 64, or K too long for 16 waves without a split).
 struct BurstPlan {
@@ -124,7 +125,15 @@ inline BurstPlan burst_plan(int m, int n, int k_tiles, int batch, int cus, long 
             // kernels)
             if (gate && !mx && waves == 16 && m > 16 && 2 * wgs > cus) continue;
             const double kb = (16.0 * nb + m) * kt_per * 128 / 1024.0;
-            const double cost = 2.5 + 0.025 * kb * (double)((wgs + cus - 1) / cus) + (split > 1 ? 3.4 : 0.0);
+            // MX plans: + 0.6 us per slice past 4.  Without it the model took
+            // 8-16 slices of 1-2 K-tiles per wave for MX decode shapes whose
+            // few slices ran 1.2-2.5x faster (graph-replayed, 29 shapes M =
+            // 16-64, N = 512-7168, K = 4096-16384, aiter and row-major: MXFP4
+            // aiter M = 48, N = 1536, K = 8192 18.5 -> 9.1 us, M = 64, N =
+            // 512, K = 4096 13.8 -> 5.6; geometric mean 1.39x, two shapes
+            // 1-5% slower); the fp32 block-scale plans keep the fitted model
+            const double cost = 2.5 + 0.025 * kb * (double)((wgs + cus - 1) / cus) + (split > 1 ? 3.4 : 0.0) +
+                                (mx && split > 4 ? 0.6 * (split - 4) : 0.0);
             if (cost < best.cost_us) {
                 best.ok = true;
                 best.mb = mb;
