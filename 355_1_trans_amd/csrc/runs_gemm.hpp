@@ -123,8 +123,13 @@ __global__ __launch_bounds__(kRunsWaves * 64, 1) void runs_gemm_kernel(const Run
     const uint8_t* B = p.b + bz * p.b_batch;
     const uint8_t* SFA = p.sfa + bz * p.sfa_batch;
     const uint8_t* SFB = p.sfb + bz * p.sfb_batch;
-    auto rsrc = [](const void* base, int bytes) __attribute__((always_inline)) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+    // loads at K offset koff (bytes, wave-uniform) of an operand of `range`
+    // bytes: the base moves by koff and the range shrinks by it, so that the
+    // hardware's bounds check (the VGPR offset against the range; the SGPR
+    // offset is not checked) returns zeros for every byte past the operand
+    auto rsrc = [](const uint8_t* base, int range, int koff) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base) + koff, 0, range > koff ? range - koff : 0,
+                                                 0x00020000);
     };
     // load ranges: each operand's own extent, so the K-tiles past the end of
     // the last row (read and then zeroed) load nothing past the buffer
@@ -132,7 +137,7 @@ __global__ __launch_bounds__(kRunsWaves * 64, 1) void runs_gemm_kernel(const Run
     const int a_range = (M - 1) * LDA + p.kbytes;
     const int sa_range = (M - 1) * SFA_SM + nk * KT_SC, sb_range = (N - 1) * SFB_SN + nk * KT_SC;
 
-    // ---- per-lane load offsets (K offset of the stage goes in soffset) ----
+    // ---- per-lane load offsets (the stage's K offset moves the descriptor's base) ----
     // B load j of wave w: rows 2u, 2u + 1 of the tile (u = 2w + j); lane L:
     // row + L / 32, 16-byte chunk L % 32 of the 512-byte run
     const int run_c = L & 31;              // chunk of the run this lane loads
@@ -165,15 +170,15 @@ __global__ __launch_bounds__(kRunsWaves * 64, 1) void runs_gemm_kernel(const Run
         constexpr int d = decltype(dd)::value;
         const bool live = s < nst;
         const int kt0 = kt_begin + s * ST;
-        const auto rB = rsrc(B, live ? b_range : 0), rA = rsrc(A, live ? a_range : 0);
-        const auto rS = rsrc(sc_is_b ? SFB : SFA, live && sc_job ? (sc_is_b ? sb_range : sa_range) : 0);
+        const auto rB = rsrc(B, live ? b_range : 0, kt0 * BKB), rA = rsrc(A, live ? a_range : 0, kt0 * BKB);
+        const auto rS = rsrc(sc_is_b ? SFB : SFA, live && sc_job ? (sc_is_b ? sb_range : sa_range) : 0, kt0 * KT_SC);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            bq[d][j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, b_off[j], kt0 * BKB, 2));
+            bq[d][j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rB, b_off[j], 0, 2));
 #pragma unroll
         for (int j = 0; j < MB; ++j)
-            aq[d][j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[j], kt0 * BKB, 0));
-        sq[d] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rS, sc_off, kt0 * KT_SC, 0));
+            aq[d][j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, a_off[j], 0, 0));
+        sq[d] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rS, sc_off, 0, 0));
     };
     // register slot d -> LDS buffer of stage s, K-tiles past the slice as zeros
     auto write = [&](auto dd, int s) __attribute__((always_inline)) {
