@@ -22,6 +22,7 @@
 #include "decode_gemm.hpp"
 #include "mid_gemm.hpp"
 #include "runs_gemm.hpp"
+#include "slice_gemm.hpp"
 #include "stream_gemm.hpp"
 
 static_assert(sizeof(opus_gemm_scale_kargs) == 96, "reference kargs ABI is 96 bytes");
@@ -1095,6 +1096,27 @@ RunsPlan plan_runs(int m, int n, int kt, int batch, int cus, bool have_ws) {
     r.ok = true;
     return r;
 }
+// Slice kernel (slice_gemm.hpp): M <= 64; 16 slice_nbw(mb) columns per
+// workgroup and K slices of slice_kps(mb) K-tiles (A's slice is 128 KB of
+// LDS); a split needs the workspace.
+RunsPlan plan_slice(int m, int n, int kt, int batch, bool have_ws) {
+    RunsPlan r;
+    if (m < 1 || m > 64 || n < 1 || kt < 1 || batch < 1) return r;
+    r.mb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    r.n_tiles = ceil_div(n, 16 * qg::slice_nbw(r.mb));
+    const long long tiles = (long long)r.n_tiles * batch;
+    const int kps = qg::slice_kps(r.mb);
+    const int split = ceil_div(kt, kps);
+    if (split > 255) return r;    // the counters' 8-bit arrival count
+    if (split > 1) {
+        if (!have_ws || tiles > kMaxCounters || (long long)m * n >= (1LL << 29)) return r;
+        r.ws_bytes = kCounterBytes + (size_t)split * batch * m * n * 4;
+    }
+    r.splitk = split;
+    r.kt_per_split = kps;
+    r.ok = true;
+    return r;
+}
 // its loads take 16 bytes of A / B rows and of scale rows per lane
 bool runs_ok(const opus_gemm_scale_kargs& a) {
     if (!dma_aligned(a, false) || a.stride_b % 16 || !aligned(a.ptr_sfa, 16) || !aligned(a.ptr_sfb, 16) ||
@@ -1206,6 +1228,34 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
                                    r.pl.skinny || r.pl.mid ? 0 : r.ws_bytes});
             r.ok = true;
+            if (a.m > 8 && runs_ok(a)) {
+                // the slice kernel where its plan is one round of 7/10 to all
+                // of the CUs with full K slices (or one slice >= 85% full):
+                // its B streams straight into registers and A's slice is read
+                // once per workgroup (graph-replayed, 96 shapes M = 9-64 x N =
+                // 2112-24576 x K = 4096-16384, both formats: 1.03-1.47x on the
+                // shapes this takes, e.g. MXFP4 M = 64, N = 7168, K = 16384
+                // 26.6 -> 24.6 us, M = 16 16.8 -> 14.2, M = 64, N = 24576,
+                // K = 4096 22.4 -> 15.2, MXFP8 M = 32, N = 4096, K = 16384
+                // 24.2 -> 20.0; a second sweep of the 109 shapes of a DeepSeek-
+                // like grid this rule took: geometric mean 1.13x, up to 1.5x,
+                // one MXFP8 shape 5% slower (M = 24, N = 8192, K = 8192); at two
+                // rounds or short slices it lost up to 1.8x, and 64-row plans
+                // split in two at N = 12288-16384 lost 3-11% to the band
+                // kernel, so those keep the plans below)
+                const RunsPlan sl = plan_slice(a.m, a.n, kt, a.batch, have_ws);
+                if (sl.ok) {
+                    const int kps = qg::slice_kps(sl.mb);
+                    const long long wgs = (long long)sl.n_tiles * sl.splitk * a.batch;
+                    const bool full = kt % kps == 0 || (sl.splitk == 1 && 20 * kt >= 17 * kps);
+                    if (10 * wgs >= 7LL * cus && wgs <= cus && full && !(sl.mb == 4 && sl.splitk == 2)) {
+                        r.rn = sl;
+                        r.kid = QGEMM_KID_SLICE;
+                        r.ws_bytes = std::max(r.ws_bytes, sl.ws_bytes);
+                        return r;
+                    }
+                }
+            }
             if (a.m > 40 && a.m <= 64 && kt >= 64 && (long long)ceil_div(a.n, qg::kRunsCols) * a.batch <= 128 &&
                 have_ws && runs_ok(a)) {
                 // the row-run kernel at narrow N and long K, M = 41-64: its
@@ -1309,6 +1359,12 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             if (!r.rn.ok) return r;
             r.ws_bytes = r.rn.ws_bytes;
             break;
+        case QGEMM_KID_SLICE:
+            if (!runs_ok(a)) return r;
+            r.rn = plan_slice(a.m, a.n, kt, a.batch, have_ws);
+            if (!r.rn.ok) return r;
+            r.ws_bytes = r.rn.ws_bytes;
+            break;
         default:
             return r;
     }
@@ -1340,7 +1396,8 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
             }
             return qg::launch_burst_mx(b, fp4, r.bp.mb, r.bp.nb, r.bp.waves, a.batch, bf16, stream);
         }
-        case QGEMM_KID_RUNS: {
+        case QGEMM_KID_RUNS:
+        case QGEMM_KID_SLICE: {
             qg::RunsArgs x{};
             x.t = t;
             x.splitk = r.rn.splitk;
@@ -1352,7 +1409,8 @@ hipError_t run_mx(const MxRoute& r, TileArgs t, const opus_gemm_scale_kargs& a, 
                 x.epoch = next_epoch();
                 x.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kCounterBytes);
             }
-            return qg::launch_runs(x, fp4, r.rn.mb, a.batch, bf16, stream);
+            return r.kid == QGEMM_KID_SLICE ? qg::launch_slice(x, fp4, r.rn.mb, a.batch, bf16, stream)
+                                            : qg::launch_runs(x, fp4, r.rn.mb, a.batch, bf16, stream);
         }
         case QGEMM_KID_SKINNY:
         case QGEMM_KID_DECODE:

@@ -97,6 +97,9 @@ hipError_t launch_burst_mx_grouped(const BurstGroup& g, bool fp4, int mb, int nb
 // 32 columns per workgroup; 16-byte aligned rows and scale rows)
 struct RunsArgs;
 hipError_t launch_runs(const RunsArgs& a, bool fp4, int mb, int batch, bool bf16, hipStream_t s);
+// kernels_slice.hip: slice decode kernel (the same operands and arguments; 16
+// slice_nbw(mb) columns per workgroup, K slices of slice_kps(mb) K-tiles)
+hipError_t launch_slice(const RunsArgs& a, bool fp4, int mb, int batch, bool bf16, hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);

@@ -186,6 +186,9 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
                                 (row-major entries: the scales are shuffled into the workspace first) */
 #define QGEMM_KID_RUNS    9  /* MX only: row-run decode kernel (M <= 64): B rows read in 512-byte runs,
                                 32 columns per workgroup; 16-byte aligned A / B rows and scale rows */
+#define QGEMM_KID_SLICE  10  /* MX only: slice decode kernel (M <= 64): A's K slice in LDS, B fragments
+                                straight from memory, 32 / 64 / 128 columns per workgroup for M <= 16 /
+                                32 / 64; 16-byte aligned A / B rows and scale rows */
 hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
                                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);

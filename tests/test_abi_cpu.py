@@ -451,3 +451,23 @@ def test_runs_kernel_id_contract(qgemm):
     assert L.gemm_a4w4_mxfp4_kid(ctypes.byref(a), 1, kid, None, 0, None) == HIP_INVALID_VALUE
     a = _far_kargs(qgemm, m, n, k, fp4=True)
     assert L.gemm_a4w4_mxfp4_kid(ctypes.byref(a), 1, kid, None, 0, None) == HIP_INVALID_VALUE   # split needs ws
+
+
+def test_slice_kernel_id_contract(qgemm):
+    """QGEMM_KID_SLICE (10): M <= 64, 16-byte aligned scale rows; K past one
+    slice (64 / 32 / 16 K-tiles for 16 / 32 / 64 A rows) splits and sizes the
+    workspace as counters + fp32 planes; other shapes answer 0 /
+    hipErrorInvalidValue."""
+    L = qgemm.lib()
+    kid = 10
+    q = lambda a: L.gemm_a4w4_mxfp4_kid_workspace_bytes(ctypes.byref(a), kid)
+    assert q(_far_kargs(qgemm, 65, 7168, 16384, fp4=True)) == 0                  # M > 64
+    assert q(_far_kargs(qgemm, 32, 7168, 256, fp4=True)) == 0                    # 8-byte scale rows
+    assert q(_far_kargs(qgemm, 16, 7168, 16384, fp4=True)) == 0                  # one slice: unsplit
+    for m, n, k in ((32, 7168, 16384), (64, 7168, 16384), (40, 256, 8192)):     # split
+        need = q(_far_kargs(qgemm, m, n, k, fp4=True))
+        assert need > 2048 and (need - 2048) % (m * n * 4) == 0, (m, n, k, need)
+    a = _far_kargs(qgemm, 32, 7168, 256, fp4=True)
+    assert L.gemm_a4w4_mxfp4_kid(ctypes.byref(a), 1, kid, None, 0, None) == HIP_INVALID_VALUE
+    a = _far_kargs(qgemm, 32, 7168, 16384, fp4=True)
+    assert L.gemm_a4w4_mxfp4_kid(ctypes.byref(a), 1, kid, None, 0, None) == HIP_INVALID_VALUE   # split needs ws

@@ -64,7 +64,7 @@ def _host(t):
     ("mx8", 64, 16384, 16384, "mid_gemm<fp8,MX,RAW,bf16,st4,ntb,splitk2>+splitk_reduce"),
     ("mx4", 32, 20480, 16384, "mid_gemm<fp4,MX"),
     ("mx4", 64, 16384, 7168, "band_gemm<fp4,mb4"),
-    ("mx8", 32, 12288, 4096, "band_gemm<fp8,mb2"),
+    ("mx8", 32, 12288, 4096, "slice_gemm<fp8,MX,RAW,mb2"),
 ])
 def test_mx_plan_route(qgemm, gpu, fam, m, n, k, expect):
     fp4 = fam == "mx4"

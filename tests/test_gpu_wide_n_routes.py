@@ -9,7 +9,8 @@ oracle.
   K = 2048): the decode kernel;
 * fp32 block scales, N = 8192, K = 7168, M = 32 / 64: the decode kernel
   (M = 32: not the 16-wave burst plan);
-* MXFP8 M = 64 and MXFP4 M = 48 at N = 24576: the 128 x 128 kernel.
+* MXFP8 M = 64 (K = 2048) and MXFP4 M = 48 (K = 4096) at N = 24576: the
+  slice kernel (one round of 192 workgroups, one K slice each).
 
 The expected kernel names assume the 256 CUs of an MI355X.
 """
@@ -70,7 +71,7 @@ def test_mx_wide_n_route(qgemm, gpu, fp4, m, n, k):
     trace = qgemm.last_launch()
     torch.cuda.synchronize()
     if _cus(gpu) == 256:
-        assert trace.startswith("mid_gemm<fp4" if fp4 else "mid_gemm<fp8"), trace
+        assert trace.startswith("slice_gemm<fp4" if fp4 else "slice_gemm<fp8"), trace
     rows, cols = _points(m, n, m + n + k)
     ref = (O.gemm_mx4_points if fp4 else O.gemm_mx8_points)(qa, qb, ea, eb, rows, cols)
     assert_close(ref, y.float().cpu().numpy()[rows, cols], f"{'mx4' if fp4 else 'mx8'} {m}x{n}x{k} ({trace})")
