@@ -1228,6 +1228,26 @@ MxRoute route_mx(const opus_gemm_scale_kargs& a, bool fp4, int kid, bool have_ws
             r.ws_bytes = std::max({r.sp.ok ? r.sp.ws_bytes : 0, r.pl.ws_bytes, burst_ws_bytes(r.bp, a.m, a.n, a.batch),
                                    r.pl.skinny || r.pl.mid ? 0 : r.ws_bytes});
             r.ok = true;
+            if (a.m > 16 && a.m <= 32 && have_ws && band_ok(a)) {
+                // 32-row band plans with long K slices (>= 12 K-tiles) over
+                // 7/10 or more of the CUs, where the slice kernel would split
+                // K: 128 columns of B per workgroup read once, with A's slice
+                // in LDS (graph-replayed, two boxes: MXFP4 configs[4] M = 32
+                // 16.7-18.2 us against 18.9-19.8 for the slice kernel and
+                // 18.6-20.5 for the skinny one; M = 24 / 32, N = 4096-8192,
+                // K = 8192 / 16384, both formats: 8-20% faster than the
+                // slice kernel; unsplit slice plans, N = 12288-16384, keep
+                // the slice kernel, 1.16x over these band plans)
+                const BandPlan bd = plan_band(a.m, a.n, kt, a.batch);
+                const RunsPlan sl = runs_ok(a) ? plan_slice(a.m, a.n, kt, a.batch, true) : RunsPlan{};
+                const long long wgs = (long long)bd.bands * bd.splitk * a.batch;
+                if (bd.ok && bd.splitk > 1 && bd.kps >= 12 && 10 * wgs >= 7LL * cus && (!sl.ok || sl.splitk > 1)) {
+                    r.bd = bd;
+                    r.kid = QGEMM_KID_BAND;
+                    r.ws_bytes = std::max(r.ws_bytes, bd.ws_bytes);
+                    return r;
+                }
+            }
             if (a.m > 8 && runs_ok(a)) {
                 // the slice kernel where its plan is one round of 7/10 to all
                 // of the CUs with full K slices (or one slice >= 85% full):

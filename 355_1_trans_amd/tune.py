@@ -182,7 +182,8 @@ def tune_shape(q, m, n, k, variant, kids, dev, stream):
     return res, alg
 
 
-MX_KIDS = {0: "auto", 1: "tile256", 2: "mid128", 3: "skinny", 4: "decode", 5: "burst", 6: "stream", 7: "band"}
+MX_KIDS = {0: "auto", 1: "tile256", 2: "mid128", 3: "skinny", 4: "decode", 5: "burst", 6: "stream", 7: "band",
+           8: "quad", 9: "runs", 10: "slice"}
 
 
 def tune_shape_mx(q, m, n, k, fp4, kids, dev, stream):
