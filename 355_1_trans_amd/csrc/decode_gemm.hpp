@@ -324,51 +324,67 @@ __global__ __launch_bounds__(NW * 64) void decode_gemm_kernel(const DecodeArgs d
     __syncthreads();
     if (!last_flag) return;
     const float* ws0 = dp.ws + (long long)bz * plane;
-    // MB passes of 4 columns per thread, unrolled so that every pass's
-    // partial loads are in flight together
+    // MB passes of 4 columns per thread; with whole-vector rows every pass's
+    // loads of a group of SG slices are in flight together (one round trip
+    // per group, not one per pass), the slices summed in order 0 .. splitk - 1
     static_assert(ROWS * COLS == MB * NT * 4, "reduction passes");
+    constexpr int SG = 16 / MB < 8 ? 16 / MB : 8;
+    int rm[MB], rn[MB];
+    f32x4 v[MB];
 #pragma unroll
     for (int it = 0; it < MB; ++it) {
         const int x = tid * 4 + it * NT * 4;
-        const int row = x / COLS, col = x % COLS;
-        const int m = row, nn = n0 + col;
-        if (m >= M) continue;
-        const int e = m * N + nn;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (nn + 3 < N && vec_ok) {
-            for (int s0 = 0; s0 < dp.splitk; s0 += 8) {
-                f32x4 u[8];
+        rm[it] = x / COLS;
+        rn[it] = n0 + x % COLS;
+        v[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (vec_ok) {
+        // N % 4 == 0: a thread's 4 columns are all in or all out
+        for (int s0 = 0; s0 < dp.splitk; s0 += SG) {
+            f32x4 u[SG][MB];
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    if (s0 + t < dp.splitk) u[t] = load_partial4(partial_rsrc(ws0 + (s0 + t) * split_stride), e);
+            for (int t = 0; t < SG; ++t)
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    if (s0 + t < dp.splitk)
-                        for (int r = 0; r < 4; ++r) v[r] += u[t][r];
-            }
-        } else {
+                for (int it = 0; it < MB; ++it)
+                    if (s0 + t < dp.splitk && rm[it] < M && rn[it] < N)
+                        u[t][it] = load_partial4(partial_rsrc(ws0 + (s0 + t) * split_stride), rm[it] * N + rn[it]);
+#pragma unroll
+            for (int t = 0; t < SG; ++t)
+#pragma unroll
+                for (int it = 0; it < MB; ++it)
+                    if (s0 + t < dp.splitk && rm[it] < M && rn[it] < N) v[it] += u[t][it];
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < MB; ++it) {
+            if (rm[it] >= M) continue;
             for (int s0 = 0; s0 < dp.splitk; ++s0) {
                 const auto src = partial_rsrc(ws0 + s0 * split_stride);
                 for (int r = 0; r < 4; ++r)
-                    if (nn + r < N) v[r] += load_partial1(src, e + r);
+                    if (rn[it] + r < N) v[it][r] += load_partial1(src, rm[it] * N + rn[it] + r);
             }
         }
+    }
+#pragma unroll
+    for (int it = 0; it < MB; ++it) {
+        const int m = rm[it], nn = rn[it];
+        if (m >= M) continue;
         // the thread's 4 columns start at nn
         if constexpr (BF16) {
             uint16_t* c = (uint16_t*)p.c + bz * p.c_batch + (long long)m * LDC + nn;
             if (nn + 3 < N && p.c_vec >= 4) {
-                *(u32x2*)c = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                *(u32x2*)c = u32x2{pack_bf16x2(v[it][0], v[it][1]), pack_bf16x2(v[it][2], v[it][3])};
             } else {
                 for (int r = 0; r < 4; ++r)
-                    if (nn + r < N) c[r] = bf16_bits(v[r]);
+                    if (nn + r < N) c[r] = bf16_bits(v[it][r]);
             }
         } else {
             float* c = (float*)p.c + bz * p.c_batch + (long long)m * LDC + nn;
             if (nn + 3 < N && p.c_vec >= 4) {
-                *(f32x4*)c = v;
+                *(f32x4*)c = v[it];
             } else {
                 for (int r = 0; r < 4; ++r)
-                    if (nn + r < N) c[r] = v[r];
+                    if (nn + r < N) c[r] = v[it][r];
             }
         }
     }

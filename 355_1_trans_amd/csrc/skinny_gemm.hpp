@@ -504,33 +504,54 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(const Sk
     __syncthreads();
     if (!last_flag) return;
     const float* ws0 = sp.ws + (long long)bz * plane;
-    for (int e = tid * 4; e < ROWS * COLS; e += NT * 4) {
-        const int row = e / COLS, col = e % COLS;
-        const int m = m0 + row, n = n0 + col;
-        if (m >= M) continue;
-        const int x = m * N + n;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (n + 3 < N && vec_ok) {
-            // eight slices in flight per batch of loads, summed in slice order
-            for (int s0 = 0; s0 < sp.splitk; s0 += 8) {
-                f32x4 u[8];
+    // PASSES groups of 4 columns per thread; with whole-vector rows every
+    // pass's loads of a group of SG slices are in flight together, the
+    // slices summed in order 0 .. splitk - 1
+    constexpr int PASSES = (ROWS * COLS + NT * 4 - 1) / (NT * 4);
+    constexpr int SG = 16 / PASSES < 8 ? 16 / PASSES : 8;
+    int rr[PASSES], cc[PASSES];
+    bool live[PASSES];
+    f32x4 v[PASSES];
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    if (s0 + t < sp.splitk) u[t] = load_partial4(partial_rsrc(ws0 + (s0 + t) * split_stride), x);
+    for (int q = 0; q < PASSES; ++q) {
+        const int e = tid * 4 + q * NT * 4;
+        rr[q] = e / COLS;
+        cc[q] = e % COLS;
+        live[q] = e < ROWS * COLS && m0 + rr[q] < M;
+        v[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (vec_ok) {
+        // N % 4 == 0: a thread's 4 columns are all in or all out
+        for (int s0 = 0; s0 < sp.splitk; s0 += SG) {
+            f32x4 u[SG][PASSES];
 #pragma unroll
-                for (int t = 0; t < 8; ++t)
-                    if (s0 + t < sp.splitk)
-                        for (int r = 0; r < 4; ++r) v[r] += u[t][r];
-            }
-        } else {
+            for (int t = 0; t < SG; ++t)
+#pragma unroll
+                for (int q = 0; q < PASSES; ++q)
+                    if (s0 + t < sp.splitk && live[q] && n0 + cc[q] < N)
+                        u[t][q] = load_partial4(partial_rsrc(ws0 + (s0 + t) * split_stride),
+                                                (m0 + rr[q]) * N + n0 + cc[q]);
+#pragma unroll
+            for (int t = 0; t < SG; ++t)
+#pragma unroll
+                for (int q = 0; q < PASSES; ++q)
+                    if (s0 + t < sp.splitk && live[q] && n0 + cc[q] < N) v[q] += u[t][q];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < PASSES; ++q) {
+            if (!live[q]) continue;
+            const int x = (m0 + rr[q]) * N + n0 + cc[q];
             for (int s0 = 0; s0 < sp.splitk; ++s0) {
                 const auto src = partial_rsrc(ws0 + s0 * split_stride);
                 for (int r = 0; r < 4; ++r)
-                    if (n + r < N) v[r] += load_partial1(src, x + r);
+                    if (n0 + cc[q] + r < N) v[q][r] += load_partial1(src, x + r);
             }
         }
-        store4(row, col, v);
     }
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q)
+        if (live[q]) store4(rr[q], cc[q], v[q]);
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -308,7 +308,33 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     if (tid == 0) last_flag = split_arrive(ctr, ra.epoch, ra.splitk);
     __syncthreads();
     if (!last_flag) return;
-    if (owner) {
+    if (owner && n + 3 < N && vec_ok) {
+        // every row block's loads of a group of SG slices in flight before
+        // the adds (one round trip per group, not one per row block); the
+        // slices summed in order 0 .. splitk - 1, this workgroup's own slice
+        // from its registers (the bits it stored)
+        constexpr int SG = 16 / MB < 8 ? 16 / MB : 8;
+        const float* ws0 = ra.ws + (long long)bz * plane;
+        f32x4 sum[MB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) sum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < ra.splitk; s0 += SG) {
+            f32x4 x[SG][MB];
+#pragma unroll
+            for (int s = 0; s < SG; ++s)
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    if (s0 + s < ra.splitk && s0 + s != sk && 16 * i + l16 < M)
+                        x[s][i] = load_partial4(partial_rsrc(ws0 + (s0 + s) * split_stride), (16 * i + l16) * N + n);
+#pragma unroll
+            for (int s = 0; s < SG; ++s)
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    if (s0 + s < ra.splitk && 16 * i + l16 < M) sum[i] += s0 + s == sk ? acc[i] : x[s][i];
+        }
+#pragma unroll
+        for (int i = 0; i < MB; ++i) store_c(16 * i + l16, sum[i]);
+    } else if (owner) {
         const float* ws0 = ra.ws + (long long)bz * plane;
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
@@ -316,24 +342,10 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
             if (m >= M || n >= N) continue;
             const int e = m * N + n;
             f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-            if (n + 3 < N && vec_ok) {
-                for (int s0 = 0; s0 < ra.splitk; s0 += 16) {
-                    f32x4 x[16];
-#pragma unroll
-                    for (int s = 0; s < 16; ++s)
-                        if (s0 + s < ra.splitk) x[s] = load_partial4(partial_rsrc(ws0 + (s0 + s) * split_stride), e);
-#pragma unroll
-                    for (int s = 0; s < 16; ++s)
-                        if (s0 + s < ra.splitk)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) sum[r] += x[s][r];
-                }
-            } else {
-                for (int s = 0; s < ra.splitk; ++s) {
-                    const auto src = partial_rsrc(ws0 + s * split_stride);
-                    for (int r = 0; r < 4; ++r)
-                        if (n + r < N) sum[r] += load_partial1(src, e + r);
-                }
+            for (int s = 0; s < ra.splitk; ++s) {
+                const auto src = partial_rsrc(ws0 + s * split_stride);
+                for (int r = 0; r < 4; ++r)
+                    if (n + r < N) sum[r] += load_partial1(src, e + r);
             }
             store_c(m, sum);
         }
