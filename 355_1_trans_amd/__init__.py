@@ -321,12 +321,13 @@ def gemm_a4w4(A, B, A_scale, B_scale, out=None, bias=None, alpha=1.0, beta=0.0, 
     A_scale / B_scale: E8M0 in e8m0_shuffle order (``e8m0_shuffle``, or
     ``quant_mxfp4(x, shuffle=True)``), rows padded to 32; out [M, N], bf16
     unless ``dtype`` (or a given ``out``) says fp32.  ``grid_blocks`` > 0 runs a persistent grid of that
-    many workgroups.  ``kernel_id``: 0 = the library's choice (M <= 64 on
-    the burst kernel, else the one-by-four wave kernel), 1 = the two-by-two
+    many workgroups.  ``kernel_id``: 0 = the library's choice (M = 9-64 on
+    the slice kernel where its plan fills the CUs in one round, else M <= 64
+    on the burst kernel, else the one-by-four wave kernel), 1 = the two-by-two
     wave 256x256 kernel, 5 = the burst kernel (M <= 64), 8 = the one-by-four
-    wave kernel (no persistent grid).  ``workspace``: as for the other
-    entries (None: a cached buffer when a burst plan splits K; False: none,
-    so only unsplit plans).  The epilogue has no bias or alpha/beta: anything but
+    wave kernel (no persistent grid), 10 = the slice kernel (M <= 64).
+    ``workspace``: as for the other entries (None: a cached buffer when a
+    plan splits K; False: none, so only unsplit plans).  The epilogue has no bias or alpha/beta: anything but
     the defaults raises, and so does bpreshuffle=False (row-major B goes
     through gemm_a4w4_mxfp4)."""
     if bias is not None or alpha != 1.0 or beta != 0.0:

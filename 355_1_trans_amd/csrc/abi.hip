@@ -1671,6 +1671,7 @@ struct Mx4sRoute {
     int kid = QGEMM_KID_AUTO;
     bool ok = false;
     qg::BurstPlan bp;
+    RunsPlan sl;       // SLICE
     int qsplit = 1;    // QUAD: K slices (batch 1), fp32 partial planes + splitk_reduce
     size_t ws_bytes = 0;
 };
@@ -1707,6 +1708,23 @@ Mx4sRoute route_mx4s(const opus_gemm_mxfp4_scale_kargs& x, int kid, bool have_ws
         case QGEMM_KID_AUTO: {
             r.ok = true;
             const bool quad_short = 2LL * ceil_div(x.n, 256) * x.batch >= cus && kt <= 4;
+            if (x.grid_blocks == 0 && x.m > 8 && x.m <= 64) {
+                // the slice kernel on the row-major route's rule (one round of
+                // 7/10 to all of the CUs, full K slices); W16 makes each of its
+                // B fragment loads one 1 KB run
+                const RunsPlan sl = plan_slice(x.m, x.n, kt, x.batch, have_ws);
+                if (sl.ok) {
+                    const int kps = qg::slice_kps(sl.mb);
+                    const long long wgs = (long long)sl.n_tiles * sl.splitk * x.batch;
+                    const bool full = kt % kps == 0 || (sl.splitk == 1 && 20 * kt >= 17 * kps);
+                    if (10 * wgs >= 7LL * cus && wgs <= cus && full) {
+                        r.sl = sl;
+                        r.kid = QGEMM_KID_SLICE;
+                        r.ws_bytes = sl.ws_bytes;
+                        return r;
+                    }
+                }
+            }
             if (x.grid_blocks > 0) r.kid = QGEMM_KID_TILE256;
             else if (x.m <= 64 && !quad_short && (burst(true) || (x.m > 32 && burst(false)))) r.kid = QGEMM_KID_BURST;
             else {
@@ -1731,6 +1749,12 @@ Mx4sRoute route_mx4s(const opus_gemm_mxfp4_scale_kargs& x, int kid, bool have_ws
         case QGEMM_KID_BURST:
             r.kid = kid;
             r.ok = x.grid_blocks == 0 && burst(false);
+            return r;
+        case QGEMM_KID_SLICE:
+            r.kid = kid;
+            r.sl = plan_slice(x.m, x.n, kt, x.batch, have_ws);
+            r.ok = x.grid_blocks == 0 && r.sl.ok;
+            r.ws_bytes = r.sl.ws_bytes;
             return r;
         default:
             return r;
@@ -1830,6 +1854,20 @@ hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* ar
             red.batch = 1;
             red.c_batch = t.c_batch;
             return qg::launch_splitk_reduce(red, bf16, stream);
+        }
+        case QGEMM_KID_SLICE: {
+            qg::RunsArgs ra{};
+            ra.t = t;
+            ra.splitk = r.sl.splitk;
+            ra.kt_per_split = r.sl.kt_per_split;
+            ra.n_tiles = r.sl.n_tiles;
+            ra.b_bytes = (long long)x.n * kb;
+            if (r.sl.splitk > 1) {
+                ra.counters = static_cast<unsigned*>(workspace);
+                ra.epoch = next_epoch();
+                ra.ws = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes);
+            }
+            return qg::launch_slice_mx4s(ra, r.sl.mb, x.batch, bf16, stream);
         }
         case QGEMM_KID_BURST: {
             qg::BurstArgs b{};

@@ -100,6 +100,9 @@ hipError_t launch_runs(const RunsArgs& a, bool fp4, int mb, int batch, bool bf16
 // kernels_slice.hip: slice decode kernel (the same operands and arguments; 16
 // slice_nbw(mb) columns per workgroup, K slices of slice_kps(mb) K-tiles)
 hipError_t launch_slice(const RunsArgs& a, bool fp4, int mb, int batch, bool bf16, hipStream_t s);
+// the same for MXFP4 in aiter's formats: W16 B (b_bytes = N * K / 2) and
+// e8m0_shuffle scales (sfa_sm / sfb_sn = bytes per 32-row block)
+hipError_t launch_slice_mx4s(const RunsArgs& a, int mb, int batch, bool bf16, hipStream_t s);
 // B' (K-panel) -> B'' (fragment order of the LDS-bypass path)
 hipError_t launch_repack_frag(const uint8_t* bk, uint8_t* bpp, int n, int k, int batch, long long bk_batch,
                               long long bpp_batch, hipStream_t s);

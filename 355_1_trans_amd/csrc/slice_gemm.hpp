@@ -40,6 +40,15 @@
 // (fp8: one MFMA; fp4: chunk q in the first MFMA, q + 4 in the second); lane
 // group q's scale byte covers those 32 elements; srcA = B, srcB = A; the
 // accumulator of lane L holds C[m = r][n = 4q .. 4q + 3].
+//
+// W16 (MXFP4 in aiter's gemm_a4w4 bpreshuffle formats): B in
+// shuffle_weight(16,16) order, where a 16-row block's K-tile is 2 KB laid out
+// [8 chunks][16 rows][16 B], so the lane order above makes each fragment
+// load one contiguous 1 KB run; scales in e8m0_shuffle order (per 32-row
+// block and K-tile 256 bytes, the dword at q * 64 + (r % 16) * 4 holding
+// groups q and q + 4 of rows r % 16 and 16 + r % 16).  A's slice of those
+// bytes comes into LDS as it lies; the wave's B scale dword of each K-tile
+// is loaded with its B fragments.
 #pragma once
 #include <utility>
 
@@ -54,10 +63,11 @@ __host__ __device__ constexpr int slice_nbw(int mb) { return mb == 1 ? 2 : (mb =
 __host__ __device__ constexpr int slice_kq(int mb) { return kSliceWaves / slice_nbw(mb); }
 __host__ __device__ constexpr int slice_kps(int mb) { return kSliceKtw * slice_kq(mb); }
 
-template <int FMT, int MB, bool BF16>
+template <int FMT, int MB, bool BF16, bool W16 = false>
 __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const RunsArgs ra) {
     constexpr bool FP4 = FMT == kFmtFp4;
     static_assert(MB == 1 || MB == 2 || MB == 4, "A rows: 16, 32 or 64");
+    static_assert(!W16 || FP4, "W16 / e8m0_shuffle operands: MXFP4");
     constexpr int BKB = 128, KW = kSliceKtw, D = kSliceDepth;
     constexpr int NBW = slice_nbw(MB), KQ = slice_kq(MB), KPS = slice_kps(MB);
     constexpr int RA = 16 * MB, RB = 16 * NBW;
@@ -67,8 +77,10 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     // scales in LDS as [K-tile][row] entries of KT_SC bytes: a fragment's 16
     // rows read one contiguous 64 / 128 bytes
     constexpr int SA_KT = RA * KT_SC, SB_KT = RB * KT_SC;
-    constexpr int OFF_SA = RA * A_ROW, OFF_SB = OFF_SA + KPS * SA_KT;
-    constexpr int LDS_BYTES = OFF_SB + KPS * SB_KT;
+    // W16: A's e8m0_shuffle bytes of the slice, [32-row block][K-tile][256]
+    constexpr int NBA = (RA + 31) / 32, SA_W = NBA * KPS * 256;
+    constexpr int OFF_SA = RA * A_ROW, OFF_SB = OFF_SA + (W16 ? SA_W : KPS * SA_KT);
+    constexpr int LDS_BYTES = W16 ? OFF_SB : OFF_SB + KPS * SB_KT;
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
     static_assert(kSliceWaves * MB * 64 * 16 <= RA * A_ROW, "the waves' partial tiles fit the A image");
     // A loads: 1 KB of one row each, 16 per wave
@@ -80,6 +92,8 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     constexpr int S_PER_WAVE = (S_PIECES / 64 + kSliceWaves - 1) / kSliceWaves;
     constexpr int KT_PER_PIECE = 16 / KT_SC;
     static_assert(RA * SPR % 64 == 0, "A's and B's scale pieces meet at an instruction boundary");
+    constexpr int SW_PIECES = SA_W / 16, SW_PER_WAVE = (SW_PIECES / 64 + kSliceWaves - 1) / kSliceWaves;
+    static_assert(SW_PIECES % 64 == 0, "W16: A's scale pieces fill whole instructions");
     __shared__ __attribute__((aligned(16))) uint8_t lds_mem[LDS_BYTES];
     __shared__ int last_flag;
     QG_LDS uint8_t* const lds = (QG_LDS uint8_t*)lds_mem;
@@ -109,7 +123,10 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     };
     const int b_range = (int)min(ra.b_bytes, 0x7fffffffLL);
     const int a_range = (M - 1) * LDA + p.kbytes;
-    const int sa_range = (M - 1) * SFA_SM + nk * KT_SC, sb_range = (N - 1) * SFB_SN + nk * KT_SC;
+    // W16: SFA_SM / SFB_SN are the bytes of one 32-row block, K-tile step 256
+    const int rows32a = (M + 31) / 32, rows32b = (N + 31) / 32;
+    const int sa_range = W16 ? (rows32a - 1) * SFA_SM + nk * 256 : (M - 1) * SFA_SM + nk * KT_SC;
+    const int sb_range = (N - 1) * SFB_SN + nk * KT_SC;
     const i32x4 z = {0, 0, 0, 0};
 
     // ---- A's slice and the scale bytes -> registers (issued first) ----
@@ -121,11 +138,22 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
         av[j] = __builtin_bit_cast(
             i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, min(row, M - 1) * LDA + pc * 1024 + L * 16, 0, 0));
     }
-    const auto rSA = rsrc(SFA, sa_range, kt_begin * KT_SC, true);
-    const auto rSB = rsrc(SFB + (long long)n0 * SFB_SN, sb_range - n0 * SFB_SN, kt_begin * KT_SC, true);
-    i32x4 sv[S_PER_WAVE];
+    i32x4 sv[W16 ? SW_PER_WAVE : S_PER_WAVE];
+    if constexpr (W16) {
+        // A's e8m0_shuffle bytes of the slice: KPS * 256 contiguous bytes per
+        // 32-row block; blocks past the last read zeros
+        const auto rSA = rsrc(SFA, sa_range, kt_begin * 256, true);
 #pragma unroll
-    for (int j = 0; j < S_PER_WAVE; ++j) {
+        for (int j = 0; j < SW_PER_WAVE; ++j) {
+            const int pc = (w + j * kSliceWaves) * 64 + L, blk = pc / (KPS * 16), within = pc % (KPS * 16);
+            sv[j] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rSA, pc < SW_PIECES ? blk * SFA_SM + within * 16 : 0, 0, 0));
+        }
+    }
+    const auto rSA = rsrc(SFA, sa_range, kt_begin * KT_SC, !W16);
+    const auto rSB = rsrc(SFB + (long long)n0 * SFB_SN, sb_range - n0 * SFB_SN, kt_begin * KT_SC, !W16);
+#pragma unroll
+    for (int j = 0; j < (W16 ? 0 : S_PER_WAVE); ++j) {
         const int ins = w + j * kSliceWaves, pc = ins * 64 + L;    // instruction, piece
         const bool is_a = ins * 64 < RA * SPR;                      // wave-uniform
         const int pr = is_a ? pc : pc - RA * SPR, row = pr / SPR, piece = pr % SPR;
@@ -139,15 +167,24 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
 
     // ---- the wave's B: 16 rows, K-tiles [kt_w, kt_w + KW) ----
     const int kt_w = kt_begin + kq * KW;
-    const auto rB = rsrc(B, b_range, kt_w * BKB, true);
+    // W16: the wave's 16-row block blk16 (its K-tile kt at blk16 * 16 * LDB +
+    // kt * 2048; a block past N reads zeros) and its scale dwords (32-row
+    // block blk16 / 2, half blk16 % 2)
+    const int blk16 = n0 / 16 + bw;
+    const auto rB = W16 ? rsrc(B, b_range, blk16 * 16 * LDB + kt_w * 2048, true) : rsrc(B, b_range, kt_w * BKB, true);
     const auto rZ = rsrc(B, 0, 0, false);
-    const int b_off = min(n0 + 16 * bw + l16, N - 1) * LDB + q * 16;
+    const auto rSW = rsrc(SFB + (long long)(blk16 >> 1) * SFB_SN, nk * 256, kt_w * 256, W16 && (blk16 >> 1) < rows32b);
+    const int b_off = W16 ? L * 16 : min(n0 + 16 * bw + l16, N - 1) * LDB + q * 16;
+    constexpr int B_KT = W16 ? 2048 : BKB, B_HI = W16 ? 1024 : 64;
     i32x4 bq[D][2];
+    int bsw[D];
     auto issue = [&](auto dd, int j) __attribute__((always_inline)) {
         constexpr int d = decltype(dd)::value;
         const auto r = kt_w + j < kt_end ? rB : rZ;
-        bq[d][0] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + j * BKB, 0, 0));
-        bq[d][1] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + j * BKB + 64, 0, 0));
+        bq[d][0] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + j * B_KT, 0, 0));
+        bq[d][1] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + j * B_KT + B_HI, 0, 0));
+        if constexpr (W16)
+            bsw[d] = (int)__builtin_amdgcn_raw_buffer_load_b32(kt_w + j < kt_end ? rSW : rZ, j * 256 + L * 4, 0, 0);
     };
     runs::static_for<D>([&](auto dd) __attribute__((always_inline)) { issue(dd, decltype(dd)::value); });
     __builtin_amdgcn_sched_barrier(0);
@@ -159,9 +196,18 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
         const int c = pc * 64 + L;
         *(QG_LDS i32x4*)(lds + row * A_ROW + ((c ^ (row & 15)) << 4)) = kt_begin + (c >> 3) < kt_end ? av[j] : z;
     }
+    // W16: A's scale bytes as they lie, K-tiles past the slice as zeros
+    if constexpr (W16) {
+#pragma unroll
+        for (int j = 0; j < SW_PER_WAVE; ++j) {
+            const int pc = (w + j * kSliceWaves) * 64 + L;
+            if (pc < SW_PIECES)
+                *(QG_LDS i32x4*)(lds + OFF_SA + pc * 16) = kt_begin + (pc % (KPS * 16)) / 16 < kt_end ? sv[j] : z;
+        }
+    }
     // scale pieces into [K-tile][row]
 #pragma unroll
-    for (int j = 0; j < S_PER_WAVE; ++j) {
+    for (int j = 0; j < (W16 ? 0 : S_PER_WAVE); ++j) {
         const int ins = w + j * kSliceWaves, pc = ins * 64 + L;
         if (pc < S_PIECES) {
             const bool is_a = ins * 64 < RA * SPR;
@@ -192,7 +238,12 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
         const i32x4 b_lo = bq[j % D][0], b_hi = bq[j % D][1];
         const QG_LDS uint8_t* sbp = lds + OFF_SB + kt * SB_KT + (16 * bw + l16) * KT_SC;
         int sb0, sb1 = 0;
-        if constexpr (FP4) {
+        if constexpr (W16) {
+            // bytes hB (groups 0-3) and 2 + hB (groups 4-7) of the dword, hB = blk16 % 2
+            const int x = bsw[j % D] >> (8 * (blk16 & 1));
+            sb0 = x;
+            sb1 = x >> 16;
+        } else if constexpr (FP4) {
             const u32x2 x = *(const QG_LDS u32x2*)sbp;
             sb0 = (int)(x[0] >> (8 * q));
             sb1 = (int)(x[1] >> (8 * q));
@@ -205,10 +256,20 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
             const QG_LDS uint8_t* arow = lds + (16 * i + l16) * A_ROW;
             const i32x4 a_lo = *(const QG_LDS i32x4*)(arow + alo);
             const i32x4 a_hi = *(const QG_LDS i32x4*)(arow + ahi);
-            const QG_LDS uint8_t* sap = lds + OFF_SA + kt * SA_KT + (16 * i + l16) * KT_SC;
+            const QG_LDS uint8_t* sap = W16 ? lds + OFF_SA + ((i >> 1) * KPS + kt) * 256 + L * 4
+                                            : lds + OFF_SA + kt * SA_KT + (16 * i + l16) * KT_SC;
             if constexpr (FP4) {
-                const u32x2 x = *(const QG_LDS u32x2*)sap;
-                const int sa0 = (int)(x[0] >> (8 * q)), sa1 = (int)(x[1] >> (8 * q));
+                int sa0, sa1;
+                if constexpr (W16) {
+                    // rows 16 i + r: half i % 2 of 32-row block i / 2
+                    const int x = (int)(*(const QG_LDS uint32_t*)sap >> (8 * (i & 1)));
+                    sa0 = x;
+                    sa1 = x >> 16;
+                } else {
+                    const u32x2 x = *(const QG_LDS u32x2*)sap;
+                    sa0 = (int)(x[0] >> (8 * q));
+                    sa1 = (int)(x[1] >> (8 * q));
+                }
                 const i32x8 b0 = i32x8{b_lo[0], b_lo[1], b_lo[2], b_lo[3], 0, 0, 0, 0};
                 const i32x8 b1 = i32x8{b_hi[0], b_hi[1], b_hi[2], b_hi[3], 0, 0, 0, 0};
                 const i32x8 a0 = i32x8{a_lo[0], a_lo[1], a_lo[2], a_lo[3], 0, 0, 0, 0};

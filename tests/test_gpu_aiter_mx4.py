@@ -48,7 +48,8 @@ def test_gemm_a4w4_bpreshuffle(qgemm, gpu, m, n, k, dtype, kernel_id):
     if kernel_id == 1:
         assert trace == f"wide_gemm<fp4,MXS,W16,{f},pb{pb}>", trace
     elif m <= 64:
-        assert trace.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,")), trace
+        assert trace.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,", "slice_gemm<fp4,MXS,W16,")), \
+            trace
     else:    # (split over K into fp32 planes where the tiles leave most CUs idle)
         assert trace == f"quad_gemm<fp4,MXS,W16,{f}>" or \
             trace.startswith(f"quad_gemm<fp4,MXS,W16,fp32>+splitk_reduce<{f},"), trace
@@ -80,10 +81,12 @@ def test_gemm_a4w4_decode_burst(qgemm, gpu, m, n, k, dtype):
     y2 = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=5, workspace=junk)
     torch.cuda.synchronize()
     assert torch.equal(y, y2), f"two calls differ ({trace})"
-    # the library's choice: the burst kernel where its plan gate accepts the shape
+    # the library's choice: the slice kernel where its plan fills the CUs in
+    # one round, else the burst kernel where its plan gate accepts the shape
     y0 = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype)
     trace0 = qgemm.last_launch()
-    assert trace0.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,")), trace0
+    assert trace0.startswith(("burst_gemm<fp4,MXS,FRAG,", "quad_gemm<fp4,MXS,W16,", "slice_gemm<fp4,MXS,W16,")), \
+        trace0
     assert_close(ref, out_to_f32(y0), f"a4w4 decode auto {m}x{n}x{k} ({trace0})")
     # no workspace: an unsplit plan, or refused when K needs a split
     try:
@@ -207,3 +210,62 @@ def test_gemm_a4w4_middle_m_split(qgemm, gpu, m, n, k, dtype):
     t0 = qgemm.last_launch()
     assert t0.startswith("quad_gemm<fp4,MXS,W16,") and "splitk" not in t0, t0
     assert_close(ref, out_to_f32(y0), f"a4w4 middle unsplit {m}x{n}x{k} ({t0})")
+
+
+# the slice kernel on aiter's operands (W16 B: each fragment load one 1 KB
+# run; e8m0_shuffle scales: A's slice of them in LDS as they lie, B's dword
+# per K-tile with its fragments): row counts across its 16 / 32 / 64-row
+# plans and 32-row scale-block halves, N % 32 == 16 (a 16-row block whose
+# 32-row scale block is half used), K slices past the end, K split over
+# workgroups with a workspace of garbage, and configs[4]'s shapes
+SLICE = [(9, 4096, 4096), (16, 7168, 16384), (17, 2064, 8192), (32, 7168, 16384), (33, 1040, 4096),
+         (48, 4096, 6144), (64, 7168, 16384), (64, 3088, 2304), (12, 700 - 700 % 16, 14336)]
+
+
+_SLICE_REF = {}
+
+
+@pytest.mark.parametrize("m,n,k", SLICE)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gemm_a4w4_slice(qgemm, gpu, m, n, k, dtype):
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=11 * m + n + k)
+    A, B, SA, SB = _aiter_operands(qa, qb, ea, eb, gpu)
+    if (m, n, k) not in _SLICE_REF:    # the oracle once per shape (both output types)
+        _SLICE_REF[(m, n, k)] = O.gemm_mx4(qa, qb, ea, eb)
+    ref = _SLICE_REF[(m, n, k)]
+    args = qgemm.Mxfp4Kargs(A.data_ptr(), B.data_ptr(), 0, m, n, k, 1, k // 2, k // 2, n, 0, 0, 0, SA.data_ptr(),
+                            SB.data_ptr(), k, k, 0, 0, 0)
+    need = qgemm.lib().gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(ctypes.byref(args), 10)
+    junk = torch.full((max(need, 256),), 0xFF, dtype=torch.uint8, device=gpu)
+    y = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=10, workspace=junk)
+    trace = qgemm.last_launch()
+    assert trace.startswith("slice_gemm<fp4,MXS,W16,"), trace
+    assert (need > 0) == (not trace.endswith(",splitk1>")), (need, trace)
+    assert_close(ref, out_to_f32(y), f"a4w4 slice {m}x{n}x{k} ({trace})")
+    y2 = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=10, workspace=junk)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), f"two calls differ ({trace})"
+    if need:    # the plan's counter words (one per 16 * nbw-column tile) re-armed to zero
+        nbw = 2 if m <= 16 else (4 if m <= 32 else 8)
+        tiles = -(-n // (16 * nbw))
+        assert int(junk[:4 * tiles].to(torch.int32).sum()) == 0, "split-K counters not re-armed"
+    # no workspace: refused when K needs a split
+    try:
+        yn = qgemm.gemm_a4w4(A, B, SA, SB, dtype=dtype, kernel_id=10, workspace=False)
+    except RuntimeError as e:
+        assert "HIP error 1" in str(e) and need > 0, (trace, str(e))
+    else:
+        assert need == 0 and torch.equal(yn, y), trace
+
+
+def test_gemm_a4w4_slice_matches_row_major(qgemm, gpu):
+    """configs[4] M = 64 on both MXFP4 entries' slice kernels: the same bits
+    (same products, same order of sums)."""
+    m, n, k = 64, 7168, 16384
+    qa, qb, ea, eb = make_mx4(m, n, k, seed=99)
+    A, B, SA, SB = _aiter_operands(qa, qb, ea, eb, gpu)
+    ya = qgemm.gemm_a4w4(A, B, SA, SB, kernel_id=10)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+    yr = qgemm.gemm_a4w4_mxfp4(dev(qa), dev(qb), dev(ea), dev(eb))
+    assert qgemm.last_launch().startswith("slice_gemm<fp4,MX,RAW,mb4"), qgemm.last_launch()
+    assert torch.equal(ya, yr)
