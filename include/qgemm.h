@@ -188,7 +188,8 @@ hipError_t gemm_a8w8_blockscale_ldsbypass_repack(const opus_gemm_ldsbypass_kargs
                                 32 columns per workgroup; 16-byte aligned A / B rows and scale rows */
 #define QGEMM_KID_SLICE  10  /* MX only: slice decode kernel (M <= 64): A's K slice in LDS, B fragments
                                 straight from memory, 32 / 64 / 128 columns per workgroup for M <= 16 /
-                                32 / 64; 16-byte aligned A / B rows and scale rows */
+                                32 / 64; row-major entries: 16-byte aligned A / B rows and scale rows;
+                                also the aiter-format MXFP4 entry (W16 B, e8m0_shuffle scales) */
 hipError_t gemm_a8w8_blockscale_bpreshuffle_kid(const opus_gemm_kargs* args, int out_dtype, int kernel_id,
                                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t gemm_a8w8_blockscale_bpreshuffle_kid_workspace_bytes(const opus_gemm_kargs* args, int kernel_id);
@@ -276,16 +277,19 @@ typedef struct opus_gemm_mxfp4_scale_kargs {
  * shapes run faster through gemm_a4w4_mxfp4 with row-major operands). */
 hipError_t gemm_a4w4_mxfp4_bpreshuffle(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, hipStream_t stream);
 /* The same with a kernel id and an optional workspace: QGEMM_KID_AUTO (the
- * library's choice: M <= 64 on the burst kernel where its plan takes the
- * shape -- B's 16-row blocks are the 16x16x128 MFMA's operand order,
- * streamed as whole 1 KB loads -- with a K split only when the workspace is
- * given; otherwise the one-by-four wave kernel, or the two-by-two wave
- * kernel for grid_blocks > 0), QGEMM_KID_TILE256 (the two-by-two wave 256x256
- * tile kernel, the only one that takes grid_blocks > 0), QGEMM_KID_QUAD (one-by-
- * four waves, B straight from memory into registers) or QGEMM_KID_BURST
- * (M <= 64); other ids, and shapes a forced id cannot take, are rejected.
- * The workspace (size from the query below, 256-byte aligned, any
- * contents) carries a burst plan's split-K counters and fp32 partials; the
+ * library's choice: M = 9-64 on the slice kernel where its plan is one round
+ * of 7/10 to all of the CUs with full K slices, else M <= 64 on the burst
+ * kernel where its plan takes the shape -- B's 16-row blocks are the
+ * 16x16x128 MFMA's operand order, streamed as whole 1 KB loads -- with a K
+ * split only when the workspace is given; otherwise the one-by-four wave
+ * kernel, or the two-by-two wave kernel for grid_blocks > 0),
+ * QGEMM_KID_TILE256 (the two-by-two wave 256x256 tile kernel, the only one
+ * that takes grid_blocks > 0), QGEMM_KID_QUAD (one-by-four waves, B straight
+ * from memory into registers), QGEMM_KID_BURST (M <= 64) or QGEMM_KID_SLICE
+ * (M <= 64: A's K slice in LDS, B's W16 fragments straight into registers);
+ * other ids, and shapes a forced id cannot take, are rejected.  The
+ * workspace (size from the query below, 256-byte aligned, any contents)
+ * carries a burst or slice plan's split-K counters and fp32 partials; the
  * plain entry above runs without one. */
 hipError_t gemm_a4w4_mxfp4_bpreshuffle_kid(const opus_gemm_mxfp4_scale_kargs* args, int out_dtype, int kernel_id,
                                            void* workspace, size_t workspace_bytes, hipStream_t stream);
