@@ -178,13 +178,24 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     constexpr int B_KT = W16 ? 2048 : BKB, B_HI = W16 ? 1024 : 64;
     i32x4 bq[D][2];
     int bsw[D];
+    // step j of the wave's walk takes K-tile jr(j) of its part.  Without the
+    // rotation every wave of the grid reads the same 2 KB offset of a 32 KB
+    // K window at the same step, and with W16's contiguous 2 KB K-tiles those
+    // reads crowd into few HBM channels: rotating by wave, K part and tile
+    // (weights replayed from HBM, one box: W16 configs[4] M = 16 / 32 / 48 /
+    // 64 14.0 / 19.2 / 24.2 / 26.3 -> 13.8 / 18.2 / 20.3 / 22.0 us; row-major
+    // 64-row plans 2.8-3.2% faster, its 16-row plans 2% slower, so those keep
+    // the plain walk)
+    const int rot = W16 || MB == 4 ? (5 * bw + 3 * kq + 7 * nt) & (KW - 1) : 0;
+    auto jr = [&](int j) __attribute__((always_inline)) { return (j + rot) & (KW - 1); };
     auto issue = [&](auto dd, int j) __attribute__((always_inline)) {
         constexpr int d = decltype(dd)::value;
-        const auto r = kt_w + j < kt_end ? rB : rZ;
-        bq[d][0] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + j * B_KT, 0, 0));
-        bq[d][1] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + j * B_KT + B_HI, 0, 0));
+        const int jj = jr(j);
+        const auto r = kt_w + jj < kt_end ? rB : rZ;
+        bq[d][0] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + jj * B_KT, 0, 0));
+        bq[d][1] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + jj * B_KT + B_HI, 0, 0));
         if constexpr (W16)
-            bsw[d] = (int)__builtin_amdgcn_raw_buffer_load_b32(kt_w + j < kt_end ? rSW : rZ, j * 256 + L * 4, 0, 0);
+            bsw[d] = (int)__builtin_amdgcn_raw_buffer_load_b32(kt_w + jj < kt_end ? rSW : rZ, jj * 256 + L * 4, 0, 0);
     };
     runs::static_for<D>([&](auto dd) __attribute__((always_inline)) { issue(dd, decltype(dd)::value); });
     __builtin_amdgcn_sched_barrier(0);
@@ -234,7 +245,7 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     for (int i = 0; i < MB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     runs::static_for<KW>([&](auto jj) __attribute__((always_inline)) {
         constexpr int j = decltype(jj)::value;
-        const int kt = kq * KW + j;
+        const int kt = kq * KW + jr(j);
         const i32x4 b_lo = bq[j % D][0], b_hi = bq[j % D][1];
         const QG_LDS uint8_t* sbp = lds + OFF_SB + kt * SB_KT + (16 * bw + l16) * KT_SC;
         int sb0, sb1 = 0;
