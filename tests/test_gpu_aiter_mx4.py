@@ -269,3 +269,39 @@ def test_gemm_a4w4_slice_matches_row_major(qgemm, gpu):
     yr = qgemm.gemm_a4w4_mxfp4(dev(qa), dev(qb), dev(ea), dev(eb))
     assert qgemm.last_launch().startswith("slice_gemm<fp4,MX,RAW,mb4"), qgemm.last_launch()
     assert torch.equal(ya, yr)
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 2064, 4096), (48, 1024, 6144)])
+def test_gemm_a4w4_slice_batched_c_abi(qgemm, gpu, m, n, k):
+    """Batch 2 on the slice kernel (kernel id 10) through the C ABI, padded
+    A-scale batch strides; (48, 1024, 6144) splits K in two (a workspace of
+    garbage), (32, 2064, 4096) runs unsplit with a half-used last scale
+    block."""
+    batch = 2
+    data = [make_mx4(m, n, k, seed=70 + i + m) for i in range(batch)]
+    kb, kg = k // 2, k // 32
+    A = torch.stack([torch.from_numpy(d[0]) for d in data]).to(gpu)
+    B = torch.stack([torch.from_numpy(O.shuffle_weight_16x16(d[1])) for d in data]).to(gpu)
+    sa_rows, sb_rows = (m + 31) // 32 * 32 + 32, (n + 31) // 32 * 32
+    SA = torch.full((batch, sa_rows * kg), 0x7F, dtype=torch.uint8)
+    SB = torch.empty((batch, sb_rows * kg), dtype=torch.uint8)
+    for i, d in enumerate(data):
+        sa = O.e8m0_shuffle(d[2]).reshape(-1)
+        SA[i, :sa.size] = torch.from_numpy(sa)
+        SB[i] = torch.from_numpy(O.e8m0_shuffle(d[3]).reshape(-1))
+    SA, SB = SA.to(gpu), SB.to(gpu)
+    L = qgemm.lib()
+    C = torch.full((batch, m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+    args = qgemm.Mxfp4Kargs(A.data_ptr(), B.data_ptr(), C.data_ptr(), m, n, k, batch, kb, kb, n, m * kb, n * kb,
+                            m * n, SA.data_ptr(), SB.data_ptr(), 32 * kg, 32 * kg, sa_rows * kg, sb_rows * kg, 0)
+    need = L.gemm_a4w4_mxfp4_bpreshuffle_kid_workspace_bytes(ctypes.byref(args), 10)
+    junk = torch.full((max(need, 256),), 0xA5, dtype=torch.uint8, device=gpu)
+    st = L.gemm_a4w4_mxfp4_bpreshuffle_kid(ctypes.byref(args), 1, 10, ctypes.c_void_p(junk.data_ptr()), junk.numel(),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0
+    torch.cuda.synchronize()
+    trace = qgemm.last_launch()
+    assert trace.startswith("slice_gemm<fp4,MXS,W16,"), trace
+    assert (need > 0) == (not trace.endswith(",splitk1>")), (need, trace)
+    for i, d in enumerate(data):
+        assert_close(O.gemm_mx4(*d), C[i].float().cpu().numpy(), f"slice batch {i} {m}x{n}x{k} ({trace})")
