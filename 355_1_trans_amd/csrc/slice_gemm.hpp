@@ -22,8 +22,9 @@
 //    (w % KQ) of the slice: each K-tile's two fragment loads (bytes 0-63 and
 //    64-127 of 16 rows) go straight into registers, D K-tiles ahead, and meet
 //    A's fragments read from LDS -- B never passes through LDS and no wave
-//    waits for another inside the K loop; B loads with the default cache
-//    policy (the non-temporal one ran configs[4] M = 1-64 10-15% slower);
+//    waits for another inside the K loop; row-major B loads with the default
+//    cache policy (the non-temporal one ran configs[4] M = 1-64 10-15%
+//    slower), W16 B non-temporal;
 //  * the KQ waves of a block add their tiles in K order through LDS; a K
 //    split over workgroups uses the epoch-tagged counters and device-coherent
 //    partials of common.hpp, the last workgroup of a tile summing the slices
@@ -176,6 +177,10 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
     const auto rSW = rsrc(SFB + (long long)(blk16 >> 1) * SFB_SN, nk * 256, kt_w * 256, W16 && (blk16 >> 1) < rows32b);
     const int b_off = W16 ? L * 16 : min(n0 + 16 * bw + l16, N - 1) * LDB + q * 16;
     constexpr int B_KT = W16 ? 2048 : BKB, B_HI = W16 ? 1024 : 64;
+    // cache policy of the B loads: non-temporal for W16 (aiter configs[4]
+    // M = 32 / 64 18.4 / 22.1 -> 16.5 / 20.5 us with the rotated walk), the
+    // default for row-major B (non-temporal 5-8% slower there)
+    constexpr int B_AUX = W16 ? 2 : 0;
     i32x4 bq[D][2];
     int bsw[D];
     // step j of the wave's walk takes K-tile jr(j) of its part.  Without the
@@ -192,8 +197,8 @@ __global__ __launch_bounds__(kSliceWaves * 64, 1) void slice_gemm_kernel(const R
         constexpr int d = decltype(dd)::value;
         const int jj = jr(j);
         const auto r = kt_w + jj < kt_end ? rB : rZ;
-        bq[d][0] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + jj * B_KT, 0, 0));
-        bq[d][1] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + jj * B_KT + B_HI, 0, 0));
+        bq[d][0] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + jj * B_KT, 0, B_AUX));
+        bq[d][1] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_off + jj * B_KT + B_HI, 0, B_AUX));
         if constexpr (W16)
             bsw[d] = (int)__builtin_amdgcn_raw_buffer_load_b32(kt_w + jj < kt_end ? rSW : rZ, jj * 256 + L * 4, 0, 0);
     };
