@@ -77,7 +77,8 @@ LAYOUT_CODE = {"bs8nn": 1, "bs8tt": 2, "bs8tn": 3}   # QGEMM_LAYOUT_*
 
 # the other BASELINE configs the default run measures after the headline:
 # (workload, M override)
-EXTRA_WORKLOADS = (("mxfp4_8192", None), ("mxfp4_8192_aiter", None), ("bs_c0", None), ("mxfp4_c4", 32))
+EXTRA_WORKLOADS = (("mxfp4_8192", None), ("mxfp4_8192_aiter", None), ("bs_c0", None), ("mxfp4_c4", 32),
+                   ("mxfp4_c4_aiter", 32))
 
 NAMES = {"mx8": "MXFP8 TN GEMM, e4m3 x e4m3, E8M0 per 32 K",
          "mx4": "MXFP4 A4W4 GEMM, e2m1 x e2m1, E8M0 per 32 K",
@@ -108,7 +109,7 @@ def parse():
     p.add_argument("--no-check", action="store_true", help="skip the output check against the oracle")
     p.add_argument("--no-extra", action="store_true",
                    help="default run only: skip the extra records (configs[3] row-major and in aiter's "
-                        "formats, configs[0], configs[4] M = 32)")
+                        "formats, configs[0], configs[4] M = 32 row-major and in aiter's formats)")
     p.add_argument("--sfa-km", action="store_true",
                    help="block-scale fp32 workloads: pass A's scales column-major [K/128][M] (the reference's "
                         "layout) instead of BASELINE's row-major [M][K/128]")
